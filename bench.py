@@ -1,0 +1,179 @@
+"""Benchmark of the MI355X decode hot path (BASELINE.json metric).
+
+Workload ("config 2"): the full Qwen2.5-0.5B-shaped q4 model
+(24 layers, vocabulary 151936, affine group-64 4-bit weights) generated from seed 2; a
+256-position prefix K/V cache prefilled from random prompt tokens; then `--steps` greedy
+1-row decode steps, each one persistent-kernel launch, all recorded in one hipGraph.
+Inputs are resident in HBM before timing starts. Also timed: the 16-row tree-verify pass
+of config 3 (seed 3, prefix 512).
+
+A step is one pass of the hot path over one token. value = tokens/s of the timed steps;
+the line also carries us_per_token, the roofline of the dominant kernel (the pass kernel
+is the whole step) and the CPU baseline (numpy fp32 oracle on the same dequantized
+weights, rank 0 only, bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"] if (ROOT / "BASELINE.json").exists() else \
+    "q4 decode us/token (1 row) + achieved HBM GB/s vs peak; 16-row verify us"
+HBM_PEAK_GBS = 8000.0
+Q4_MATRIX_BYTES = 277_853_184     # q4 codes + scales of every matrix incl. the tied lm_head
+F32_NORM_BIAS_BYTES = 286_208     # f32 norms + QKV biases as stored in .ill v1
+EMBED_ROW_BYTES = 504             # one q4 embedding row (448 B codes + 56 B scales)
+KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
+
+
+def step_bytes(L: float) -> float:
+    """Algorithmic HBM bytes of one 1-row q4 step attending to L positions."""
+    return Q4_MATRIX_BYTES + F32_NORM_BIAS_BYTES + EMBED_ROW_BYTES + KV_BYTES_PER_POS * L + KV_BYTES_PER_POS
+
+
+def model_path(fmt: int, seed: int) -> str:
+    from instantllm_amd import synth
+    d = Path(os.environ.get("ILL_MODEL_DIR", "/tmp/ill_models"))
+    d.mkdir(parents=True, exist_ok=True)
+    p = d / f"qwen05b_fmt{fmt}_seed{seed}.ill"
+    if not p.exists():
+        synth.build_model(str(p), fmt, seed)
+    return str(p)
+
+
+def cpu_baseline(path: str, prompt: list[int], n_decode: int) -> dict:
+    """numpy fp32 oracle on the dequantized model: prefill + `n_decode` decode steps."""
+    from oracle import illread, qwen
+    m = qwen.Model(illread.load(path))
+    cache = m.new_cache(len(prompt) + n_decode + 1)
+    t0 = time.perf_counter()
+    lg = m.forward(prompt, cache)
+    t1 = time.perf_counter()
+    times = []
+    tok = int(np.argmax(lg))
+    for _ in range(n_decode):
+        s = time.perf_counter()
+        lg = m.forward([tok], cache)
+        times.append(time.perf_counter() - s)
+        tok = int(np.argmax(lg))
+    med = float(np.median(times))
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    return {
+        "value": round(1.0 / med, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+        "sample": f"numpy fp32 oracle (oracle/qwen.py) on the dequantized q4 model: {len(prompt)}-token "
+                  f"prefill {t1 - t0:.2f} s, then {n_decode} decode steps, median {med * 1e3:.1f} ms "
+                  f"(min {min(times) * 1e3:.1f} ms)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prefix", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the decode step does not shard; "
+              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+    from instantllm_amd import illfile as F
+    from instantllm_amd.engine import Engine
+    from oracle.tree import random_tree
+
+    path = model_path(F.FMT_Q4, 2)
+    rng = np.random.default_rng(2)
+    prompt = [int(t) for t in rng.integers(0, F.VOCAB, size=args.prefix)]
+    K, W = args.steps, args.warmup
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=max(4096, K + W + 16))
+    no_eos = (-5, -5)   # the reference's idsbench disables the stop ids (main.swift:165)
+
+    def run(nsteps: int) -> tuple[float, float, float]:
+        e.reset_out_tokens()
+        e.set_state(pos=0, n=len(prompt), maxsteps=nsteps + 1, eos=no_eos)
+        e.prefill(prompt)
+        e.sync()
+        e.capture_steps(nsteps)
+        e.sync()
+        t0 = time.perf_counter()
+        ms_dev = e.time_graph(1)   # HIP events around the graph launch on the engine stream
+        t1 = time.perf_counter()
+        return (t1 - t0) * 1e3, ms_dev, e.get_state()["pos"]
+
+    if W > 0:
+        run(W)
+    wall_ms, dev_ms, pos_end = run(K)
+    if pos_end != len(prompt) + K:
+        raise RuntimeError(f"decode did not advance: pos {pos_end}")
+    toks = e.out_tokens()[: K + 1].tolist()
+    us_tok = dev_ms * 1e3 / K
+    L_avg = len(prompt) + (K + 1) / 2.0
+    achieved = step_bytes(L_avg) / (us_tok * 1e-6) / 1e9
+
+    # 16-row tree-verify pass (config 3): prefix 512, 15 drafts + root
+    vr = np.random.default_rng(3)
+    vprompt = [int(t) for t in vr.integers(0, F.VOCAB, size=512)]
+    e.set_state(pos=0, n=512, maxsteps=64, eos=no_eos)
+    e.prefill(vprompt)
+    st = e.get_state()
+    tree = random_tree(vr, 16, F.VOCAB)
+    tree[33] = int(e.out_tokens()[0])
+    verify_us = []
+    for _ in range(5):
+        e.set_state(pos=st["pos"], n=16, maxsteps=64, eos=no_eos)
+        e.verify_pass(16, tree=tree)
+        verify_us.append(e.last_pass_ms() * 1e3)
+    e.set_state(pos=st["pos"], n=1, maxsteps=64, eos=no_eos)
+    one_us = []
+    for _ in range(5):
+        e.set_state(pos=st["pos"], n=1, maxsteps=64, eos=no_eos)
+        e.decode_step()
+        one_us.append(e.last_pass_ms() * 1e3)
+    e.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(K / (dev_ms * 1e-3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(dev_ms / K, 5),
+        "us_per_token": round(us_tok, 2),
+        "wall_ms_per_step": round(wall_ms / K, 5),
+        "verify16_us": round(float(np.median(verify_us)), 2),
+        "decode1_single_launch_us": round(float(np.median(one_us)), 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 weights, int8 MFMA (exact int32) + fp32 epilogues",
+        "data": "synthetic (seeded random weights and token ids)",
+        "config": {"workload": "config 2: q4 1-row greedy decode, Qwen2.5-0.5B shape (24L, d896, 14/2 heads, "
+                               "FFN 4864, vocab 151936), prefix KV 256, each step one persistent kernel in a hipGraph",
+                   "prefix": len(prompt), "model_seed": 2, "first_tokens": toks[:8]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": f"bytes(L)={step_bytes(L_avg):.0f} at mean L={L_avg:.1f}; dominant kernel "
+                             "ill_pass_kernel<1> (the whole step), duration from HIP events over the timed graph"},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(path, prompt[:48], args.cpu_steps)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,115 @@
+/* C ABI of the MI355X decode engine (libillhip.so).
+ *
+ * Drop-in for the pass API of the reference's Swift `Engine`
+ * (Sources/Engine/Engine.swift); the reference's only C ABI is the one-function shim
+ * Sources/CShim/include/cshim.h:3-4, which this header extends in the same style: plain
+ * C types, an opaque handle, no GPU types in the signatures.
+ *
+ * Conventions: every function returns 0 on success or a negative error code; the message
+ * of the last error on the calling thread is available from ill_last_error(). The caller
+ * owns host arrays; the engine owns device memory. An engine is single-threaded and runs
+ * on one HIP stream of one GPU.
+ */
+#ifndef ILL_HIP_H
+#define ILL_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ill_engine ill_engine;
+
+enum {
+  ILL_OK = 0,
+  ILL_E_ARG = -1,      /* bad argument (shape, size, state) */
+  ILL_E_FILE = -2,     /* model file missing or malformed */
+  ILL_E_HIP = -3,      /* HIP runtime error */
+  ILL_E_TIMEOUT = -4,  /* a device-side bounded wait expired (the pass was abandoned) */
+  ILL_E_FORMAT = -5    /* weight format not supported by this build */
+};
+
+/* Thread-local message of the last failure (never NULL). */
+const char* ill_last_error(void);
+
+/* Engine(modelPath:maxContext:maxPass:maxSteps:) (Engine.swift:71-232): maps the .ill v1
+ * file (ModelFile.swift:73-98), repacks the weights into the device tile layout and copies
+ * them to HBM once. max_context is rounded up to a multiple of 64. */
+int ill_create(const char* ill_path, int max_context, int max_pass, int max_steps, ill_engine** out);
+int ill_destroy(ill_engine* e);
+
+/* Model facts of the loaded file. */
+int ill_vocab(const ill_engine* e);
+int ill_layers(const ill_engine* e);
+int ill_format(const ill_engine* e);   /* 0 f16, 1 q8, 2 q4 */
+
+/* The 16-int device State (Shaders.swift:37-54): pos, n, step, done, maxctx, maxsteps,
+ * eos0, eos1, nver, tspec, passes, accepted, tlmh, nodraft, learned, tree.
+ * Host writes it before a request (Engine.swift:945-964). */
+int ill_set_state(ill_engine* e, const int32_t state[16]);
+int ill_get_state(ill_engine* e, int32_t state[16]);
+
+/* encodePrefill (Engine.swift:588-601): n tokens at positions state.pos.., lm_head on the
+ * last row and a greedy commit (the first generated token lands in out_tokens[step] and
+ * becomes the next step's input). write_logits keeps that row's fp32 logits. */
+int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits);
+
+/* encodeDecodeStep (Engine.swift:605-609): one 1-row step on the last committed token. */
+int ill_decode_step(ill_engine* e, int write_logits);
+
+/* encodeWidePass / encodeSpecPass + k_commit_spec (Engine.swift:567-579, :503-547;
+ * Shaders.swift:246-418 without drafting): one pass over `rows` (<= 16) rows.
+ * tree != NULL: the 65-int tree [n, depth[16], parent[16], tok[16], anc[16]] with tok[0] =
+ * the last committed token; rows attend to the context and their ancestors, the longest
+ * path whose drafts equal their parent's argmax is committed and its K/V compacted.
+ * tree == NULL: a chain of toks[0..rows-1] = [last token, drafts...]. */
+int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t* toks, int write_logits);
+
+/* Record `nsteps` decode steps into one hipGraph; ill_launch_graph replays it. Steps after
+ * the stop flag early-exit on the device (Shaders.swift:41). */
+int ill_capture_steps(ill_engine* e, int nsteps);
+int ill_launch_graph(ill_engine* e);
+
+int ill_sync(ill_engine* e);
+
+/* Pinned host array [max_steps] of committed tokens (-1 = not yet written): poll it with
+ * volatile loads, as the reference does with ill_volatile_load (cshim.h:4). */
+const int32_t* ill_out_tokens(ill_engine* e);
+int ill_reset_out_tokens(ill_engine* e);
+
+/* fp32 logits of pass row `row` from the last pass that wrote logits ([vocab] floats). */
+int ill_read_logits(ill_engine* e, int row, float* out);
+
+/* Prefix K/V save/load (Engine.swift:788-838) in the reference cache layout:
+ * [layer][kv_head][npos][64] f16 bits, for positions 0..npos-1. */
+int ill_kv_copy_out(ill_engine* e, int npos, uint16_t* k, uint16_t* v);
+int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v);
+
+/* Engine.generate (Engine.swift:922-1038) for one request without drafting: sets the
+ * state, prefills `ntok` tokens, then runs decode steps in captured graphs of `chunk`
+ * steps while polling out_tokens. Writes up to max_new tokens (stop token excluded) to
+ * out and returns their count through n_out; logits_out (optional, [vocab]) receives the
+ * first token's logits. */
+int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk,
+                 int32_t* out, int* n_out, float* logits_out);
+
+/* Timing (Engine.profile / gpuTime, Engine.swift:621-729): GPU milliseconds of `iters`
+ * replays of the captured graph, measured with HIP events on the engine's stream. */
+int ill_time_graph(ill_engine* e, int iters, float* ms);
+
+/* GPU milliseconds of the most recent single pass (prefill chunk, decode step or verify
+ * pass launched through the functions above), from HIP events around its kernel. */
+int ill_last_pass_ms(ill_engine* e, float* ms);
+
+/* Per-workgroup timeline of the pass kernel (the persistent-kernel counterpart of
+ * Engine.profile's per-kernel times): when on, thread 0 of every workgroup stores the
+ * 100 MHz device clock at the start, input-ready and done points of its role in every
+ * layer (slots 3l, 3l+1, 3l+2), of the lm_head (3*30 .. +2) and of the commit (+3 .. +5).
+ * ill_trace_read copies [256][slots] u64 values of the last pass and returns `slots`. */
+int ill_trace_enable(ill_engine* e, int on);
+int ill_trace_read(ill_engine* e, uint64_t* out, int* slots);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,85 @@
+// Shared host/device definitions of the MI355X decode engine.
+//
+// Model shape is fixed like the reference engine (Sources/Engine/Shaders.swift:12-21):
+// hidden 896, FFN 4864, 14 query heads, 2 KV heads, head_dim 64, QKV rows 1152. The layer
+// count and vocabulary come from the .ill file (24 / 151936 for the real model).
+#pragma once
+#include <stdint.h>
+
+#define ILL_H 896
+#define ILL_FF 4864
+#define ILL_NH 14
+#define ILL_NKV 2
+#define ILL_HD 64
+#define ILL_QKV 1152
+#define ILL_EPS 1e-6f
+#define ILL_MAXT 16          // rows per pass (1-row decode .. 16-row tree verify)
+#define ILL_MAXLAYERS 30
+
+// Device layout unit sizes (q4): a "block" is 16 rows x 128 columns = 2 quant groups.
+#define ILL_KST 7            // 896 / 128 column blocks per K = 896 row tile
+#define ILL_NGU 76           // 4864 / 64 hidden-unit blocks of the fused gate/up/down role
+#define ILL_NOT 56           // 896 / 16 row tiles of O and down
+#define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV
+
+// Persistent-kernel geometry.
+#define ILL_WG 256           // workgroups (one per CU on MI355X)
+#define ILL_WG_THREADS 512   // 8 waves
+#define ILL_WAVES 8
+
+// Role bases: WG index ranges per layer role (WG i runs on XCD i % 8, so every range is
+// spread over all eight XCDs).
+#define ILL_R_QKV 0          // 36 WGs: one 32-row rotary block each
+#define ILL_R_ATT 36         // 28 WGs: (kv group, row) attention items
+#define ILL_N_ATT 28
+#define ILL_R_O 64           // 56 WGs: one 16-row O tile each
+#define ILL_R_GUD 120        // 76 WGs: 64 hidden units (gate+up+SiLU+down partial) each
+#define ILL_R_RED 196        // 56 WGs: residual + down-partial reduction for 16 rows each
+
+// State: the reference's 16-int control block (Shaders.swift:37-54), same field order.
+struct IllState {
+  int32_t pos, n, step, done, maxctx, maxsteps, eos0, eos1;
+  int32_t nver, tspec, passes, accepted, tlmh, nodraft, learned, tree;
+};
+
+// Engine-private control block (device memory).
+struct IllCtl {
+  uint32_t epoch;       // pass counter; tags are epoch * 32 + layer + 1
+  int32_t err;          // nonzero: a bounded wait timed out (code = where)
+  int32_t mode;         // pass mode of the kernel in flight
+  int32_t nrows;        // valid rows of the pass
+  int32_t lmh_row0;     // first row whose logits/argmax the pass computes
+  int32_t lmh_rows;     // rows of the lm_head
+  int32_t write_logits;
+  int32_t commit;       // 0: advance pos only (prefill chunk), 1: greedy commit, 2: spec commit
+  int32_t last_tok;     // last committed token (decode input)
+  int32_t pad[7];
+};
+
+enum IllMode { ILL_MODE_DECODE = 0, ILL_MODE_ROWS = 1, ILL_MODE_TREE = 2 };
+
+// Tree buffer layout (Shaders.swift:23-30): [n, depth[16], parent[16], tok[16], anc[16]].
+#define ILL_TR_DEPTH 1
+#define ILL_TR_PARENT 17
+#define ILL_TR_TOK 33
+#define ILL_TR_ANC 49
+#define ILL_TR_INTS 65
+
+// Per-layer device weight pointers (repacked layout).
+struct IllLayerW {
+  const uint8_t* wqkv;   const uint32_t* sqkv;   // 72 row tiles x 7 blocks
+  const uint8_t* wo;     const uint32_t* so;     // 56 row tiles x 7 blocks
+  const uint8_t* wgu;    const uint32_t* sgu;    // 76 unit blocks x 8 tiles x 7 blocks
+  const uint8_t* wd;     const uint32_t* sd;     // 76 groups x 56 row tiles (512 B each)
+  const float* bqkv;     // 1152, stored (rotary block) order
+  const float* ln1;
+  const float* ln2;
+};
+
+struct IllWeights {
+  const uint8_t* wemb; const uint32_t* semb;   // V/16 row tiles x 7 blocks (tied lm_head)
+  const float* fnorm;
+  int32_t vocab;
+  int32_t layers;
+  int32_t fmt;
+};

@@ -1,0 +1,221 @@
+// Device helpers of the MI355X decode engine: tagged words, bounded waits, MFMA tiles.
+//
+// Within one pass kernel, every value that crosses workgroups is a 64-bit word
+// (payload | tag << 32) written and read with agent-scope atomics. Agent-scope atomics are
+// coherent across the eight XCD L2s, so no cache writeback/invalidate fence is needed,
+// and a consumer waits for exactly the words it reads (no grid barrier). The tag is
+// epoch * 32 + layer + 1; the epoch advances once per pass, so a word from an earlier
+// pass or layer never passes the check.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include "ill_common.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+#define ILL_WAIT_TICKS 200000000ull   // 2 s of the 100 MHz constant clock
+
+__device__ __forceinline__ uint64_t aload64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void astore64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t aload32(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void astore32(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void astore32u(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t mkw(float v, uint32_t tag) {
+  return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+__device__ __forceinline__ uint64_t mkwu(uint32_t v, uint32_t tag) { return ((uint64_t)tag << 32) | (uint64_t)v; }
+__device__ __forceinline__ bool wok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float wval(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+__device__ __forceinline__ uint64_t clk() { return wall_clock64(); }
+
+// Records the first timeout code; every wait gives up once any is recorded.
+__device__ __forceinline__ void set_err(IllCtl* ctl, int code) {
+  int32_t zero = 0;
+  __hip_atomic_compare_exchange_strong(&ctl->err, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup-wide bounded wait: `ready()` is evaluated by every thread (it loads the words
+// the thread needs and checks their tags). Returns false (uniformly) on timeout or when
+// another workgroup has already recorded an error.
+template <class F>
+__device__ __forceinline__ bool wg_wait(F&& ready, IllCtl* ctl, int code) {
+  const uint64_t t0 = clk();
+  for (;;) {
+    const bool ok = ready();
+    if (__syncthreads_and(ok)) return true;
+    int bad = 0;
+    if (threadIdx.x == 0) {
+      bad = aload32(&ctl->err) != 0;
+      if (!bad && clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); bad = 1; }
+    }
+    if (__syncthreads_or(bad)) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Wave-wide bounded wait (lanes of one wave only). On failure the caller must still reach
+// the next workgroup barrier and then test `wg_failed`.
+template <class F>
+__device__ __forceinline__ bool wave_wait(F&& ready, IllCtl* ctl, int code) {
+  const uint64_t t0 = clk();
+  for (;;) {
+    const bool ok = ready();
+    if (__all(ok)) return true;
+    if (aload32(&ctl->err) != 0) return false;
+    if (clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); return false; }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+__device__ __forceinline__ bool wg_failed(IllCtl* ctl) {
+  int bad = 0;
+  if (threadIdx.x == 0) bad = aload32(&ctl->err) != 0;
+  return __syncthreads_or(bad);
+}
+
+// ---- wave reductions (xor butterflies: every lane ends with the same, order-fixed value)
+__device__ __forceinline__ float wsum64(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wmax_xor(float v, int lo, int hi) {
+  for (int o = hi; o >= lo; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wsum_xor(float v, int lo, int hi) {
+  for (int o = hi; o >= lo; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int isum_xor(int v, int lo, int hi) {
+  for (int o = hi; o >= lo; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return __half2float(__ushort_as_half((unsigned short)bits16));
+}
+__device__ __forceinline__ uint32_t f2h(float v) { return (uint32_t)__half_as_ushort(__float2half_rn(v)); }
+
+// ---- activation quantization ------------------------------------------------------------
+// A row of activations is coded per 64-column group as 16-bit fixed point
+// v = rint(x / d), d = max|x| / 32639, split into int8 hi = (v + 128) >> 8 and
+// lo = v - 256 hi, so an int8 MFMA over hi and lo gives sum(w*v) exactly.
+// Byte p of a lane's 16-byte operand holds column 16*kg + kPerm[p]: the order in which
+// a 4-bit weight word unpacks (low nibbles of 4 bytes, then high nibbles).
+__device__ __forceinline__ int q4perm(int p) {
+  // 0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15
+  return ((p >> 3) << 3) | ((p & 3) << 1) | ((p >> 2) & 1);
+}
+#define ILL_QMAX 32639.0f
+
+// 16 values (cols 16*kg + i, i = 0..15) of one row -> operand bytes (q4 order), local sums.
+__device__ __forceinline__ void quant16(const float* v, float d, uint32_t hi[4], uint32_t lo[4], int& sumq) {
+  int q[16];
+  sumq = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    q[i] = d > 0.f ? (int)rintf(v[i] / d) : 0;
+    sumq += q[i];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) { hi[r] = 0; lo[r] = 0; }
+#pragma unroll
+  for (int p = 0; p < 16; p++) {
+    const int x = q[q4perm(p)];
+    const int h = (x + 128) >> 8;
+    const int l = x - (h << 8);
+    hi[p >> 2] |= ((uint32_t)(h & 0xff)) << (8 * (p & 3));
+    lo[p >> 2] |= ((uint32_t)(l & 0xff)) << (8 * (p & 3));
+  }
+}
+
+// ---- q4 tile machinery ----------------------------------------------------------------
+// A repacked q4 row tile (16 rows x 896 columns) is 7 blocks of 1 KiB; in block cb, lane
+// l = 16*kg + n holds 16 bytes: row n, columns 128*cb + 16*kg .. +16 (bytes 0-7, group 2cb)
+// and 128*cb + 64 + 16*kg .. +16 (bytes 8-15, group 2cb+1), two columns per byte (even
+// column in the low nibble). Scales: 7 x 128 B; lane n reads (scale, min) f16 pairs of
+// row n for both groups.
+struct Q4Tile {
+  uint4 w[ILL_KST];
+  uint2 s[ILL_KST];
+};
+
+__device__ __forceinline__ void q4_load(Q4Tile& t, const uint8_t* wtile, const uint32_t* stile, int lane) {
+  const int n = lane & 15;
+#pragma unroll
+  for (int cb = 0; cb < ILL_KST; cb++) {
+    t.w[cb] = *(const uint4*)(wtile + cb * 1024 + lane * 16);
+    t.s[cb] = *(const uint2*)(stile + cb * 32 + n * 2);
+  }
+}
+
+__device__ __forceinline__ v4i q4_unpack(uint32_t a, uint32_t b) {
+  v4i r;
+  r[0] = (int)(a & 0x0F0F0F0Fu);
+  r[1] = (int)((a >> 4) & 0x0F0F0F0Fu);
+  r[2] = (int)(b & 0x0F0F0F0Fu);
+  r[3] = (int)((b >> 4) & 0x0F0F0F0Fu);
+  return r;
+}
+
+// Prepared activations of a K = 896 input in LDS (see prep896): A operands per group G,
+// lane-group kg and row m, and per (G, row) the pair (d, X = d * sum(v)).
+struct PrepLds {
+  uint4 ahi[14 * 4 * 16];
+  uint4 alo[14 * 4 * 16];
+  float2 sc[14 * 16];
+};
+
+// Accumulate one 16-row tile over K = 896: acc[j] (rows t = 4*kg + j of the pass, weight
+// row n) += sum_G s*d*S + m*X. The per-value operation sequence is independent of T.
+template <int T>
+__device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, int lane, float acc[4]) {
+  const int kg = lane >> 4, m = lane & 15;
+  constexpr int RPL = T >= 4 ? 4 : T;
+#pragma unroll
+  for (int cb = 0; cb < ILL_KST; cb++) {
+#pragma unroll
+    for (int gi = 0; gi < 2; gi++) {
+      const int G = 2 * cb + gi;
+      const uint4 wv = t.w[cb];
+      const v4i b = gi == 0 ? q4_unpack(wv.x, wv.y) : q4_unpack(wv.z, wv.w);
+      v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
+      if (m < T) {
+        const uint4 h = P.ahi[(G * 4 + kg) * 16 + m];
+        const uint4 l = P.alo[(G * 4 + kg) * 16 + m];
+        ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
+        al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
+      }
+      const v4i z = {0, 0, 0, 0};
+      const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+      const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+      const uint32_t sm = gi == 0 ? t.s[cb].x : t.s[cb].y;
+      const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+#pragma unroll
+      for (int j = 0; j < RPL; j++) {
+        const int row = 4 * kg + j;
+        if (row < T) {
+          const float2 dx = P.sc[G * 16 + row];
+          const int S = (dh[j] << 8) + dl[j];
+          const float t1 = dx.x * (float)S;
+          acc[j] = fmaf(sw, t1, acc[j]);
+          acc[j] = fmaf(mw, dx.y, acc[j]);
+        }
+      }
+    }
+  }
+}

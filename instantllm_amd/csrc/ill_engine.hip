@@ -1,0 +1,701 @@
+// Host engine of the MI355X decode path and the C ABI of include/ill_hip.h.
+//
+// Mirrors the reference's Swift Engine (Sources/Engine/Engine.swift): it maps the .ill
+// file, owns the device buffers and the device State, and encodes passes. Each pass is a
+// single persistent kernel launch (ill_pass.h); decode steps are recorded into hipGraphs
+// so the generate loop never returns to the host between tokens.
+#include <hip/hip_runtime.h>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ill_hip.h"
+#include "ill_pass.h"
+
+namespace {
+
+thread_local std::string g_err = "no error";
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HCK(x)                                                                            \
+  do {                                                                                    \
+    hipError_t e_ = (x);                                                                  \
+    if (e_ != hipSuccess) return fail(ILL_E_HIP, "%s: %s (%s:%d)", #x, hipGetErrorString(e_), __FILE__, __LINE__); \
+  } while (0)
+
+constexpr uint32_t kMagic = 0x314D4C49;   // "ILM1" (ModelFile.swift:62)
+constexpr int kHeader = 16384;
+
+struct Mapped {
+  void* base = nullptr;
+  size_t len = 0;
+  ~Mapped() {
+    if (base) munmap(base, len);
+  }
+};
+
+// ---- repacking of the .ill tensors into the device tile layout ------------------------
+// q4 row tile: block (rt, cb) = 1 KiB; lane l = 16 kg + n stores 8 bytes of row n at
+// columns 128 cb + 16 kg (group 2 cb) then 8 bytes at 128 cb + 64 + 16 kg (group 2 cb + 1).
+void repack_rows(const uint8_t* w, const uint32_t* sb, int K, const std::vector<int>& rows, uint8_t* dw, uint32_t* ds) {
+  const int nb = K / 128, rb = K / 2, sg = K / 64;
+  const int ntile = (int)rows.size() / 16;
+  for (int rt = 0; rt < ntile; rt++)
+    for (int cb = 0; cb < nb; cb++) {
+      uint8_t* blk = dw + ((size_t)rt * nb + cb) * 1024;
+      uint32_t* sblk = ds + ((size_t)rt * nb + cb) * 32;
+      for (int l = 0; l < 64; l++) {
+        const int kg = l >> 4, n = l & 15;
+        const int r = rows[16 * rt + n];
+        memcpy(blk + l * 16, w + (size_t)r * rb + (128 * cb + 16 * kg) / 2, 8);
+        memcpy(blk + l * 16 + 8, w + (size_t)r * rb + (128 * cb + 64 + 16 * kg) / 2, 8);
+      }
+      for (int n = 0; n < 16; n++) {
+        const int r = rows[16 * rt + n];
+        sblk[n * 2 + 0] = sb[(size_t)r * sg + 2 * cb];
+        sblk[n * 2 + 1] = sb[(size_t)r * sg + 2 * cb + 1];
+      }
+    }
+}
+
+// down projection [896][4864]: block (G, rt) = 512 B; lane l = 16 kg + n stores 8 bytes of
+// row 16 rt + n at columns 64 G + 16 kg; scales [G][rt][n].
+void repack_down(const uint8_t* w, const uint32_t* sb, uint8_t* dw, uint32_t* ds) {
+  const int rb = ILL_FF / 2, sg = ILL_FF / 64;
+  for (int G = 0; G < ILL_NGU; G++)
+    for (int rt = 0; rt < ILL_NOT; rt++) {
+      uint8_t* blk = dw + ((size_t)G * ILL_NOT + rt) * 512;
+      for (int l = 0; l < 64; l++) {
+        const int kg = l >> 4, n = l & 15;
+        memcpy(blk + l * 8, w + (size_t)(16 * rt + n) * rb + (64 * G + 16 * kg) / 2, 8);
+      }
+      for (int n = 0; n < 16; n++) ds[((size_t)G * ILL_NOT + rt) * 16 + n] = sb[(size_t)(16 * rt + n) * sg + G];
+    }
+}
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct ill_engine {
+  int fmt = 2, layers = 0, vocab = 0, maxctx = 0, maxpass = 16, maxsteps = 0;
+  hipStream_t stream = nullptr;
+  uint8_t* dweights = nullptr;
+  IllLayerW* dlayers = nullptr;
+  IllWeights W{};
+  std::vector<IllLayerW> hlayers;
+  IllState* st = nullptr;
+  IllCtl* ctl = nullptr;
+  int32_t* ptoks = nullptr;
+  int32_t* tree = nullptr;
+  float2* rope = nullptr;
+  uint16_t* kc = nullptr;
+  uint16_t* vt = nullptr;
+  uint64_t *xa = nullptr, *xb = nullptr, *q = nullptr, *kvn = nullptr, *attn = nullptr, *part = nullptr, *lmp = nullptr;
+  float* logits = nullptr;
+  int32_t* out_dev = nullptr;
+  int32_t* out_host = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  int graph_steps = 0;
+  IllCtl hctl{};
+  IllPassArgs args{};
+  int logits_rows_valid = 0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;   // bracket the last single-pass launch
+};
+
+namespace {
+
+int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, int commit) {
+  IllCtl c{};
+  c.mode = mode;
+  c.nrows = nrows;
+  c.lmh_row0 = lmh0;
+  c.lmh_rows = lmhn;
+  c.write_logits = wlog;
+  c.commit = commit;
+  // epoch / err / last_tok are device-owned: write only the host fields (offset 8..)
+  e->hctl = c;
+  HCK(hipMemcpyAsync((char*)e->ctl + offsetof(IllCtl, mode), (char*)&e->hctl + offsetof(IllCtl, mode),
+                     offsetof(IllCtl, last_tok) - offsetof(IllCtl, mode), hipMemcpyHostToDevice, e->stream));
+  return 0;
+}
+
+int launch(ill_engine* e, int T) {
+  HCK(hipEventRecord(e->ev0, e->stream));
+  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  HCK(hipGetLastError());
+  HCK(hipEventRecord(e->ev1, e->stream));
+  return 0;
+}
+
+int check_err(ill_engine* e) {
+  int32_t err = 0;
+  HCK(hipMemcpyAsync(&err, &e->ctl->err, 4, hipMemcpyDeviceToHost, e->stream));
+  HCK(hipStreamSynchronize(e->stream));
+  if (err) {
+    int32_t zero = 0;
+    hipMemcpy(&e->ctl->err, &zero, 4, hipMemcpyHostToDevice);
+    return fail(ILL_E_TIMEOUT, "device wait timed out (site %d); the pass was abandoned", err);
+  }
+  return 0;
+}
+
+int read_state(ill_engine* e, IllState* s) {
+  HCK(hipMemcpyAsync(s, e->st, sizeof(IllState), hipMemcpyDeviceToHost, e->stream));
+  HCK(hipStreamSynchronize(e->stream));
+  return 0;
+}
+
+int write_pos_n(ill_engine* e, int pos, int n) {
+  int32_t v[2] = {pos, n};
+  HCK(hipMemcpyAsync(e->st, v, 8, hipMemcpyHostToDevice, e->stream));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ill_last_error(void) { return g_err.c_str(); }
+
+int ill_create(const char* path, int max_context, int max_pass, int max_steps, ill_engine** out) {
+  if (!path || !out) return fail(ILL_E_ARG, "null argument");
+  *out = nullptr;
+  if (max_context < 64 || max_steps < 1) return fail(ILL_E_ARG, "bad sizes");
+  if (max_pass < 1 || max_pass > ILL_MAXT) max_pass = ILL_MAXT;
+  Mapped m;
+  {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return fail(ILL_E_FILE, "cannot open %s", path);
+    struct stat sb;
+    if (fstat(fd, &sb) != 0) {
+      close(fd);
+      return fail(ILL_E_FILE, "cannot stat %s", path);
+    }
+    m.len = (size_t)sb.st_size;
+    if (m.len < (size_t)kHeader) {
+      close(fd);
+      return fail(ILL_E_FILE, "%s: bad size %zu", path, m.len);
+    }
+    m.base = mmap(nullptr, m.len, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (m.base == MAP_FAILED) {
+      m.base = nullptr;
+      return fail(ILL_E_FILE, "mmap failed for %s", path);
+    }
+  }
+  const uint8_t* base = (const uint8_t*)m.base;
+  uint32_t hdr[4];
+  memcpy(hdr, base, 16);
+  if (hdr[0] != kMagic) return fail(ILL_E_FILE, "%s: not an instantllm model", path);
+  if (hdr[1] != 1) return fail(ILL_E_FILE, "%s: unsupported version %u", path, hdr[1]);
+  const int fmt = (int)hdr[2], count = (int)hdr[3];
+  if (fmt < 0 || fmt > 2) return fail(ILL_E_FILE, "%s: unknown weight format %d", path, fmt);
+  if (count < 16 || (count - 4) % 12 || 16 + (size_t)count * 16 > (size_t)kHeader) return fail(ILL_E_FILE, "%s: tensor table mismatch", path);
+  const int layers = (count - 4) / 12;
+  if (layers > ILL_MAXLAYERS) return fail(ILL_E_FILE, "%s: %d layers (max %d)", path, layers, ILL_MAXLAYERS);
+  if (fmt != 2) return fail(ILL_E_FORMAT, "%s: weight format %d (only q4 is built into this engine so far)", path, fmt);
+  std::vector<uint64_t> tab(2 * (size_t)count);
+  memcpy(tab.data(), base + 16, tab.size() * 8);
+  auto off = [&](int id) { return tab[2 * id]; };
+  auto size = [&](int id) { return tab[2 * id + 1]; };
+  for (int id = 0; id < count; id++)
+    if (size(id) && off(id) + size(id) > m.len) return fail(ILL_E_FILE, "%s: tensor %d out of range", path, id);
+  auto need = [&](int id, size_t bytes) { return size(id) == bytes; };
+  const int vocab = (int)(size(0) * 2 / ILL_H);
+  if (vocab < 16 || vocab % 16 || !need(0, (size_t)vocab * ILL_H / 2) || !need(1, (size_t)vocab * (ILL_H / 64) * 4) ||
+      !need(2, ILL_H * 4))
+    return fail(ILL_E_FILE, "%s: bad embedding tensors", path);
+  for (int l = 0; l < layers; l++) {
+    const int b = 3 + 12 * l;
+    if (!need(b + 0, ILL_H * 4) || !need(b + 1, (size_t)ILL_QKV * ILL_H / 2) || !need(b + 2, (size_t)ILL_QKV * 14 * 4) ||
+        !need(b + 3, ILL_QKV * 4) || !need(b + 4, (size_t)ILL_H * ILL_H / 2) || !need(b + 5, (size_t)ILL_H * 14 * 4) ||
+        !need(b + 6, ILL_H * 4) || !need(b + 7, (size_t)2 * ILL_FF * ILL_H / 2) || !need(b + 8, (size_t)2 * ILL_FF * 14 * 4) ||
+        !need(b + 9, (size_t)ILL_H * ILL_FF / 2) || !need(b + 10, (size_t)ILL_H * 76 * 4))
+      return fail(ILL_E_FILE, "%s: layer %d tensor sizes do not match the q4 model shape", path, l);
+  }
+
+  ill_engine* e = new ill_engine();
+  e->fmt = fmt;
+  e->layers = layers;
+  e->vocab = vocab;
+  e->maxctx = (max_context + 63) / 64 * 64;
+  e->maxpass = max_pass;
+  e->maxsteps = max_steps;
+  auto cleanup = [&](int rc) {
+    ill_destroy(e);
+    return rc;
+  };
+
+  // ---- device weight layout: one allocation, every tensor 256-byte aligned
+  const size_t qkvW = (size_t)ILL_QKV * ILL_H / 2, qkvS = (size_t)ILL_QKV / 16 * ILL_KST * 128;
+  const size_t oW = (size_t)ILL_H * ILL_H / 2, oS = (size_t)ILL_H / 16 * ILL_KST * 128;
+  const size_t guW = (size_t)2 * ILL_FF * ILL_H / 2, guS = (size_t)2 * ILL_FF / 16 * ILL_KST * 128;
+  const size_t dW = (size_t)ILL_H * ILL_FF / 2, dS = (size_t)ILL_NGU * ILL_NOT * 64;
+  const size_t embW = (size_t)vocab * ILL_H / 2, embS = (size_t)vocab / 16 * ILL_KST * 128;
+  size_t per_layer = al256(qkvW) + al256(qkvS) + al256(oW) + al256(oS) + al256(guW) + al256(guS) + al256(dW) + al256(dS) +
+                     al256(ILL_QKV * 4) + 2 * al256(ILL_H * 4);
+  size_t total = al256(embW) + al256(embS) + al256(ILL_H * 4) + per_layer * layers;
+  std::vector<uint8_t> host(total);
+  size_t cur = 0;
+  auto take = [&](size_t n) {
+    const size_t o = cur;
+    cur += al256(n);
+    return o;
+  };
+  std::vector<int> ident;
+  // embedding / lm_head
+  const size_t o_embW = take(embW), o_embS = take(embS), o_fn = take(ILL_H * 4);
+  {
+    ident.resize(vocab);
+    for (int i = 0; i < vocab; i++) ident[i] = i;
+    repack_rows(base + off(0), (const uint32_t*)(base + off(1)), ILL_H, ident, host.data() + o_embW, (uint32_t*)(host.data() + o_embS));
+    memcpy(host.data() + o_fn, base + off(2), ILL_H * 4);
+  }
+  struct LO { size_t qkvW, qkvS, oW, oS, guW, guS, dW, dS, b, ln1, ln2; };
+  std::vector<LO> lo(layers);
+  std::vector<int> rows_qkv(ILL_QKV), rows_o(ILL_H), rows_gu(2 * ILL_FF);
+  for (int i = 0; i < ILL_QKV; i++) rows_qkv[i] = i;
+  for (int i = 0; i < ILL_H; i++) rows_o[i] = i;
+  // gate/up: unit block ub, tile k (0-3 gate, 4-7 up), row n -> unit 64 ub + 16 (k % 4) + n;
+  // .ill row of gate unit u = 4 (u / 2) + u % 2, of up unit u = 4 (u / 2) + 2 + u % 2.
+  for (int ub = 0; ub < ILL_NGU; ub++)
+    for (int k = 0; k < 8; k++)
+      for (int n = 0; n < 16; n++) {
+        const int u = 64 * ub + 16 * (k & 3) + n;
+        rows_gu[(ub * 8 + k) * 16 + n] = 4 * (u / 2) + (k >= 4 ? 2 : 0) + (u & 1);
+      }
+  for (int l = 0; l < layers; l++) {
+    const int b = 3 + 12 * l;
+    LO& L = lo[l];
+    L.qkvW = take(qkvW); L.qkvS = take(qkvS); L.oW = take(oW); L.oS = take(oS);
+    L.guW = take(guW); L.guS = take(guS); L.dW = take(dW); L.dS = take(dS);
+    L.b = take(ILL_QKV * 4); L.ln1 = take(ILL_H * 4); L.ln2 = take(ILL_H * 4);
+    repack_rows(base + off(b + 1), (const uint32_t*)(base + off(b + 2)), ILL_H, rows_qkv, host.data() + L.qkvW, (uint32_t*)(host.data() + L.qkvS));
+    repack_rows(base + off(b + 4), (const uint32_t*)(base + off(b + 5)), ILL_H, rows_o, host.data() + L.oW, (uint32_t*)(host.data() + L.oS));
+    repack_rows(base + off(b + 7), (const uint32_t*)(base + off(b + 8)), ILL_H, rows_gu, host.data() + L.guW, (uint32_t*)(host.data() + L.guS));
+    repack_down(base + off(b + 9), (const uint32_t*)(base + off(b + 10)), host.data() + L.dW, (uint32_t*)(host.data() + L.dS));
+    memcpy(host.data() + L.b, base + off(b + 3), ILL_QKV * 4);
+    memcpy(host.data() + L.ln1, base + off(b + 0), ILL_H * 4);
+    memcpy(host.data() + L.ln2, base + off(b + 6), ILL_H * 4);
+  }
+
+  if (hipSetDevice(0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "no HIP device"));
+  int maxb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, 0) != hipSuccess || maxb < 1)
+    return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d)", maxb));
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipGetDeviceProperties failed"));
+  if (prop.multiProcessorCount * maxb < ILL_WG)
+    return cleanup(fail(ILL_E_HIP, "device has %d CUs x %d: the persistent pass needs %d resident workgroups", prop.multiProcessorCount, maxb, ILL_WG));
+  if (hipStreamCreate(&e->stream) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipStreamCreate failed"));
+  if (hipEventCreate(&e->ev0) != hipSuccess || hipEventCreate(&e->ev1) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipEventCreate failed"));
+  if (hipMalloc(&e->dweights, total) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights allocation failed (%zu B)", total));
+  if (hipMemcpy(e->dweights, host.data(), total, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights upload failed"));
+  host.clear();
+  host.shrink_to_fit();
+  uint8_t* D = e->dweights;
+  e->W.wemb = D + o_embW;
+  e->W.semb = (const uint32_t*)(D + o_embS);
+  e->W.fnorm = (const float*)(D + o_fn);
+  e->W.vocab = vocab;
+  e->W.layers = layers;
+  e->W.fmt = fmt;
+  e->hlayers.resize(layers);
+  for (int l = 0; l < layers; l++) {
+    IllLayerW& w = e->hlayers[l];
+    const LO& L = lo[l];
+    w.wqkv = D + L.qkvW; w.sqkv = (const uint32_t*)(D + L.qkvS);
+    w.wo = D + L.oW; w.so = (const uint32_t*)(D + L.oS);
+    w.wgu = D + L.guW; w.sgu = (const uint32_t*)(D + L.guS);
+    w.wd = D + L.dW; w.sd = (const uint32_t*)(D + L.dS);
+    w.bqkv = (const float*)(D + L.b); w.ln1 = (const float*)(D + L.ln1); w.ln2 = (const float*)(D + L.ln2);
+  }
+  auto dalloc = [&](void** p, size_t bytes) {
+    if (hipMalloc(p, bytes) != hipSuccess) return false;
+    return hipMemset(*p, 0, bytes) == hipSuccess;
+  };
+  const size_t kvb = (size_t)layers * ILL_NKV * e->maxctx * 64 * 2;
+  const size_t tw = (size_t)16 * ILL_H * 8;
+  bool ok = dalloc((void**)&e->dlayers, sizeof(IllLayerW) * layers) && dalloc((void**)&e->st, 64) && dalloc((void**)&e->ctl, 64) &&
+            dalloc((void**)&e->ptoks, 64) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
+            dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
+            dalloc((void**)&e->xa, tw) && dalloc((void**)&e->xb, tw) && dalloc((void**)&e->q, tw) && dalloc((void**)&e->attn, tw) &&
+            dalloc((void**)&e->kvn, (size_t)16 * 2 * 2 * 32 * 8) && dalloc((void**)&e->part, (size_t)ILL_NGU * tw) &&
+            dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
+            dalloc((void**)&e->out_dev, (size_t)max_steps * 4);
+  if (!ok) return cleanup(fail(ILL_E_HIP, "device buffer allocation failed"));
+  if (hipHostMalloc((void**)&e->out_host, (size_t)max_steps * 4, hipHostMallocDefault) != hipSuccess)
+    return cleanup(fail(ILL_E_HIP, "pinned token buffer allocation failed"));
+  for (int i = 0; i < max_steps; i++) e->out_host[i] = -1;
+  if (hipMemcpy(e->dlayers, e->hlayers.data(), sizeof(IllLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
+    return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
+  {
+    // RoPE table: angle = pos * theta^(-2i/64) in float64, cos/sin rounded once to fp32
+    // (tools/reference/qwen_ref.py:118-127).
+    std::vector<float2> r((size_t)(e->maxctx + 16) * 32);
+    for (int p = 0; p < e->maxctx + 16; p++)
+      for (int i = 0; i < 32; i++) {
+        const double inv = 1.0 / std::pow(1000000.0, (double)(2 * i) / 64.0);
+        const double ang = (double)p * inv;
+        r[(size_t)p * 32 + i] = make_float2((float)std::cos(ang), (float)std::sin(ang));
+      }
+    if (hipMemcpy(e->rope, r.data(), r.size() * 8, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "rope upload failed"));
+  }
+  {
+    IllCtl c{};
+    c.epoch = 1;
+    if (hipMemcpy(e->ctl, &c, sizeof c, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "ctl upload failed"));
+    IllState s{};
+    s.maxctx = e->maxctx;
+    s.maxsteps = max_steps;
+    s.eos0 = 151645;
+    s.eos1 = 151643;
+    s.nver = 1;
+    s.tspec = 1;
+    s.done = 1;   // idle until a request sets the state
+    if (hipMemcpy(e->st, &s, sizeof s, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "state upload failed"));
+  }
+  IllPassArgs& a = e->args;
+  a.W = e->W;
+  a.L = e->dlayers;
+  a.st = e->st;
+  a.ctl = e->ctl;
+  a.ptoks = e->ptoks;
+  a.tree = e->tree;
+  a.rope = e->rope;
+  a.kc = e->kc;
+  a.vt = e->vt;
+  a.xa = e->xa;
+  a.xb = e->xb;
+  a.q = e->q;
+  a.kvn = e->kvn;
+  a.attn = e->attn;
+  a.part = e->part;
+  a.lmp = e->lmp;
+  a.logits = e->logits;
+  a.out_dev = e->out_dev;
+  a.out_host = e->out_host;
+  a.maxctx = e->maxctx;
+  a.maxsteps = max_steps;
+  if (hipDeviceSynchronize() != hipSuccess) return cleanup(fail(ILL_E_HIP, "device sync failed"));
+  *out = e;
+  return ILL_OK;
+}
+
+int ill_destroy(ill_engine* e) {
+  if (!e) return ILL_OK;
+  if (e->stream) hipStreamSynchronize(e->stream);
+  if (e->gexec) hipGraphExecDestroy(e->gexec);
+  if (e->graph) hipGraphDestroy(e->graph);
+  void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->xa, e->xb,
+                  e->q, e->kvn, e->attn, e->part, e->lmp, e->logits, e->out_dev};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  if (e->out_host) hipHostFree(e->out_host);
+  if (e->ev0) hipEventDestroy(e->ev0);
+  if (e->ev1) hipEventDestroy(e->ev1);
+  if (e->stream) hipStreamDestroy(e->stream);
+  delete e;
+  return ILL_OK;
+}
+
+int ill_vocab(const ill_engine* e) { return e ? e->vocab : ILL_E_ARG; }
+int ill_layers(const ill_engine* e) { return e ? e->layers : ILL_E_ARG; }
+int ill_format(const ill_engine* e) { return e ? e->fmt : ILL_E_ARG; }
+
+int ill_set_state(ill_engine* e, const int32_t state[16]) {
+  if (!e || !state) return fail(ILL_E_ARG, "null argument");
+  IllState s;
+  memcpy(&s, state, sizeof s);
+  if (s.maxctx != e->maxctx) s.maxctx = e->maxctx;
+  if (s.maxsteps > e->maxsteps || s.maxsteps < 1) return fail(ILL_E_ARG, "maxsteps %d outside 1..%d", s.maxsteps, e->maxsteps);
+  if (s.pos < 0 || s.pos >= e->maxctx) return fail(ILL_E_ARG, "pos %d outside the context", s.pos);
+  HCK(hipMemcpyAsync(e->st, &s, sizeof s, hipMemcpyHostToDevice, e->stream));
+  HCK(hipStreamSynchronize(e->stream));
+  return ILL_OK;
+}
+
+int ill_get_state(ill_engine* e, int32_t state[16]) {
+  if (!e || !state) return fail(ILL_E_ARG, "null argument");
+  IllState s;
+  const int rc = read_state(e, &s);
+  if (rc) return rc;
+  memcpy(state, &s, sizeof s);
+  return ILL_OK;
+}
+
+int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
+  if (!e || !toks || n < 1) return fail(ILL_E_ARG, "bad prefill arguments");
+  IllState s;
+  int rc = read_state(e, &s);
+  if (rc) return rc;
+  if (s.done) return fail(ILL_E_ARG, "state is done: set the state before a prefill");
+  if (s.pos + n + 16 > e->maxctx) return fail(ILL_E_ARG, "prompt of %d tokens at pos %d exceeds the context %d", n, s.pos, e->maxctx);
+  for (int i = 0; i < n; i++)
+    if (toks[i] < 0 || toks[i] >= e->vocab) return fail(ILL_E_ARG, "token %d out of range", toks[i]);
+  int pos = s.pos;
+  for (int c0 = 0; c0 < n; c0 += 16) {
+    const int rows = n - c0 < 16 ? n - c0 : 16;
+    const bool last = c0 + rows == n;
+    HCK(hipMemcpyAsync(e->ptoks, toks + c0, rows * 4, hipMemcpyHostToDevice, e->stream));
+    if ((rc = write_pos_n(e, pos, rows))) return rc;
+    if (last) rc = set_ctl(e, ILL_MODE_ROWS, rows, rows - 1, 1, write_logits, 1);
+    else rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, 0, 0, 0);
+    if (rc) return rc;
+    if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
+    pos += rows;
+    // the staging copies above read host memory asynchronously: keep `toks` alive
+    HCK(hipStreamSynchronize(e->stream));
+  }
+  if (write_logits) e->logits_rows_valid = 0;
+  if ((rc = check_err(e))) return rc;
+  if (write_logits) {
+    // the last row's logits sit at row (rows - 1); move them to row 0 for ill_read_logits
+    const int rows = (n - 1) % 16 + 1;
+    if (rows != 1) HCK(hipMemcpy(e->logits, e->logits + (size_t)(rows - 1) * e->vocab, (size_t)e->vocab * 4, hipMemcpyDeviceToDevice));
+    e->logits_rows_valid = 1;
+  }
+  return ILL_OK;
+}
+
+int ill_decode_step(ill_engine* e, int write_logits) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits, 1);
+  if (rc) return rc;
+  if ((rc = launch(e, 1))) return rc;
+  if ((rc = check_err(e))) return rc;
+  if (write_logits) e->logits_rows_valid = 1;
+  return ILL_OK;
+}
+
+int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t* toks, int write_logits) {
+  if (!e || rows < 1 || rows > 16) return fail(ILL_E_ARG, "rows must be 1..16");
+  int32_t tk[16];
+  if (tree) {
+    if (tree[0] != rows) return fail(ILL_E_ARG, "tree[0] = %d but rows = %d", tree[0], rows);
+    for (int i = 1; i < rows; i++) {
+      const int p = tree[ILL_TR_PARENT + i];
+      if (p < 0 || p >= i) return fail(ILL_E_ARG, "tree parent[%d] = %d must be in 0..%d", i, p, i - 1);
+      if (tree[ILL_TR_DEPTH + i] != tree[ILL_TR_DEPTH + p] + 1) return fail(ILL_E_ARG, "tree depth[%d] inconsistent with its parent", i);
+    }
+    if (tree[ILL_TR_DEPTH] != 0) return fail(ILL_E_ARG, "tree root depth must be 0");
+    for (int i = 0; i < rows; i++) tk[i] = tree[ILL_TR_TOK + i];
+  } else {
+    if (!toks) return fail(ILL_E_ARG, "chain pass needs toks");
+    for (int i = 0; i < rows; i++) tk[i] = toks[i];
+  }
+  for (int i = 0; i < rows; i++)
+    if (tk[i] < 0 || tk[i] >= e->vocab) return fail(ILL_E_ARG, "token %d out of range", tk[i]);
+  IllState s;
+  int rc = read_state(e, &s);
+  if (rc) return rc;
+  if (s.done) return fail(ILL_E_ARG, "state is done");
+  if (s.pos + 16 > e->maxctx) return fail(ILL_E_ARG, "pass exceeds the context");
+  HCK(hipMemcpyAsync(e->ptoks, tk, rows * 4, hipMemcpyHostToDevice, e->stream));
+  if (tree) HCK(hipMemcpyAsync(e->tree, tree, ILL_TR_INTS * 4, hipMemcpyHostToDevice, e->stream));
+  if ((rc = write_pos_n(e, s.pos, rows))) return rc;
+  if ((rc = set_ctl(e, tree ? ILL_MODE_TREE : ILL_MODE_ROWS, rows, 0, rows, write_logits, 2))) return rc;
+  if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
+  if ((rc = check_err(e))) return rc;
+  if (write_logits) e->logits_rows_valid = rows;
+  return ILL_OK;
+}
+
+int ill_capture_steps(ill_engine* e, int nsteps) {
+  if (!e || nsteps < 1) return fail(ILL_E_ARG, "bad step count");
+  if (e->gexec) {
+    hipGraphExecDestroy(e->gexec);
+    e->gexec = nullptr;
+  }
+  if (e->graph) {
+    hipGraphDestroy(e->graph);
+    e->graph = nullptr;
+  }
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  for (int i = 0; i < nsteps; i++)
+    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  HCK(hipStreamEndCapture(e->stream, &e->graph));
+  HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
+  e->graph_steps = nsteps;
+  return ILL_OK;
+}
+
+int ill_launch_graph(ill_engine* e) {
+  if (!e || !e->gexec) return fail(ILL_E_ARG, "no captured graph");
+  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
+  if (rc) return rc;
+  HCK(hipGraphLaunch(e->gexec, e->stream));
+  return ILL_OK;
+}
+
+int ill_sync(ill_engine* e) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  return check_err(e);
+}
+
+const int32_t* ill_out_tokens(ill_engine* e) { return e ? e->out_host : nullptr; }
+
+int ill_reset_out_tokens(ill_engine* e) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  HCK(hipStreamSynchronize(e->stream));
+  for (int i = 0; i < e->maxsteps; i++) e->out_host[i] = -1;
+  return ILL_OK;
+}
+
+int ill_read_logits(ill_engine* e, int row, float* out) {
+  if (!e || !out || row < 0 || row >= 16) return fail(ILL_E_ARG, "bad logits row");
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipMemcpy(out, e->logits + (size_t)row * e->vocab, (size_t)e->vocab * 4, hipMemcpyDeviceToHost));
+  return ILL_OK;
+}
+
+// reference cache layout [layer][kvh][npos][64]; the engine keeps K in that layout (with
+// maxctx rows) and V transposed per 64 slots.
+int ill_kv_copy_out(ill_engine* e, int npos, uint16_t* k, uint16_t* v) {
+  if (!e || !k || !v || npos < 0 || npos > e->maxctx) return fail(ILL_E_ARG, "bad kv copy");
+  HCK(hipStreamSynchronize(e->stream));
+  const size_t per = (size_t)e->maxctx * 64;
+  std::vector<uint16_t> kt(per), vtt(per);
+  for (int lh = 0; lh < e->layers * ILL_NKV; lh++) {
+    HCK(hipMemcpy(kt.data(), e->kc + lh * per, per * 2, hipMemcpyDeviceToHost));
+    HCK(hipMemcpy(vtt.data(), e->vt + lh * per, per * 2, hipMemcpyDeviceToHost));
+    memcpy(k + (size_t)lh * npos * 64, kt.data(), (size_t)npos * 64 * 2);
+    for (int p = 0; p < npos; p++)
+      for (int d = 0; d < 64; d++) v[((size_t)lh * npos + p) * 64 + d] = vtt[(size_t)(p >> 6) * 4096 + d * 64 + (p & 63)];
+  }
+  return ILL_OK;
+}
+
+int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v) {
+  if (!e || !k || !v || npos < 0 || npos > e->maxctx) return fail(ILL_E_ARG, "bad kv copy");
+  HCK(hipStreamSynchronize(e->stream));
+  const size_t per = (size_t)e->maxctx * 64;
+  std::vector<uint16_t> kt(per), vtt(per);
+  for (int lh = 0; lh < e->layers * ILL_NKV; lh++) {
+    HCK(hipMemcpy(kt.data(), e->kc + lh * per, per * 2, hipMemcpyDeviceToHost));
+    HCK(hipMemcpy(vtt.data(), e->vt + lh * per, per * 2, hipMemcpyDeviceToHost));
+    memcpy(kt.data(), k + (size_t)lh * npos * 64, (size_t)npos * 64 * 2);
+    for (int p = 0; p < npos; p++)
+      for (int d = 0; d < 64; d++) vtt[(size_t)(p >> 6) * 4096 + d * 64 + (p & 63)] = v[((size_t)lh * npos + p) * 64 + d];
+    HCK(hipMemcpy(e->kc + lh * per, kt.data(), per * 2, hipMemcpyHostToDevice));
+    HCK(hipMemcpy(e->vt + lh * per, vtt.data(), per * 2, hipMemcpyHostToDevice));
+  }
+  return ILL_OK;
+}
+
+int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk, int32_t* out, int* n_out, float* logits_out) {
+  if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
+  if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
+  if (chunk < 1) chunk = 1;
+  *n_out = 0;
+  int rc;
+  if ((rc = ill_reset_out_tokens(e))) return rc;
+  int32_t s[16] = {0};
+  s[0] = 0;
+  s[1] = ntok;
+  s[4] = e->maxctx;
+  s[5] = max_new;
+  s[6] = 151645;
+  s[7] = 151643;
+  s[8] = 1;
+  s[9] = 1;
+  if ((rc = ill_set_state(e, s))) return rc;
+  if ((rc = ill_prefill(e, toks, ntok, logits_out != nullptr))) return rc;
+  if (logits_out && (rc = ill_read_logits(e, 0, logits_out))) return rc;
+  if (e->graph_steps != chunk && (rc = ill_capture_steps(e, chunk))) return rc;
+  volatile const int32_t* ot = e->out_host;
+  int got = 0, encoded = 1;
+  bool stopped = false;
+  while (!stopped && got < max_new) {
+    if (encoded < max_new && encoded - got <= chunk) {
+      if ((rc = ill_launch_graph(e))) return rc;
+      encoded += chunk;
+      continue;
+    }
+    const int t = ot[got];
+    if (t < 0) {
+      // a finished stream with no new token means the device stopped (or failed)
+      if (hipStreamQuery(e->stream) == hipSuccess && ot[got] < 0) {
+        if ((rc = check_err(e))) return rc;
+        if (encoded >= max_new) break;
+      }
+      continue;
+    }
+    got++;
+    if (t == 151645 || t == 151643) break;
+    out[(*n_out)++] = t;
+  }
+  HCK(hipStreamSynchronize(e->stream));
+  return check_err(e);
+}
+
+int ill_time_graph(ill_engine* e, int iters, float* ms) {
+  if (!e || !e->gexec || iters < 1 || !ms) return fail(ILL_E_ARG, "bad timing arguments");
+  hipEvent_t a, b;
+  HCK(hipEventCreate(&a));
+  HCK(hipEventCreate(&b));
+  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
+  if (rc) return rc;
+  HCK(hipEventRecord(a, e->stream));
+  for (int i = 0; i < iters; i++) HCK(hipGraphLaunch(e->gexec, e->stream));
+  HCK(hipEventRecord(b, e->stream));
+  HCK(hipEventSynchronize(b));
+  HCK(hipEventElapsedTime(ms, a, b));
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  return check_err(e);
+}
+
+int ill_trace_enable(ill_engine* e, int on) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  HCK(hipStreamSynchronize(e->stream));
+  if (on && !e->args.trace) {
+    void* p = nullptr;
+    HCK(hipMalloc(&p, (size_t)ILL_WG * ILL_TRACE_SLOTS * 8));
+    HCK(hipMemset(p, 0, (size_t)ILL_WG * ILL_TRACE_SLOTS * 8));
+    e->args.trace = (uint64_t*)p;
+  } else if (!on && e->args.trace) {
+    HCK(hipFree(e->args.trace));
+    e->args.trace = nullptr;
+  }
+  return ILL_OK;
+}
+
+int ill_trace_read(ill_engine* e, uint64_t* out, int* slots) {
+  if (!e || !out || !slots) return fail(ILL_E_ARG, "null argument");
+  if (!e->args.trace) return fail(ILL_E_ARG, "trace is off");
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipMemcpy(out, e->args.trace, (size_t)ILL_WG * ILL_TRACE_SLOTS * 8, hipMemcpyDeviceToHost));
+  *slots = ILL_TRACE_SLOTS;
+  return ILL_OK;
+}
+
+int ill_last_pass_ms(ill_engine* e, float* ms) {
+  if (!e || !ms) return fail(ILL_E_ARG, "null argument");
+  HCK(hipEventSynchronize(e->ev1));
+  HCK(hipEventElapsedTime(ms, e->ev0, e->ev1));
+  return ILL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,212 @@
+"""Python binding of the C ABI (include/ill_hip.h) -- the check/bench harness's view of
+the engine. It mirrors the reference's Swift `Engine` API (Sources/Engine/Engine.swift):
+`Engine(model_path, max_context, max_pass, max_steps)`, `generate`, the pass encoders
+(prefill / decode step / verify pass / commit inside the pass) and the device State.
+
+Everything runs in libillhip.so on the GPU; this module only marshals arguments. There is
+no CPU fallback: a missing library raises at import of the engine.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libillhip.so"
+
+ILL_OK, ILL_E_ARG, ILL_E_FILE, ILL_E_HIP, ILL_E_TIMEOUT, ILL_E_FORMAT = 0, -1, -2, -3, -4, -5
+TR_DEPTH, TR_PARENT, TR_TOK, TR_ANC, TR_INTS = 1, 17, 33, 49, 65
+STATE_FIELDS = ("pos", "n", "step", "done", "maxctx", "maxsteps", "eos0", "eos1",
+                "nver", "tspec", "passes", "accepted", "tlmh", "nodraft", "learned", "tree")
+
+_lib = None
+
+
+class IllError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"ill error {code}: {msg}")
+        self.code = code
+
+
+def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load libillhip.so (built by instantllm_amd/build.py). Raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build it with `python instantllm_amd/build.py` "
+                           "(the engine has no CPU fallback)")
+    lib = C.CDLL(str(p))
+    P, I32, F32 = C.c_void_p, C.c_int32, C.c_float
+    ip = C.POINTER(C.c_int32)
+    sig = {
+        "ill_last_error": (C.c_char_p, []),
+        "ill_create": (C.c_int, [C.c_char_p, C.c_int, C.c_int, C.c_int, C.POINTER(P)]),
+        "ill_destroy": (C.c_int, [P]),
+        "ill_vocab": (C.c_int, [P]),
+        "ill_layers": (C.c_int, [P]),
+        "ill_format": (C.c_int, [P]),
+        "ill_set_state": (C.c_int, [P, ip]),
+        "ill_get_state": (C.c_int, [P, ip]),
+        "ill_prefill": (C.c_int, [P, ip, C.c_int, C.c_int]),
+        "ill_decode_step": (C.c_int, [P, C.c_int]),
+        "ill_verify_pass": (C.c_int, [P, C.c_int, ip, ip, C.c_int]),
+        "ill_capture_steps": (C.c_int, [P, C.c_int]),
+        "ill_launch_graph": (C.c_int, [P]),
+        "ill_sync": (C.c_int, [P]),
+        "ill_out_tokens": (ip, [P]),
+        "ill_reset_out_tokens": (C.c_int, [P]),
+        "ill_read_logits": (C.c_int, [P, C.c_int, C.POINTER(F32)]),
+        "ill_kv_copy_out": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16)]),
+        "ill_kv_copy_in": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16)]),
+        "ill_generate": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), C.POINTER(F32)]),
+        "ill_time_graph": (C.c_int, [P, C.c_int, C.POINTER(F32)]),
+        "ill_last_pass_ms": (C.c_int, [P, C.POINTER(F32)]),
+        "ill_trace_enable": (C.c_int, [P, C.c_int]),
+        "ill_trace_read": (C.c_int, [P, C.POINTER(C.c_uint64), C.POINTER(C.c_int)]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _ = I32
+    _lib = lib
+    return lib
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def _ptr(a: np.ndarray, t):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+class Engine:
+    """One model on one GPU (Engine.swift:71)."""
+
+    def __init__(self, model_path: str, max_context: int = 2048, max_pass: int = 16, max_steps: int = 4096):
+        self.lib = load_library()
+        h = C.c_void_p()
+        self._check(self.lib.ill_create(str(model_path).encode(), max_context, max_pass, max_steps, C.byref(h)))
+        self.h = h
+        self.vocab = self.lib.ill_vocab(h)
+        self.layers = self.lib.ill_layers(h)
+        self.format = self.lib.ill_format(h)
+        self.max_steps = max_steps
+        self.max_context = (max_context + 63) // 64 * 64
+
+    def _check(self, rc: int):
+        if rc != ILL_OK:
+            raise IllError(rc, self.lib.ill_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.ill_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- device State (Shaders.swift:37-54) -------------------------------------------
+    def set_state(self, pos: int = 0, n: int = 1, maxsteps: int = 64, eos=(151645, 151643), **kw):
+        s = dict(pos=pos, n=n, step=0, done=0, maxctx=self.max_context, maxsteps=maxsteps,
+                 eos0=eos[0], eos1=eos[1], nver=1, tspec=1)
+        s.update(kw)
+        a = _i32([s.get(f, 0) for f in STATE_FIELDS])
+        self._check(self.lib.ill_set_state(self.h, _ptr(a, C.c_int32)))
+
+    def get_state(self) -> dict:
+        a = np.zeros(16, np.int32)
+        self._check(self.lib.ill_get_state(self.h, _ptr(a, C.c_int32)))
+        return {f: int(v) for f, v in zip(STATE_FIELDS, a)}
+
+    # ---- passes --------------------------------------------------------------------------
+    def prefill(self, toks, write_logits: bool = False):
+        a = _i32(toks)
+        self._check(self.lib.ill_prefill(self.h, _ptr(a, C.c_int32), len(a), int(write_logits)))
+
+    def decode_step(self, write_logits: bool = False):
+        self._check(self.lib.ill_decode_step(self.h, int(write_logits)))
+
+    def verify_pass(self, rows: int, tree=None, toks=None, write_logits: bool = False):
+        t = _ptr(_i32(tree), C.c_int32) if tree is not None else None
+        k = _ptr(_i32(toks), C.c_int32) if toks is not None else None
+        self._check(self.lib.ill_verify_pass(self.h, rows, t, k, int(write_logits)))
+
+    def capture_steps(self, n: int):
+        self._check(self.lib.ill_capture_steps(self.h, n))
+
+    def launch_graph(self):
+        self._check(self.lib.ill_launch_graph(self.h))
+
+    def sync(self):
+        self._check(self.lib.ill_sync(self.h))
+
+    def out_tokens(self) -> np.ndarray:
+        p = self.lib.ill_out_tokens(self.h)
+        return np.ctypeslib.as_array(p, shape=(self.max_steps,))
+
+    def reset_out_tokens(self):
+        self._check(self.lib.ill_reset_out_tokens(self.h))
+
+    def read_logits(self, row: int = 0) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        self._check(self.lib.ill_read_logits(self.h, row, _ptr(out, C.c_float)))
+        return out
+
+    def kv_copy_out(self, npos: int):
+        k = np.empty((self.layers, 2, npos, 64), np.uint16)
+        v = np.empty_like(k)
+        self._check(self.lib.ill_kv_copy_out(self.h, npos, _ptr(k, C.c_uint16), _ptr(v, C.c_uint16)))
+        return k, v
+
+    def kv_copy_in(self, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        npos = k.shape[2]
+        self._check(self.lib.ill_kv_copy_in(self.h, npos, _ptr(k, C.c_uint16), _ptr(v, C.c_uint16)))
+
+    def generate(self, tokens, max_new: int, chunk: int = 8, want_logits: bool = False):
+        """Engine.generate (Engine.swift:922-1038) without drafting."""
+        a = _i32(tokens)
+        out = np.zeros(max_new, np.int32)
+        n = C.c_int(0)
+        lg = np.empty(self.vocab, np.float32) if want_logits else None
+        self._check(self.lib.ill_generate(self.h, _ptr(a, C.c_int32), len(a), max_new, chunk,
+                                          _ptr(out, C.c_int32), C.byref(n),
+                                          _ptr(lg, C.c_float) if lg is not None else None))
+        toks = out[: n.value].tolist()
+        return (toks, lg) if want_logits else toks
+
+    def last_pass_ms(self) -> float:
+        ms = C.c_float(0)
+        self._check(self.lib.ill_last_pass_ms(self.h, C.byref(ms)))
+        return ms.value
+
+    def trace_enable(self, on: bool = True):
+        self._check(self.lib.ill_trace_enable(self.h, int(on)))
+
+    def trace_read(self) -> np.ndarray:
+        """[256, slots] device-clock ticks (100 MHz) of the last pass; 0 = not reached."""
+        out = np.zeros(256 * 96, np.uint64)
+        n = C.c_int(0)
+        self._check(self.lib.ill_trace_read(self.h, _ptr(out, C.c_uint64), C.byref(n)))
+        return out[: 256 * n.value].reshape(256, n.value)
+
+    def time_graph(self, iters: int) -> float:
+        ms = C.c_float(0)
+        self._check(self.lib.ill_time_graph(self.h, iters, C.byref(ms)))
+        return ms.value

@@ -80,6 +80,15 @@ def float_embed(seed: int, s: ModelShape = ModelShape()) -> np.ndarray:
     return gen_tensor(seed, "embed", -1, (s.vocab, s.hidden))
 
 
+def float_embed_chunks(seed: int, s: ModelShape = ModelShape(), rows: int = 8192):
+    """The embedding in row chunks: the same values as `float_embed` (one generator,
+    drawn in order) without materializing the whole table."""
+    g = _rng(seed, _key("embed"))
+    for r0 in range(0, s.vocab, rows):
+        n = min(rows, s.vocab - r0)
+        yield _f16_round(0.02 * g.standard_normal((n, s.hidden), dtype=np.float32))
+
+
 def float_norm(seed: int, s: ModelShape = ModelShape()) -> np.ndarray:
     return gen_tensor(seed, "norm", -1, (s.hidden,))
 
@@ -138,9 +147,13 @@ def build_model(path: str, fmt: int, seed: int, shape: ModelShape = ModelShape()
                 q8_group: int = 64) -> int:
     """Generate the seeded model and write it as an `.ill` v1 file. Returns its size."""
     tensors: dict[int, bytes | np.ndarray] = {}
-    emb = float_embed(seed, shape)
-    tensors[F.EMBED], tensors[F.EMBED_SB] = _emit_matrix(fmt, emb, q8_group)
-    del emb
+    wparts, sparts = [], []
+    for chunk in float_embed_chunks(seed, shape):
+        w, sb = _emit_matrix(fmt, chunk, q8_group)
+        wparts.append(w)
+        sparts.append(sb)
+    tensors[F.EMBED], tensors[F.EMBED_SB] = b"".join(wparts), b"".join(sparts)
+    del wparts, sparts
     tensors[F.FINAL_NORM] = float_norm(seed, shape).astype("<f4")
     qo = F.qkv_row_order()
     go = F.gu_row_order(shape.ff)

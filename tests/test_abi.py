@@ -1,0 +1,52 @@
+"""CPU-side checks of the C-ABI library: it loads and exports every function declared in
+include/ill_hip.h (no compute calls without a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = (ROOT / "include" / "ill_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ill_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_pass_api():
+    names = declared_functions()
+    for f in ("ill_create", "ill_destroy", "ill_prefill", "ill_decode_step", "ill_verify_pass",
+              "ill_capture_steps", "ill_launch_graph", "ill_out_tokens", "ill_set_state", "ill_get_state"):
+        assert f in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib_path = ROOT / "instantllm_amd" / "libillhip.so"
+    if not lib_path.exists():
+        pytest.skip("libillhip.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(lib_path))
+    missing = [f for f in declared_functions() if not hasattr(lib, f)]
+    assert not missing, missing
+
+
+def test_last_error_and_bad_path_without_gpu():
+    """ill_create validates the file before touching the GPU."""
+    from instantllm_amd.engine import load_library
+    lib_path = ROOT / "instantllm_amd" / "libillhip.so"
+    if not lib_path.exists():
+        pytest.skip("libillhip.so not built")
+    lib = load_library()
+    h = ctypes.c_void_p()
+    rc = lib.ill_create(b"/nonexistent/model.ill", 1024, 16, 64, ctypes.byref(h))
+    assert rc == -2
+    assert b"cannot open" in lib.ill_last_error()
+
+
+def test_engine_binding_fails_loudly_without_library(tmp_path):
+    from instantllm_amd import engine
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        engine.load_library(tmp_path / "missing.so")

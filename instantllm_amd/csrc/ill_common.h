@@ -19,22 +19,15 @@
 // Device layout unit sizes (q4): a "block" is 16 rows x 128 columns = 2 quant groups.
 #define ILL_KST 7            // 896 / 128 column blocks per K = 896 row tile
 #define ILL_NGU 76           // 4864 / 64 hidden-unit blocks of the fused gate/up/down role
+#define ILL_GUD_N ILL_NGU    // contributions to each element of the post-MLP residual
 #define ILL_NOT 56           // 896 / 16 row tiles of O and down
 #define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV
 
-// Persistent-kernel geometry.
+// Persistent-kernel geometry (WG i runs on XCD i % 8, so consecutive WG ranges are
+// spread over all eight XCDs).
 #define ILL_WG 256           // workgroups (one per CU on MI355X)
 #define ILL_WG_THREADS 512   // 8 waves
 #define ILL_WAVES 8
-
-// Role bases: WG index ranges per layer role (WG i runs on XCD i % 8, so every range is
-// spread over all eight XCDs).
-#define ILL_R_QKV 0          // 36 WGs: one 32-row rotary block each
-#define ILL_R_ATT 36         // 28 WGs: (kv group, row) attention items
-#define ILL_N_ATT 28
-#define ILL_R_O 64           // 56 WGs: one 16-row O tile each
-#define ILL_R_GUD 120        // 76 WGs: 64 hidden units (gate+up+SiLU+down partial) each
-#define ILL_R_RED 196        // 56 WGs: residual + down-partial reduction for 16 rows each
 
 // State: the reference's 16-int control block (Shaders.swift:37-54), same field order.
 struct IllState {
@@ -53,7 +46,8 @@ struct IllCtl {
   int32_t write_logits;
   int32_t commit;       // 0: advance pos only (prefill chunk), 1: greedy commit, 2: spec commit
   int32_t last_tok;     // last committed token (decode input)
-  int32_t pad[7];
+  int32_t bank_rows[2]; // rows of each residual-accumulator bank still to be cleared
+  int32_t pad[5];
 };
 
 enum IllMode { ILL_MODE_DECODE = 0, ILL_MODE_ROWS = 1, ILL_MODE_TREE = 2 };
@@ -68,9 +62,9 @@ enum IllMode { ILL_MODE_DECODE = 0, ILL_MODE_ROWS = 1, ILL_MODE_TREE = 2 };
 // Per-layer device weight pointers (repacked layout).
 struct IllLayerW {
   const uint8_t* wqkv;   const uint32_t* sqkv;   // 72 row tiles x 7 blocks
-  const uint8_t* wo;     const uint32_t* so;     // 56 row tiles x 7 blocks
+  const uint8_t* wo;     const uint32_t* so;     // 14 column groups (heads) x 56 row tiles (512 B each)
   const uint8_t* wgu;    const uint32_t* sgu;    // 76 unit blocks x 8 tiles x 7 blocks
-  const uint8_t* wd;     const uint32_t* sd;     // 76 groups x 56 row tiles (512 B each)
+  const uint8_t* wd;     const uint32_t* sd;     // 76 column groups x 56 row tiles (512 B each)
   const float* bqkv;     // 1152, stored (rotary block) order
   const float* ln1;
   const float* ln2;

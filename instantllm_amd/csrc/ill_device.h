@@ -17,20 +17,41 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 #define ILL_WAIT_TICKS 200000000ull   // 2 s of the 100 MHz constant clock
 
+// Every device-side access to HBM goes through these helpers, which name the global
+// address space explicitly. Pointers taken from the argument struct are otherwise generic
+// and compile to FLAT instructions, which also count against lgkmcnt: every later LDS read
+// would then wait for all outstanding HBM loads and atomics of the wave.
+#define GAS __attribute__((address_space(1)))
+typedef unsigned int gu32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int gu32x2 __attribute__((ext_vector_type(2)));
+template <class T>
+__device__ __forceinline__ T gld(const T* p) {
+  T r;
+  if constexpr (sizeof(T) == 16) {
+    const gu32x4 x = *(const GAS gu32x4*)p;
+    __builtin_memcpy(&r, &x, 16);
+  } else if constexpr (sizeof(T) == 8) {
+    const gu32x2 x = *(const GAS gu32x2*)p;
+    __builtin_memcpy(&r, &x, 8);
+  } else {
+    r = *(const GAS T*)p;
+  }
+  return r;
+}
+template <class T>
+__device__ __forceinline__ void gst(T* p, T v) { *(GAS T*)p = v; }
+
 __device__ __forceinline__ uint64_t aload64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const GAS uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void astore64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((GAS uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int32_t aload32(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const GAS int32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void astore32(int32_t* p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void astore32u(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((GAS int32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t mkw(float v, uint32_t tag) {
   return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
@@ -41,10 +62,13 @@ __device__ __forceinline__ float wval(uint64_t w) { return __uint_as_float((uint
 
 __device__ __forceinline__ uint64_t clk() { return wall_clock64(); }
 
+// Tag of the lm_head argmax partials of a pass.
+__device__ __forceinline__ uint32_t tagof_lmh(uint32_t epoch) { return epoch * 32u + 31u; }
+
 // Records the first timeout code; every wait gives up once any is recorded.
 __device__ __forceinline__ void set_err(IllCtl* ctl, int code) {
   int32_t zero = 0;
-  __hip_atomic_compare_exchange_strong(&ctl->err, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+  __hip_atomic_compare_exchange_strong((GAS int32_t*)&ctl->err, &zero, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -158,10 +182,23 @@ __device__ __forceinline__ void q4_load(Q4Tile& t, const uint8_t* wtile, const u
   const int n = lane & 15;
 #pragma unroll
   for (int cb = 0; cb < ILL_KST; cb++) {
-    t.w[cb] = *(const uint4*)(wtile + cb * 1024 + lane * 16);
-    t.s[cb] = *(const uint2*)(stile + cb * 32 + n * 2);
+    t.w[cb] = gld((const uint4*)(wtile + cb * 1024 + lane * 16));
+    t.s[cb] = gld((const uint2*)(stile + cb * 32 + n * 2));
   }
 }
+
+// Asynchronous HBM -> LDS copy of `bytes` (a multiple of 16) by one wave: each lane moves 16 B
+// per instruction with global_load_lds_dwordx4 (no registers involved). Completion is
+// tracked by the wave's vmcnt; the LDS destination must be 16-byte aligned.
+__device__ __forceinline__ void wave_copy_to_lds(const uint8_t* src, uint8_t* lds_dst, int bytes, int lane) {
+  for (int off = 0; off < bytes; off += 1024) {
+    const int rem = bytes - off;
+    if (lane * 16 < rem)
+      __builtin_amdgcn_global_load_lds((const void*)(src + off + lane * 16),
+                                       (__attribute__((address_space(3))) void*)(lds_dst + off), 16, 0, 0);
+  }
+}
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0); }
 
 __device__ __forceinline__ v4i q4_unpack(uint32_t a, uint32_t b) {
   v4i r;
@@ -182,16 +219,19 @@ struct PrepLds {
 
 // Accumulate one 16-row tile over K = 896: acc[j] (rows t = 4*kg + j of the pass, weight
 // row n) += sum_G s*d*S + m*X. The per-value operation sequence is independent of T.
-template <int T>
-__device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, int lane, float acc[4]) {
+// `fetch(cb, w, s)` supplies block cb's 16 weight bytes and (scale, min) pairs for this lane.
+template <int T, class Fetch>
+__device__ __forceinline__ void q4_tile896f(Fetch fetch, const PrepLds& P, int lane, float acc[4]) {
   const int kg = lane >> 4, m = lane & 15;
   constexpr int RPL = T >= 4 ? 4 : T;
 #pragma unroll
   for (int cb = 0; cb < ILL_KST; cb++) {
+    uint4 wv;
+    uint2 sv;
+    fetch(cb, wv, sv);
 #pragma unroll
     for (int gi = 0; gi < 2; gi++) {
       const int G = 2 * cb + gi;
-      const uint4 wv = t.w[cb];
       const v4i b = gi == 0 ? q4_unpack(wv.x, wv.y) : q4_unpack(wv.z, wv.w);
       v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
       if (m < T) {
@@ -203,7 +243,7 @@ __device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, in
       const v4i z = {0, 0, 0, 0};
       const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
       const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-      const uint32_t sm = gi == 0 ? t.s[cb].x : t.s[cb].y;
+      const uint32_t sm = gi == 0 ? sv.x : sv.y;
       const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
 #pragma unroll
       for (int j = 0; j < RPL; j++) {
@@ -218,4 +258,20 @@ __device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, in
       }
     }
   }
+}
+
+// Tile held in registers (lm_head stream).
+template <int T>
+__device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, int lane, float acc[4]) {
+  q4_tile896f<T>([&](int cb, uint4& w, uint2& s) { w = t.w[cb]; s = t.s[cb]; }, P, lane, acc);
+}
+
+// Tile staged in LDS in the HBM block layout: 7 x 1 KiB weights at `w`, 7 x 128 B scales at `s`.
+template <int T>
+__device__ __forceinline__ void q4_tile896_lds(const uint8_t* w, const uint8_t* s, const PrepLds& P, int lane, float acc[4]) {
+  const int n = lane & 15;
+  q4_tile896f<T>([&](int cb, uint4& wv, uint2& sv) {
+    wv = *(const uint4*)(w + cb * 1024 + lane * 16);
+    sv = *(const uint2*)(s + cb * 128 + n * 8);
+  }, P, lane, acc);
 }

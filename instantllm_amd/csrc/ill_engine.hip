@@ -75,11 +75,12 @@ void repack_rows(const uint8_t* w, const uint32_t* sb, int K, const std::vector<
     }
 }
 
-// down projection [896][4864]: block (G, rt) = 512 B; lane l = 16 kg + n stores 8 bytes of
-// row 16 rt + n at columns 64 G + 16 kg; scales [G][rt][n].
-void repack_down(const uint8_t* w, const uint32_t* sb, uint8_t* dw, uint32_t* ds) {
-  const int rb = ILL_FF / 2, sg = ILL_FF / 64;
-  for (int G = 0; G < ILL_NGU; G++)
+// Split-K layout of a [896][K] projection (O: K = 896, down: K = 4864): block (G, rt) =
+// 512 B; lane l = 16 kg + n stores 8 bytes of row 16 rt + n at columns 64 G + 16 kg;
+// scales [G][rt][n]. A workgroup owning column group G reads one contiguous 28 KiB run.
+void repack_split(const uint8_t* w, const uint32_t* sb, int K, uint8_t* dw, uint32_t* ds) {
+  const int rb = K / 2, sg = K / 64;
+  for (int G = 0; G < sg; G++)
     for (int rt = 0; rt < ILL_NOT; rt++) {
       uint8_t* blk = dw + ((size_t)G * ILL_NOT + rt) * 512;
       for (int l = 0; l < 64; l++) {
@@ -108,7 +109,8 @@ struct ill_engine {
   float2* rope = nullptr;
   uint16_t* kc = nullptr;
   uint16_t* vt = nullptr;
-  uint64_t *xa = nullptr, *xb = nullptr, *q = nullptr, *kvn = nullptr, *attn = nullptr, *part = nullptr, *lmp = nullptr;
+  uint64_t *acc = nullptr, *lmp = nullptr;
+  size_t acc_bytes = 0;
   float* logits = nullptr;
   int32_t* out_dev = nullptr;
   int32_t* out_host = nullptr;
@@ -140,8 +142,8 @@ int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, in
 
 int launch(ill_engine* e, int T) {
   HCK(hipEventRecord(e->ev0, e->stream));
-  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
-  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
+  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
   HCK(hipGetLastError());
   HCK(hipEventRecord(e->ev1, e->stream));
   return 0;
@@ -152,8 +154,12 @@ int check_err(ill_engine* e) {
   HCK(hipMemcpyAsync(&err, &e->ctl->err, 4, hipMemcpyDeviceToHost, e->stream));
   HCK(hipStreamSynchronize(e->stream));
   if (err) {
-    int32_t zero = 0;
-    hipMemcpy(&e->ctl->err, &zero, 4, hipMemcpyHostToDevice);
+    // an abandoned pass leaves partial sums behind: clear both accumulator banks
+    int32_t zero[3] = {0, 0, 0};
+    hipMemcpy(&e->ctl->err, zero, 4, hipMemcpyHostToDevice);
+    hipMemcpy(&e->ctl->bank_rows[0], zero, 8, hipMemcpyHostToDevice);
+    hipMemset(e->acc, 0, e->acc_bytes);
+    hipDeviceSynchronize();
     return fail(ILL_E_TIMEOUT, "device wait timed out (site %d); the pass was abandoned", err);
   }
   return 0;
@@ -248,7 +254,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
 
   // ---- device weight layout: one allocation, every tensor 256-byte aligned
   const size_t qkvW = (size_t)ILL_QKV * ILL_H / 2, qkvS = (size_t)ILL_QKV / 16 * ILL_KST * 128;
-  const size_t oW = (size_t)ILL_H * ILL_H / 2, oS = (size_t)ILL_H / 16 * ILL_KST * 128;
+  const size_t oW = (size_t)ILL_H * ILL_H / 2, oS = (size_t)ILL_NH * ILL_NOT * 64;
   const size_t guW = (size_t)2 * ILL_FF * ILL_H / 2, guS = (size_t)2 * ILL_FF / 16 * ILL_KST * 128;
   const size_t dW = (size_t)ILL_H * ILL_FF / 2, dS = (size_t)ILL_NGU * ILL_NOT * 64;
   const size_t embW = (size_t)vocab * ILL_H / 2, embS = (size_t)vocab / 16 * ILL_KST * 128;
@@ -291,9 +297,9 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     L.guW = take(guW); L.guS = take(guS); L.dW = take(dW); L.dS = take(dS);
     L.b = take(ILL_QKV * 4); L.ln1 = take(ILL_H * 4); L.ln2 = take(ILL_H * 4);
     repack_rows(base + off(b + 1), (const uint32_t*)(base + off(b + 2)), ILL_H, rows_qkv, host.data() + L.qkvW, (uint32_t*)(host.data() + L.qkvS));
-    repack_rows(base + off(b + 4), (const uint32_t*)(base + off(b + 5)), ILL_H, rows_o, host.data() + L.oW, (uint32_t*)(host.data() + L.oS));
+    repack_split(base + off(b + 4), (const uint32_t*)(base + off(b + 5)), ILL_H, host.data() + L.oW, (uint32_t*)(host.data() + L.oS));
     repack_rows(base + off(b + 7), (const uint32_t*)(base + off(b + 8)), ILL_H, rows_gu, host.data() + L.guW, (uint32_t*)(host.data() + L.guS));
-    repack_down(base + off(b + 9), (const uint32_t*)(base + off(b + 10)), host.data() + L.dW, (uint32_t*)(host.data() + L.dS));
+    repack_split(base + off(b + 9), (const uint32_t*)(base + off(b + 10)), ILL_FF, host.data() + L.dW, (uint32_t*)(host.data() + L.dS));
     memcpy(host.data() + L.b, base + off(b + 3), ILL_QKV * 4);
     memcpy(host.data() + L.ln1, base + off(b + 0), ILL_H * 4);
     memcpy(host.data() + L.ln2, base + off(b + 6), ILL_H * 4);
@@ -301,7 +307,10 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
 
   if (hipSetDevice(0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "no HIP device"));
   int maxb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, 0) != hipSuccess || maxb < 1)
+  if (hipFuncSetAttribute((const void*)ill_pass_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, ILL_STAGE_BYTES) != hipSuccess ||
+      hipFuncSetAttribute((const void*)ill_pass_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, ILL_STAGE_BYTES) != hipSuccess)
+    return cleanup(fail(ILL_E_HIP, "cannot raise the pass kernel's LDS limit to %d B", ILL_STAGE_BYTES));
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, ILL_STAGE_BYTES) != hipSuccess || maxb < 1)
     return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d)", maxb));
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipGetDeviceProperties failed"));
@@ -335,12 +344,11 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     return hipMemset(*p, 0, bytes) == hipSuccess;
   };
   const size_t kvb = (size_t)layers * ILL_NKV * e->maxctx * 64 * 2;
-  const size_t tw = (size_t)16 * ILL_H * 8;
+  e->acc_bytes = (size_t)2 * layers * 2 * 16 * ILL_H * 8;
   bool ok = dalloc((void**)&e->dlayers, sizeof(IllLayerW) * layers) && dalloc((void**)&e->st, 64) && dalloc((void**)&e->ctl, 64) &&
             dalloc((void**)&e->ptoks, 64) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
-            dalloc((void**)&e->xa, tw) && dalloc((void**)&e->xb, tw) && dalloc((void**)&e->q, tw) && dalloc((void**)&e->attn, tw) &&
-            dalloc((void**)&e->kvn, (size_t)16 * 2 * 2 * 32 * 8) && dalloc((void**)&e->part, (size_t)ILL_NGU * tw) &&
+            dalloc((void**)&e->acc, e->acc_bytes) &&
             dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
             dalloc((void**)&e->out_dev, (size_t)max_steps * 4);
   if (!ok) return cleanup(fail(ILL_E_HIP, "device buffer allocation failed"));
@@ -385,12 +393,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.rope = e->rope;
   a.kc = e->kc;
   a.vt = e->vt;
-  a.xa = e->xa;
-  a.xb = e->xb;
-  a.q = e->q;
-  a.kvn = e->kvn;
-  a.attn = e->attn;
-  a.part = e->part;
+  a.acc = e->acc;
   a.lmp = e->lmp;
   a.logits = e->logits;
   a.out_dev = e->out_dev;
@@ -407,8 +410,8 @@ int ill_destroy(ill_engine* e) {
   if (e->stream) hipStreamSynchronize(e->stream);
   if (e->gexec) hipGraphExecDestroy(e->gexec);
   if (e->graph) hipGraphDestroy(e->graph);
-  void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->xa, e->xb,
-                  e->q, e->kvn, e->attn, e->part, e->lmp, e->logits, e->out_dev};
+  void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
+                  e->lmp, e->logits, e->out_dev, e->args.trace};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);
@@ -534,7 +537,7 @@ int ill_capture_steps(ill_engine* e, int nsteps) {
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   for (int i = 0; i < nsteps; i++)
-    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = nsteps;

@@ -3,22 +3,35 @@
 //
 // The reference encodes the same work as 24 x 5 + 2 dependent dispatches
 // (Sources/Engine/Engine.swift:245-292, :605-609). Here 256 workgroups stay resident and
-// each takes one role per layer; roles hand data to each other through tagged words
-// (ill_device.h), so a consumer waits only for the words it needs:
+// each layer is two dependent stages:
 //
-//   QKV  (36 WGs)  x_l -> RMSNorm -> 32-row rotary block of QKV -> bias, RoPE, q / K / V
-//   ATT  (28 WGs)  (kv group, row): MFMA flash attention over 64-position chunks
-//   O    (56 WGs)  attention output -> 16-row tile of O -> + residual -> x'
-//   GUD  (76 WGs)  x' -> RMSNorm -> 64 hidden units of gate/up -> SiLU*up -> down partial
-//   RED  (56 WGs)  x' + sum of the 76 down partials (fixed order) -> x_{l+1}
-//   LMH  (all)     final RMSNorm -> tied lm_head tiles -> per-WG argmax partials
-//   COMMIT (WG 0)  argmax (ties -> lowest id), token record, state advance, tree accept,
-//                  KV compaction, epoch advance
+//   ATT[h]   (14 WGs, one per query head h, KV group g = h / 7)
+//            x_l -> RMSNorm -> rows of q_h, k_g, v_g (+ bias, RoPE) -> MFMA flash attention
+//            over 64-position chunks -> O projection restricted to head h's 64 columns
+//            (split K) -> adds its 896-row partial into the residual accumulator XA[l]
+//   GUD[ub]  (76 WGs, 64 hidden units each)
+//            x'_l = XA[l] -> RMSNorm -> gate/up rows -> SiLU * up -> down projection
+//            restricted to the 64 units (split K) -> adds into XB[l] (= x_{l+1})
+//   LMH      (all WGs) final RMSNorm -> tied lm_head tiles -> per-WG argmax partials
+//   COMMIT   (WG 0) argmax (ties -> lowest id), token record, state advance, tree accept,
+//            KV compaction, epoch advance
 //
-// Every role issues its weight loads for a layer before it waits for that layer's input,
-// so HBM streaming overlaps the dependency chain.
+// Residual accumulators hold 64-bit fixed point with the number of contributions in the
+// top byte: each contributor adds (1 << 56) + (rint(v * 2^24) + 2^48). Integer addition
+// makes the sum independent of arrival order (deterministic, and the same for any T), and
+// a consumer knows an element is complete when its count reaches the number of
+// contributors. ATT[0] and GUD[0] fold the incoming residual into their contribution.
+// Accumulators alternate between two banks by pass; the idle bank is zeroed during the
+// lm_head phase.
+//
+// Every role issues its weight loads for the next layer as soon as it has finished the
+// current one, so HBM streaming overlaps the dependency chain.
 #pragma once
 #include "ill_device.h"
+
+#define ILL_NATT 14          // ATT workgroups (one per query head)
+#define ILL_R_ATT0 0         // ATT WGs 0..13
+#define ILL_R_GUD0 16        // GUD WGs 16..91
 
 struct IllPassArgs {
   IllWeights W;
@@ -30,12 +43,7 @@ struct IllPassArgs {
   const float2* rope;      // [maxctx + 16][32] (cos, sin)
   uint16_t* kc;            // K cache [layer][kvh][maxctx][64] f16
   uint16_t* vt;            // V cache transposed per 64 slots [layer][kvh][maxctx/64][64 dims][64] f16
-  uint64_t* xa;            // [16][896] layer input
-  uint64_t* xb;            // [16][896] residual after attention
-  uint64_t* q;             // [16][896] rotated queries
-  uint64_t* kvn;           // [16][kvh 2][k/v 2][32] this pass's K/V rows: word d = f16 pair (d, d+32)
-  uint64_t* attn;          // [16][896]
-  uint64_t* part;          // [76][16][896] down partials
+  uint64_t* acc;           // residual accumulators [bank 2][layer][A/B][16][896]
   uint64_t* lmp;           // [256][16][2] lm_head argmax partials (value, index)
   float* logits;           // [16][V]
   int32_t* out_dev;        // [maxsteps]
@@ -45,70 +53,61 @@ struct IllPassArgs {
   int maxsteps;
 };
 
-// Trace slots per workgroup: 3 per layer (role start, input ready, output written) and
-// 3 for the lm_head / commit tail.
-#define ILL_TRACE_SLOTS (3 * ILL_MAXLAYERS + 6)
+// Trace slots per workgroup: 6 per layer (role start, input ready, three role-specific
+// intermediate points, done) and 6 for the lm_head / commit tail.
+#define ILL_TR_TAIL (6 * ILL_MAXLAYERS)
+#define ILL_TRACE_SLOTS (ILL_TR_TAIL + 6)
 __device__ __forceinline__ void trace_mark(const IllPassArgs& a, int slot) {
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * ILL_TRACE_SLOTS + slot] = wall_clock64();
 }
 
 struct PassHdr {
   uint32_t epoch;
-  int mode, nrows, pos, lmh0, lmhn, wlog, commit, done;
+  int mode, nrows, pos, lmh0, lmhn, wlog, commit, done, bank, zrows;
   int tok[16], depth[16], parent[16];
+  int prow[16][16];        // prow[t][d]: pass row on row t's path at depth d
 };
 
-struct AttLds {
-  v8h qa[2 * 2 * 64];            // [ks][hi/lo][lane]
-  float P[ILL_WAVES][8][64];     // per-wave softmax weights of one chunk
-  float cm[ILL_WAVES][8], cl[ILL_WAVES][8];
-  float co[ILL_WAVES][7][64];
-  int prow[16];
-};
+// ---- residual fixed point --------------------------------------------------------------
+#define FX_COUNT (1ull << 56)
+#define FX_BIAS (1ll << 48)
+#define FX_SCALE 16777216.0f        // 2^24
+#define FX_INV (1.0f / 16777216.0f)
 
-struct GudLds {
-  PrepLds prep;
-  float gu[8][16][16];           // [tile][row][unit]
-  uint4 ahi[4 * 16], alo[4 * 16];
-  float2 dsc[16];
-};
+__device__ __forceinline__ int64_t fx_of(float v) {
+  int64_t q = __float2ll_rn(v * FX_SCALE);
+  const int64_t lim = FX_BIAS - 1;
+  return q > lim ? lim : (q < -lim ? -lim : q);
+}
+__device__ __forceinline__ uint64_t fx_word(int64_t q) { return FX_COUNT + (uint64_t)(q + FX_BIAS); }
+// value of a completed accumulator word (count = n contributions)
+__device__ __forceinline__ int64_t fx_value(uint64_t w) {
+  const int64_t n = (int64_t)(w >> 56);
+  return (int64_t)(w & ((1ull << 56) - 1)) - n * FX_BIAS;
+}
+__device__ __forceinline__ int fx_count(uint64_t w) { return (int)(w >> 56); }
+__device__ __forceinline__ float fx_float(int64_t v) { return (float)v * FX_INV; }
+__device__ __forceinline__ void fx_add(uint64_t* p, uint64_t w) {
+  __hip_atomic_fetch_add((GAS unsigned long long*)p, (unsigned long long)w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-struct LmhLds {
-  PrepLds prep;
-  float bv[ILL_WAVES][16];
-  int bi[ILL_WAVES][16];
-};
-
-struct CommitLds {
-  float v[256];
-  int i[256];
-  int g[16];
-  int path[16];
-  int npath, pos0;
-};
-
-union PassLds {
-  PrepLds prep;
-  AttLds att;
-  GudLds gud;
-  LmhLds lmh;
-  CommitLds cm;
-};
-
-__device__ __forceinline__ uint32_t tagof(uint32_t epoch, int layer) { return epoch * 32u + (uint32_t)layer + 1u; }
+__device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int l, int kind, int t) {
+  return a.acc + ((((size_t)bank * a.W.layers + l) * 2 + kind) * 16 + t) * ILL_H;
+}
 
 // ---- activation sources for prep896 --------------------------------------------------
-struct SrcTagged {
-  const uint64_t* base;
-  uint32_t tag;
+// Residual accumulator row (complete when every word has `expect` contributions).
+struct SrcAcc {
+  const uint64_t* base;   // row 0; rows are ILL_H apart
+  int expect;
   __device__ __forceinline__ bool load(int t, int c0, float* v) const {
-    const uint64_t* p = base + t * ILL_H + c0;
+    const uint64_t* p = base + (size_t)t * ILL_H + c0;
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const uint64_t w = aload64(p + i);
-      ok &= wok(w, tag);
-      v[i] = wval(w);
+      ok &= fx_count(w) == expect;
+      v[i] = fx_float(fx_value(w));
     }
     return ok;
   }
@@ -120,14 +119,13 @@ __device__ __forceinline__ void embed16(const IllWeights& W, int tok, int c0, fl
   const int rt = tok >> 4, n = tok & 15;
   const int cb = c0 >> 7, gi = (c0 >> 6) & 1, kg = (c0 >> 4) & 3;
   const uint8_t* blk = W.wemb + ((size_t)rt * ILL_KST + cb) * 1024 + (kg * 16 + n) * 16 + gi * 8;
-  const uint2 b = *(const uint2*)blk;
-  const uint32_t sm = W.semb[((size_t)rt * ILL_KST + cb) * 32 + n * 2 + gi];
+  const uint2 b = gld((const uint2*)blk);
+  const uint32_t sm = gld(W.semb + ((size_t)rt * ILL_KST + cb) * 32 + n * 2 + gi);
   const float s = h2f(sm & 0xffff), m = h2f(sm >> 16);
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const uint32_t word = i < 8 ? b.x : b.y;
-    const int k = i & 7;
-    const uint32_t q = (word >> (4 * k)) & 0xF;
+    const uint32_t q = (word >> (4 * (i & 7))) & 0xF;
     v[i] = s * (float)q + m;
   }
 }
@@ -147,9 +145,9 @@ struct SrcEmbed {
   }
 };
 
-// RMSNorm (optional) + 16-bit fixed-point coding of rows 0..nrows-1 of a K = 896 input
-// into MFMA operands. Row t is handled by wave t % 8 with the same instruction sequence
-// for every T: lane (G, kg) = (lane / 4, lane % 4), lanes 56-63 idle.
+// RMSNorm + 16-bit fixed-point coding of rows 0..nrows-1 of a K = 896 input into MFMA
+// operands. Row t is handled by wave t % 8 with the same instruction sequence for every
+// T: lane (G, kg) = (lane / 4, lane % 4), lanes 56-63 idle.
 template <int T, class Src>
 __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds& P,
                                         IllCtl* ctl, int code) {
@@ -174,16 +172,14 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
 #pragma unroll
       for (int i = 0; i < 16; i++) v[i] = 0.f;
     }
-    if (gamma) {
-      float ss = 0.f;
+    float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; i++) ss = fmaf(v[i], v[i], ss);
-      ss = wsum64(ss);
-      const float scale = 1.0f / sqrtf(ss / (float)ILL_H + ILL_EPS);
-      if (act) {
+    for (int i = 0; i < 16; i++) ss = fmaf(v[i], v[i], ss);
+    ss = wsum64(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)ILL_H + ILL_EPS);
+    if (act) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = v[i] * scale * gamma[c0 + i];
-      }
+      for (int i = 0; i < 16; i++) v[i] = v[i] * scale * gld(gamma + c0 + i);
     }
     float mx = 0.f;
 #pragma unroll
@@ -204,73 +200,112 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   return !wg_failed(ctl);
 }
 
-// ---------------------------------------------------------------------------------------
-template <int T>
-__device__ bool role_qkv(const IllPassArgs& a, const PassHdr& H, PassLds& S, int l, int b) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const IllLayerW& L = a.L[l];
-  Q4Tile t0, t1;
-  if (w == 0) {
-    q4_load(t0, L.wqkv + (size_t)(2 * b) * ILL_KST * 1024, L.sqkv + (2 * b) * ILL_KST * 32, lane);
-    q4_load(t1, L.wqkv + (size_t)(2 * b + 1) * ILL_KST * 1024, L.sqkv + (2 * b + 1) * ILL_KST * 32, lane);
-  }
-  bool ok;
-  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, H.nrows, S.prep, a.ctl, 100 + l);
-  else ok = prep896<T>(SrcTagged{a.xa, tagof(H.epoch, l)}, L.ln1, H.nrows, S.prep, a.ctl, 100 + l);
-  if (!ok) return false;
-  trace_mark(a, 3 * l + 1);
-  if (w == 0) {
-    float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
-    q4_tile896<T>(t0, S.prep, lane, acc0);
-    q4_tile896<T>(t1, S.prep, lane, acc1);
-    const int kg = lane >> 4, n = lane & 15;
-    const int head = b >> 1, d = (b & 1) * 16 + n;
-    const float bias0 = L.bqkv[32 * b + n], bias1 = L.bqkv[32 * b + 16 + n];
-    const uint32_t tag = tagof(H.epoch, l);
-    constexpr int RPL = T >= 4 ? 4 : T;
-#pragma unroll
-    for (int j = 0; j < RPL; j++) {
-      const int t = 4 * kg + j;
-      if (t >= H.nrows) continue;
-      float x0 = acc0[j] + bias0, x1 = acc1[j] + bias1;
-      const int slot = H.pos + t;
-      if (head < ILL_NH + ILL_NKV) {
-        const float2 cs = a.rope[(H.pos + H.depth[t]) * 32 + d];
-        const float r0 = x0 * cs.x - x1 * cs.y;
-        const float r1 = x1 * cs.x + x0 * cs.y;
-        x0 = r0;
-        x1 = r1;
-      }
-      if (head < ILL_NH) {
-        astore64(a.q + t * ILL_H + head * 64 + d, mkw(x0, tag));
-        astore64(a.q + t * ILL_H + head * 64 + d + 32, mkw(x1, tag));
-      } else {
-        const int kv = head < ILL_NH + ILL_NKV ? 0 : 1;
-        const int kh = head - ILL_NH - kv * ILL_NKV;
-        const uint32_t h0 = f2h(x0), h1 = f2h(x1);
-        if (kv == 0) {
-          uint16_t* kr = a.kc + (((size_t)l * ILL_NKV + kh) * a.maxctx + slot) * 64;
-          kr[d] = (uint16_t)h0;
-          kr[d + 32] = (uint16_t)h1;
-        } else {
-          uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + kh) * (a.maxctx / 64) + slot / 64) * 64 * 64;
-          vb[d * 64 + (slot & 63)] = (uint16_t)h0;
-          vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)h1;
-        }
-        astore64(a.kvn + ((t * 2 + kh) * 2 + kv) * 32 + d, mkwu(h0 | (h1 << 16), tag));
-      }
-    }
-  }
-  __syncthreads();
-  return true;
+__device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
+
+// One row (64 values, one per lane) -> 16-bit coding as a K = 64 MFMA operand:
+// lane (kg, m = row) of the operand holds units 16 kg + q4perm(p).
+__device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* alo, float2* dsc) {
+  const int lane = threadIdx.x & 63;
+  const float mx = wmax_xor(fabsf(h), 1, 32);
+  const float d = mx / ILL_QMAX;
+  const int qv = d > 0.f ? (int)rintf(h / d) : 0;
+  const int sq = isum_xor(qv, 1, 32);
+  const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
+  const int gi = lane >> 4, p = q4perm_inv(lane & 15);
+  ((uint8_t*)&ahi[gi * 16 + t])[p] = (uint8_t)(hi & 0xff);
+  ((uint8_t*)&alo[gi * 16 + t])[p] = (uint8_t)(lo & 0xff);
+  if (lane == 0) dsc[t] = make_float2(d, d * (float)sq);
+}
+
+// ---- weight staging in LDS ----------------------------------------------------------------
+// Each role copies the next layer's weights HBM -> LDS (global_load_lds) as soon as it has
+// finished the current layer, per wave, into a dynamic-LDS stage of ILL_STAGE_BYTES:
+//   ATT  QKV: wave w < 6 at w * 16128: [tile 2b: 7 KiB][tile 2b+1: 7 KiB][scales 2 x 896 B]
+//        O:   wave w at w * 4032: [7 row tiles x 512 B][7 x 64 B scales] (loaded after QKV)
+//   GUD  GU:  wave w at w * 8064: [7 KiB][896 B]
+//        down: wave w at 64512 + w * 4032: [7 x 512 B][7 x 64 B]
+#define ILL_STAGE_BYTES 96768
+#define ILL_ST_QKV 16128
+#define ILL_ST_SPLIT 4032
+#define ILL_ST_GU 8064
+#define ILL_ST_DOWN0 64512
+
+// Split-K partial of a 896-row projection over one 64-column group: the wave's 7 row
+// tiles (rows 112 w .. +112) of a [group][row tile] 512-byte block layout, staged in LDS.
+__device__ __forceinline__ void split_stage(const uint8_t* wg, const uint32_t* sg, int w, int lane, uint8_t* dst) {
+  wave_copy_to_lds(wg + (size_t)(7 * w) * 512, dst, 7 * 512, lane);
+  wave_copy_to_lds((const uint8_t*)(sg + 7 * w * 16), dst + 7 * 512, 7 * 64, lane);
 }
 
 // ---------------------------------------------------------------------------------------
-// Attention for one (kv group g, row t): virtual positions 0 .. L-1 with L = pos + depth + 1;
-// position p < pos is cache slot p, p >= pos is pass row prow[p - pos] (this pass's K/V).
-// Chunks of 64 positions go to wave (chunk % 8); each chunk is one MFMA flash-attention
-// step; chunk results combine in chunk order per wave, then over waves 0..7. Nothing here
-// depends on T, so a tree row and the same token decoded alone give identical bits.
+template <int T>
+struct AttLds {
+  union {
+    PrepLds prep;
+    float P[ILL_WAVES][T][64];
+    struct {
+      float cm[ILL_WAVES][T], cl[ILL_WAVES][T];
+      float co[ILL_WAVES][T][64];
+    } c;
+  } u;
+  float q[T][64];
+  uint16_t k[T][64];
+  uint16_t v[T][64];
+  float o[T][64];
+  uint4 ahi[4 * 16], alo[4 * 16];
+  float2 dsc[16];
+};
+
+template <int T>
+struct GudLds {
+  PrepLds prep;
+  float gu[8][T][16];
+  uint4 ahi[4 * 16], alo[4 * 16];
+  float2 dsc[16];
+};
+
+struct LmhLds {
+  PrepLds prep;
+  float bv[ILL_WAVES][16];
+  int bi[ILL_WAVES][16];
+};
+
+struct CommitLds {
+  float v[256];
+  int i[256];
+  int g[16];
+  int path[16];
+  int npath, pos0;
+};
+
+template <int T>
+union PassLds {
+  AttLds<T> att;
+  GudLds<T> gud;
+  LmhLds lmh;
+  CommitLds cm;
+};
+
+// ATT workgroup weights: waves 0-5 one 32-row QKV block each (q_h halves, k_g halves,
+// v_g halves); every wave 7 row tiles of O's head-h columns.
+__device__ __forceinline__ int att_block(int h, int w) {
+  const int g = h / 7;
+  return w < 2 ? 2 * h + w : (w < 4 ? 28 + 2 * g + (w - 2) : 32 + 2 * g + (w - 4));
+}
+
+__device__ __forceinline__ void att_stage_qkv(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
+  if (w < 6) {
+    const int b = att_block(h, w);
+    uint8_t* d = stage + w * ILL_ST_QKV;
+    wave_copy_to_lds(L.wqkv + (size_t)(2 * b) * ILL_KST * 1024, d, 2 * ILL_KST * 1024, lane);
+    wave_copy_to_lds((const uint8_t*)(L.sqkv + (2 * b) * ILL_KST * 32), d + 2 * ILL_KST * 1024, 2 * ILL_KST * 128, lane);
+  }
+}
+
+__device__ __forceinline__ void att_stage_o(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
+  split_stage(L.wo + (size_t)h * ILL_NOT * 512, L.so + h * ILL_NOT * 16, w, lane, stage + w * ILL_ST_SPLIT);
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -279,70 +314,233 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ v8h u4_to_v8h(uint4 u) {
   v8h r;
-  const uint32_t a[4] = {u.x, u.y, u.z, u.w};
+  const uint32_t x[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint32_t x = a[i];
-    r[2 * i] = __builtin_bit_cast(_Float16, (unsigned short)(x & 0xffff));
-    r[2 * i + 1] = __builtin_bit_cast(_Float16, (unsigned short)(x >> 16));
+    r[2 * i] = __builtin_bit_cast(_Float16, (unsigned short)(x[i] & 0xffff));
+    r[2 * i + 1] = __builtin_bit_cast(_Float16, (unsigned short)(x[i] >> 16));
   }
   return r;
 }
-
 __device__ __forceinline__ _Float16 hbits(uint32_t b) { return __builtin_bit_cast(_Float16, (unsigned short)(b & 0xffff)); }
 
+// One 64-position attention chunk for the rows selected by `rmask` (bit t = row t).
+// Positions p < pos come from the caches; positions pos <= p < L_t (this pass's rows on row
+// t's path) come from LDS. `shared`: every selected row maps positions identically (the
+// chunk lies below pos), so one MFMA serves all rows; otherwise `rmask` holds one row.
+// Lane layout of results: lane (g4, n) holds rows 4 g4 + j.
 template <int T>
-__device__ bool role_att(const IllPassArgs& a, const PassHdr& H, PassLds& S, int l, int g, int t) {
-  AttLds& A = S.att;
+__device__ __forceinline__ void att_chunk(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int g, int c,
+                                          uint32_t rmask, bool shared, const v8h qa[2][2],
+                                          float M[4], float Lw[4], float O[4][4]) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int depth = H.depth[t];
+  const int kg = lane >> 4, n = lane & 15;
   const int pos = H.pos;
-  const int Lt = pos + depth + 1;
-  const uint32_t tag = tagof(H.epoch, l);
-  if (threadIdx.x == 0) {
-    int r = t;
-    for (int d = depth; d >= 0; --d) {
-      A.prow[d] = r;
-      r = r > 0 ? H.parent[r] : 0;
+  const int t1 = shared ? 0 : __builtin_ctz(rmask);   // the single row of a per-row chunk
+  const int Lt = shared ? pos : pos + H.depth[t1] + 1;
+  const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
+  const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
+  // query operands restricted to the selected rows
+  v8h qh[2], ql[2];
+  const bool rowsel = (rmask >> n) & 1;
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      qh[ks][i] = rowsel ? qa[ks][0][i] : (_Float16)0.f;
+      ql[ks][i] = rowsel ? qa[ks][1][i] : (_Float16)0.f;
+    }
+  }
+  float sc[4][4];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const int vp = 64 * c + 16 * b + n;
+    v8h k0, k1;
+    if (vp < pos) {
+      const uint4* kr = (const uint4*)(kbase + (size_t)vp * 64);
+      k0 = u4_to_v8h(gld(kr + kg));
+      k1 = u4_to_v8h(gld(kr + 4 + kg));
+    } else if (vp < Lt) {
+      const uint16_t* kr = A.k[H.prow[t1][vp - pos]];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        k0[i] = hbits(kr[8 * kg + i]);
+        k1[i] = hbits(kr[32 + 8 * kg + i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) { k0[i] = (_Float16)0.f; k1[i] = (_Float16)0.f; }
+    }
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[0], k0, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[0], k0, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[1], k1, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[1], k1, s, 0, 0, 0);
+    const bool valid = shared || vp < Lt;
+#pragma unroll
+    for (int j = 0; j < 4; j++) sc[b][j] = valid ? s[j] : -INFINITY;
+  }
+  float mx[4], ls[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float m = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
+    mx[j] = wmax_xor(m, 1, 8);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    float s = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      sc[b][j] = expf(sc[b][j] - mx[j]);
+      s += sc[b][j];
+    }
+    ls[j] = wsum_xor(s, 1, 8);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int t = 4 * kg + j;
+    if (t < T && ((rmask >> t) & 1)) {
+#pragma unroll
+      for (int b = 0; b < 4; b++) A.u.P[w][t][16 * b + n] = sc[b][j];
+    }
+  }
+  wave_lds_sync();
+  v8h ph[2], pl[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float p = (n < T && rowsel) ? A.u.P[w][n < T ? n : 0][32 * ks + 8 * kg + i] : 0.f;
+      const _Float16 hi = (_Float16)p;
+      ph[ks][i] = hi;
+      pl[ks][i] = (_Float16)(p - (float)hi);
+    }
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++) {
+    const int dim = 16 * nb + n;
+    v8h vv[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const int p0 = 64 * c + 32 * ks + 8 * kg;
+      if (p0 + 7 < pos) {
+        vv[ks] = u4_to_v8h(gld((const uint4*)(vbase + ((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg)));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int vp = p0 + i;
+          uint32_t bits = 0;
+          if (vp < pos) bits = gld(vbase + ((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg + i);
+          else if (vp < Lt) bits = A.v[H.prow[t1][vp - pos]][dim];
+          vv[ks][i] = hbits(bits);
+        }
+      }
+    }
+    v4f o = {0.f, 0.f, 0.f, 0.f};
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], o, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int t = 4 * kg + j;
+      if (t < T && ((rmask >> t) & 1)) {
+        const float mn = fmaxf(M[j], mx[j]);
+        const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
+        O[nb][j] = O[nb][j] * sa + o[j] * sb;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int t = 4 * kg + j;
+    if (t < T && ((rmask >> t) & 1)) {
+      const float mn = fmaxf(M[j], mx[j]);
+      const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
+      Lw[j] = Lw[j] * sa + ls[j] * sb;
+      M[j] = mn;
+    }
+  }
+}
+
+template <int T>
+__device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int h, uint8_t* stage) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int g = h / 7;
+  const IllLayerW& L = a.L[l];
+  constexpr int RPL = T >= 4 ? 4 : T;
+  const int nrows = H.nrows;
+  // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
+  bool ok;
+  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
+  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_GUD_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
+  if (!ok) return false;
+  trace_mark(a, 6 * l + 1);
+  // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
+  if (w < 6) {
+    const int b = att_block(h, w);
+    float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
+    wait_vm();   // this wave's staged QKV block
+    const uint8_t* st = stage + w * ILL_ST_QKV;
+    q4_tile896_lds<T>(st, st + 2 * ILL_KST * 1024, A.u.prep, lane, acc0);
+    q4_tile896_lds<T>(st + ILL_KST * 1024, st + 2 * ILL_KST * 1024 + ILL_KST * 128, A.u.prep, lane, acc1);
+    const int head = b >> 1, d = (b & 1) * 16 + n;
+    const float bias0 = gld(L.bqkv + 32 * b + n), bias1 = gld(L.bqkv + 32 * b + 16 + n);
+    const bool writer = (h % 7) == 0;   // one query head per group writes the K/V cache
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int t = 4 * kg + j;
+      if (t >= nrows) continue;
+      float x0 = acc0[j] + bias0, x1 = acc1[j] + bias1;
+      if (head < ILL_NH + ILL_NKV) {
+        const float2 cs = gld(a.rope + (H.pos + H.depth[t]) * 32 + d);
+        const float r0 = x0 * cs.x - x1 * cs.y;
+        const float r1 = x1 * cs.x + x0 * cs.y;
+        x0 = r0;
+        x1 = r1;
+      }
+      const int slot = H.pos + t;
+      if (head < ILL_NH) {
+        A.q[t][d] = x0;
+        A.q[t][d + 32] = x1;
+      } else if (head < ILL_NH + ILL_NKV) {
+        const uint32_t h0 = f2h(x0), h1 = f2h(x1);
+        A.k[t][d] = (uint16_t)h0;
+        A.k[t][d + 32] = (uint16_t)h1;
+        if (writer) {
+          uint16_t* kr = a.kc + (((size_t)l * ILL_NKV + g) * a.maxctx + slot) * 64;
+          gst(kr + d, (uint16_t)h0);
+          gst(kr + d + 32, (uint16_t)h1);
+        }
+      } else {
+        const uint32_t h0 = f2h(x0), h1 = f2h(x1);
+        A.v[t][d] = (uint16_t)h0;
+        A.v[t][d + 32] = (uint16_t)h1;
+        if (writer) {
+          uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + slot / 64) * 64 * 64;
+          gst(vb + d * 64 + (slot & 63), (uint16_t)h0);
+          gst(vb + (d + 32) * 64 + (slot & 63), (uint16_t)h1);
+        }
+      }
     }
   }
   __syncthreads();
-  // wait for this row's queries and the K/V of every row on its path
-  const int nkv = (depth + 1) * 64;
-  const bool ok = wg_wait([&]() {
-    bool r = true;
-    const int i = threadIdx.x;
-    if (i < 448) r &= wok(aload64(a.q + t * ILL_H + 7 * g * 64 + i), tag);
-    for (int j = i; j < nkv; j += ILL_WG_THREADS) {
-      const int row = A.prow[j >> 6], k = j & 63;
-      r &= wok(aload64(a.kvn + ((row * 2 + g) * 2 + (k >> 5)) * 32 + (k & 31)), tag);
-    }
-    return r;
-  }, a.ctl, 200 + l);
-  if (!ok) return false;
-  trace_mark(a, 3 * l + 1);
-  // query operands: q * 0.125 split into f16 hi + lo; lane (kg, m = head), dims 32 ks + 8 kg + i
-  {
-    _Float16* qa = (_Float16*)A.qa;
-    for (int i = threadIdx.x; i < 2 * 2 * 64 * 8; i += ILL_WG_THREADS) qa[i] = (_Float16)0.f;
-    __syncthreads();
-    if (threadIdx.x < 448) {
-      const int h = threadIdx.x >> 6, dim = threadIdx.x & 63;
-      const float v = wval(aload64(a.q + t * ILL_H + (7 * g + h) * 64 + dim)) * 0.125f;
+  att_stage_o(L, h, w, lane, stage);   // O weights stream in while attention runs
+  trace_mark(a, 6 * l + 2);
+  // ---- attention for head h over T rows
+  v8h qa[2][2];   // [ks][hi/lo], lane (kg, m = row), dims 32 ks + 8 kg + i, q * 0.125
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float v = (n < T && n < nrows) ? A.q[n < T ? n : 0][32 * ks + 8 * kg + i] * 0.125f : 0.f;
       const _Float16 hi = (_Float16)v;
-      const _Float16 lo = (_Float16)(v - (float)hi);
-      const int ks = dim >> 5, kg = (dim >> 3) & 3, i = dim & 7;
-      qa[((ks * 2 + 0) * 64 + kg * 16 + h) * 8 + i] = hi;
-      qa[((ks * 2 + 1) * 64 + kg * 16 + h) * 8 + i] = lo;
+      qa[ks][0][i] = hi;
+      qa[ks][1][i] = (_Float16)(v - (float)hi);
     }
-    __syncthreads();
   }
-  const int kg = lane >> 4, n = lane & 15;
-  const v8h qh0 = A.qa[(0 * 2 + 0) * 64 + lane], ql0 = A.qa[(0 * 2 + 1) * 64 + lane];
-  const v8h qh1 = A.qa[(1 * 2 + 0) * 64 + lane], ql1 = A.qa[(1 * 2 + 1) * 64 + lane];
-  const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
-  const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
-  const uint64_t* kvk = a.kvn + (size_t)g * 2 * 32;   // + row * 128 words
   float M[4], Lw[4], O[4][4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -351,222 +549,121 @@ __device__ bool role_att(const IllPassArgs& a, const PassHdr& H, PassLds& S, int
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
-  const int nch = (Lt + 63) >> 6;
+  int maxL = 0;
+  for (int t = 0; t < nrows; t++) maxL = max(maxL, H.pos + H.depth[t] + 1);
+  const int nch = (maxL + 63) >> 6;
+  const uint32_t allrows = (nrows >= 32) ? 0xffffffffu : ((1u << nrows) - 1u);
   for (int c = w; c < nch; c += ILL_WAVES) {
-    float sc[4][4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const int vp = 64 * c + 16 * b + n;
-      v8h k0, k1;
-      if (vp < pos) {
-        const uint4* kr = (const uint4*)(kbase + (size_t)vp * 64);
-        k0 = u4_to_v8h(kr[kg]);
-        k1 = u4_to_v8h(kr[4 + kg]);
-      } else if (vp < Lt) {
-        const uint64_t* kw = kvk + (size_t)A.prow[vp - pos] * 128 + 8 * kg;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const uint32_t x = (uint32_t)aload64(kw + i);
-          k0[i] = hbits(x);
-          k1[i] = hbits(x >> 16);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) { k0[i] = (_Float16)0.f; k1[i] = (_Float16)0.f; }
-      }
-      v4f s = {0.f, 0.f, 0.f, 0.f};
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh0, k0, s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql0, k0, s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh1, k1, s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql1, k1, s, 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 4; j++) sc[b][j] = vp < Lt ? s[j] : -INFINITY;
-    }
-    float mx[4], ls[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float m = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
-      mx[j] = wmax_xor(m, 1, 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float s = 0.f;
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        sc[b][j] = expf(sc[b][j] - mx[j]);
-        s += sc[b][j];
-      }
-      ls[j] = wsum_xor(s, 1, 8);
-    }
-    // P (heads < 8) to LDS, then PV operands: lane (kg, m = head), positions 32 ks + 8 kg + i
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int head = 4 * kg + j;
-      if (head < 8) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) A.P[w][head][16 * b + n] = sc[b][j];
-      }
-    }
-    wave_lds_sync();
-    v8h ph[2], pl[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float p = n < 7 ? A.P[w][n][32 * ks + 8 * kg + i] : 0.f;
-        const _Float16 hi = (_Float16)p;
-        ph[ks][i] = hi;
-        pl[ks][i] = (_Float16)(p - (float)hi);
-      }
-    }
-    wave_lds_sync();
-#pragma unroll
-    for (int nb = 0; nb < 4; nb++) {
-      const int dim = 16 * nb + n;
-      v8h vv[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int p0 = 64 * c + 32 * ks + 8 * kg;
-        if (p0 + 7 < pos) {
-          const uint4 u = *(const uint4*)(vbase + ((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg);
-          vv[ks] = u4_to_v8h(u);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; i++) {
-            const int vp = p0 + i;
-            uint32_t bits = 0;
-            if (vp < pos) bits = vbase[((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg + i];
-            else if (vp < Lt) {
-              const uint32_t x = (uint32_t)aload64(kvk + (size_t)A.prow[vp - pos] * 128 + 32 + (dim & 31));
-              bits = dim < 32 ? (x & 0xffff) : (x >> 16);
-            }
-            vv[ks][i] = hbits(bits);
-          }
-        }
-      }
-      v4f o = {0.f, 0.f, 0.f, 0.f};
-      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], o, 0, 0, 0);
-      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], o, 0, 0, 0);
-      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], o, 0, 0, 0);
-      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], o, 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float mn = fmaxf(M[j], mx[j]);
-        const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
-        O[nb][j] = O[nb][j] * sa + o[j] * sb;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float mn = fmaxf(M[j], mx[j]);
-      const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
-      Lw[j] = Lw[j] * sa + ls[j] * sb;
-      M[j] = mn;
+    if (64 * c + 63 < H.pos) {
+      att_chunk<T>(a, H, A, l, g, c, allrows, true, qa, M, Lw, O);
+    } else {
+      for (int t = 0; t < nrows; t++)
+        if (H.pos + H.depth[t] + 1 > 64 * c) att_chunk<T>(a, H, A, l, g, c, 1u << t, false, qa, M, Lw, O);
     }
   }
-  // combine waves 0..7 in order
+  __syncthreads();   // LDS: P region becomes the combine region
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const int head = 4 * kg + j;
-    if (head < 7) {
+    const int t = 4 * kg + j;
+    if (t < T) {
       if (n == 0) {
-        A.cm[w][head] = M[j];
-        A.cl[w][head] = Lw[j];
+        A.u.c.cm[w][t] = M[j];
+        A.u.c.cl[w][t] = Lw[j];
       }
 #pragma unroll
-      for (int nb = 0; nb < 4; nb++) A.co[w][head][16 * nb + n] = O[nb][j];
+      for (int nb = 0; nb < 4; nb++) A.u.c.co[w][t][16 * nb + n] = O[nb][j];
     }
   }
   __syncthreads();
-  if (threadIdx.x < 448) {
-    const int h = threadIdx.x >> 6, dim = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < nrows * 64; i += ILL_WG_THREADS) {
+    const int t = i >> 6, dim = i & 63;
     float m = -INFINITY, s = 0.f, o = 0.f;
     for (int ww = 0; ww < ILL_WAVES; ww++) {
-      const float mw = A.cm[ww][h];
+      const float mw = A.u.c.cm[ww][t];
       if (mw == -INFINITY) continue;
       const float mn = fmaxf(m, mw);
       const float sa = expf(m - mn), sb = expf(mw - mn);
-      s = s * sa + A.cl[ww][h] * sb;
-      o = o * sa + A.co[ww][h][dim] * sb;
+      s = s * sa + A.u.c.cl[ww][t] * sb;
+      o = o * sa + A.u.c.co[ww][t][dim] * sb;
       m = mn;
     }
-    astore64(a.attn + t * ILL_H + (7 * g + h) * 64 + dim, mkw(o / s, tag));
+    A.o[t][dim] = o / s;
   }
   __syncthreads();
+  trace_mark(a, 6 * l + 3);
+  // ---- O projection restricted to head h's columns (one quant group): rows t by wave t % 8
+  for (int t = w; t < T; t += ILL_WAVES) {
+    if (t < nrows) quant_row64(A.o[t][lane], t, A.ahi, A.alo, A.dsc);
+    else if (lane < 4) {
+      A.ahi[lane * 16 + t] = make_uint4(0, 0, 0, 0);
+      A.alo[lane * 16 + t] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
+  if (n < T) {
+    const uint4 x = A.ahi[kg * 16 + n], y = A.alo[kg * 16 + n];
+    ah = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+    al = (v4i){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
+  }
+  const v4i z = {0, 0, 0, 0};
+  wait_vm();   // this wave's staged O tiles
+  const uint8_t* so = stage + w * ILL_ST_SPLIT;
+#pragma unroll
+  for (int k = 0; k < 7; k++) {
+    const int rt = 7 * w + k, row = 16 * rt + n;
+    const uint2 wv = *(const uint2*)(so + k * 512 + lane * 8);
+    const uint32_t sm = *(const uint32_t*)(so + 7 * 512 + k * 64 + n * 4);
+    const v4i bq = q4_unpack(wv.x, wv.y);
+    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
+    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
+    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int t = 4 * kg + j;
+      if (t < nrows) {
+        const float2 dx = A.dsc[t];
+        const int Sv = (dh[j] << 8) + dl[j];
+        float y = 0.f;
+        y = fmaf(sw, dx.x * (float)Sv, y);
+        y = fmaf(mw, dx.y, y);
+        int64_t qv = fx_of(y);
+        if (h == 0) {
+          // fold in the incoming residual x_l (exactly, as an integer)
+          if (l == 0) qv += fx_of(embed1(a.W, H.tok[t], row));
+          else qv += fx_value(aload64(acc_ptr(a, H.bank, l - 1, 1, t) + row));
+        }
+        fx_add(acc_ptr(a, H.bank, l, 0, t) + row, fx_word(qv));
+      }
+    }
+  }
+  trace_mark(a, 6 * l + 4);
   return true;
 }
 
 // ---------------------------------------------------------------------------------------
-template <int T>
-__device__ bool role_o(const IllPassArgs& a, const PassHdr& H, PassLds& S, int l, int ot) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const IllLayerW& L = a.L[l];
-  Q4Tile tw;
-  if (w == 0) q4_load(tw, L.wo + (size_t)ot * ILL_KST * 1024, L.so + ot * ILL_KST * 32, lane);
-  const uint32_t tag = tagof(H.epoch, l);
-  if (!prep896<T>(SrcTagged{a.attn, tag}, nullptr, H.nrows, S.prep, a.ctl, 300 + l)) return false;
-  trace_mark(a, 3 * l + 1);
-  bool alive = true;
-  if (w == 0) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    q4_tile896<T>(tw, S.prep, lane, acc);
-    const int kg = lane >> 4, n = lane & 15, row = 16 * ot + n;
-    constexpr int RPL = T >= 4 ? 4 : T;
-    float xin[4];
-    alive = wave_wait([&]() {
-      bool r = true;
-#pragma unroll
-      for (int j = 0; j < RPL; j++) {
-        const int t = 4 * kg + j;
-        if (t < H.nrows) {
-          if (l == 0) xin[j] = embed1(a.W, H.tok[t], row);
-          else {
-            const uint64_t x = aload64(a.xa + t * ILL_H + row);
-            r &= wok(x, tag);
-            xin[j] = wval(x);
-          }
-        }
-      }
-      return r;
-    }, a.ctl, 350 + l);
-    if (alive) {
-#pragma unroll
-      for (int j = 0; j < RPL; j++) {
-        const int t = 4 * kg + j;
-        if (t < H.nrows) astore64(a.xb + t * ILL_H + row, mkw(xin[j] + acc[j], tag));
-      }
-    }
-  }
-  __syncthreads();
-  return !wg_failed(a.ctl);
+__device__ __forceinline__ void gud_stage(const IllLayerW& L, int ub, int w, int lane, uint8_t* stage) {
+  const int tile = ub * 8 + w;
+  uint8_t* d = stage + w * ILL_ST_GU;
+  wave_copy_to_lds(L.wgu + (size_t)tile * ILL_KST * 1024, d, ILL_KST * 1024, lane);
+  wave_copy_to_lds((const uint8_t*)(L.sgu + tile * ILL_KST * 32), d + ILL_KST * 1024, ILL_KST * 128, lane);
+  split_stage(L.wd + (size_t)ub * ILL_NOT * 512, L.sd + ub * ILL_NOT * 16, w, lane, stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT);
 }
 
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
-
 template <int T>
-__device__ bool role_gud(const IllPassArgs& a, const PassHdr& H, PassLds& S, int l, int ub) {
-  GudLds& G = S.gud;
+__device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H, GudLds<T>& G, int l, int ub, uint8_t* stage) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kg = lane >> 4, n = lane & 15;
   const IllLayerW& L = a.L[l];
-  Q4Tile tg;
-  q4_load(tg, L.wgu + (size_t)(ub * 8 + w) * ILL_KST * 1024, L.sgu + (ub * 8 + w) * ILL_KST * 32, lane);
-  uint2 dw[7];
-  uint32_t ds[7];
-#pragma unroll
-  for (int k = 0; k < 7; k++) {
-    const int rt = 7 * w + k;
-    dw[k] = *(const uint2*)(L.wd + ((size_t)ub * ILL_NOT + rt) * 512 + lane * 8);
-    ds[k] = L.sd[(ub * ILL_NOT + rt) * 16 + n];
-  }
-  const uint32_t tag = tagof(H.epoch, l);
-  if (!prep896<T>(SrcTagged{a.xb, tag}, L.ln2, H.nrows, G.prep, a.ctl, 400 + l)) return false;
-  trace_mark(a, 3 * l + 1);
+  const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
+  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_NATT}, L.ln2, nrows, G.prep, a.ctl, 400 + l)) return false;
+  trace_mark(a, 6 * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    q4_tile896<T>(tg, G.prep, lane, acc);
+    wait_vm();   // this wave's staged gate/up tile and down tiles
+    const uint8_t* sg = stage + w * ILL_ST_GU;
+    q4_tile896_lds<T>(sg, sg + ILL_KST * 1024, G.prep, lane, acc);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
@@ -574,32 +671,20 @@ __device__ bool role_gud(const IllPassArgs& a, const PassHdr& H, PassLds& S, int
     }
   }
   __syncthreads();
-  // SiLU(gate) * up for the block's 64 units, then 16-bit coding of each row (group = 64)
+  trace_mark(a, 6 * l + 2);
+  // SiLU(gate) * up for the block's 64 units; each row coded as one 64-wide group
   for (int t = w; t < T; t += ILL_WAVES) {
-    if (t >= H.nrows) {
-      if (lane < 4) {
-        G.ahi[lane * 16 + t] = make_uint4(0, 0, 0, 0);
-        G.alo[lane * 16 + t] = make_uint4(0, 0, 0, 0);
-      }
-      if (lane == 0) G.dsc[t] = make_float2(0.f, 0.f);
-      continue;
+    if (t < nrows) {
+      const int gi = lane >> 4, nn = lane & 15;
+      const float gv = G.gu[gi][t][nn], up = G.gu[4 + gi][t][nn];
+      quant_row64(gv / (1.0f + expf(-gv)) * up, t, G.ahi, G.alo, G.dsc);
+    } else if (lane < 4) {
+      G.ahi[lane * 16 + t] = make_uint4(0, 0, 0, 0);
+      G.alo[lane * 16 + t] = make_uint4(0, 0, 0, 0);
     }
-    const int u = lane, gi = u >> 4, nn = u & 15;
-    const float gv = G.gu[gi][t][nn], up = G.gu[4 + gi][t][nn];
-    const float h = gv / (1.0f + expf(-gv)) * up;
-    const float mx = wmax_xor(fabsf(h), 1, 32);
-    const float d = mx / ILL_QMAX;
-    const int qv = d > 0.f ? (int)rintf(h / d) : 0;
-    const int sq = isum_xor(qv, 1, 32);
-    const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
-    const int p = q4perm_inv(nn);
-    uint8_t* bh = (uint8_t*)&G.ahi[gi * 16 + t];
-    uint8_t* bl = (uint8_t*)&G.alo[gi * 16 + t];
-    bh[p] = (uint8_t)(hi & 0xff);
-    bl[p] = (uint8_t)(lo & 0xff);
-    if (lane == 0) G.dsc[t] = make_float2(d, d * (float)sq);
   }
   __syncthreads();
+  trace_mark(a, 6 * l + 3);
   v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
   if (n < T) {
     const uint4 x = G.ahi[kg * 16 + n], y = G.alo[kg * 16 + n];
@@ -607,51 +692,32 @@ __device__ bool role_gud(const IllPassArgs& a, const PassHdr& H, PassLds& S, int
     al = (v4i){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
   }
   const v4i z = {0, 0, 0, 0};
+  const uint8_t* sd = stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT;
 #pragma unroll
   for (int k = 0; k < 7; k++) {
-    const int rt = 7 * w + k;
-    const v4i b = q4_unpack(dw[k].x, dw[k].y);
+    const int rt = 7 * w + k, row = 16 * rt + n;
+    const uint2 wv = *(const uint2*)(sd + k * 512 + lane * 8);
+    const uint32_t sm = *(const uint32_t*)(sd + 7 * 512 + k * 64 + n * 4);
+    const v4i b = q4_unpack(wv.x, wv.y);
     const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
     const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-    const float sw = h2f(ds[k] & 0xffff), mw = h2f(ds[k] >> 16);
+    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
-      if (t < H.nrows) {
+      if (t < nrows) {
         const float2 dx = G.dsc[t];
         const int Sv = (dh[j] << 8) + dl[j];
         float y = 0.f;
         y = fmaf(sw, dx.x * (float)Sv, y);
         y = fmaf(mw, dx.y, y);
-        astore64(a.part + ((size_t)(ub * 16 + t)) * ILL_H + 16 * rt + n, mkw(y, tag));
+        int64_t qv = fx_of(y);
+        if (ub == 0) qv += fx_value(aload64(acc_ptr(a, H.bank, l, 0, t) + row));
+        fx_add(acc_ptr(a, H.bank, l, 1, t) + row, fx_word(qv));
       }
     }
   }
-  __syncthreads();
-  return true;
-}
-
-// ---------------------------------------------------------------------------------------
-template <int T>
-__device__ bool role_red(const IllPassArgs& a, const PassHdr& H, int l, int rt) {
-  const uint32_t tag = tagof(H.epoch, l);
-  const int i = threadIdx.x;
-  const int t = i >> 4, row = 16 * rt + (i & 15);
-  const bool act = t < H.nrows;
-  const bool ok = wg_wait([&]() {
-    if (!act) return true;
-    bool r = wok(aload64(a.xb + t * ILL_H + row), tag);
-    for (int ub = 0; ub < ILL_NGU; ub++) r &= wok(aload64(a.part + ((size_t)(ub * 16 + t)) * ILL_H + row), tag);
-    return r;
-  }, a.ctl, 500 + l);
-  if (!ok) return false;
-  trace_mark(a, 3 * l + 1);
-  if (act) {
-    float acc = 0.f;
-    for (int ub = 0; ub < ILL_NGU; ub++) acc += wval(aload64(a.part + ((size_t)(ub * 16 + t)) * ILL_H + row));
-    const float x = wval(aload64(a.xb + t * ILL_H + row)) + acc;
-    astore64(a.xa + t * ILL_H + row, mkw(x, tagof(H.epoch, l + 1)));
-  }
+  trace_mark(a, 6 * l + 4);
   return true;
 }
 
@@ -661,12 +727,11 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float ov, int oi) {
 }
 
 template <int T>
-__device__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
-  LmhLds& Lm = S.lmh;
+__device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, LmhLds& Lm) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int NL = a.W.layers;
-  const uint32_t tag = tagof(H.epoch, NL);
+  const uint32_t tag = tagof_lmh(H.epoch);
   const int V = a.W.vocab, ntiles = V >> 4;
   const int wg = blockIdx.x;
   float bv[4];
@@ -677,8 +742,8 @@ __device__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcTagged{a.xa, tag}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600)) return false;
-    trace_mark(a, 3 * ILL_MAXLAYERS + 1);
+    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_GUD_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600)) return false;
+    trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {
       const int nxt = tile + ILL_WG * ILL_WAVES;
@@ -691,7 +756,7 @@ __device__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
       for (int j = 0; j < RPL; j++) {
         const int t = 4 * kg + j;
         if (t >= H.lmh0 && t < H.lmh0 + H.lmhn) {
-          if (H.wlog) a.logits[(size_t)t * V + idx] = acc[j];
+          if (H.wlog) gst(a.logits + (size_t)t * V + idx, acc[j]);
           amax_merge(bv[j], bi[j], acc[j], idx);
         }
       }
@@ -699,7 +764,6 @@ __device__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
       tile = nxt;
     }
   }
-  // per-row best over the 16 lanes of each lane-group, then over waves
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     for (int o = 8; o >= 1; o >>= 1) {
@@ -725,16 +789,31 @@ __device__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
     astore64(a.lmp + (wg * 16 + t) * 2 + 0, mkw(v, tag));
     astore64(a.lmp + (wg * 16 + t) * 2 + 1, mkwu((uint32_t)id, tag));
   }
-  __syncthreads();
   return true;
 }
 
+// Zero this workgroup's share of the other accumulator bank (used by the previous pass,
+// next used by the following pass).
+__device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const PassHdr& H) {
+  if (H.zrows <= 0) return;
+  const int NL = a.W.layers;
+  const size_t per_row = ILL_H;
+  const int other = H.bank ^ 1;
+  const size_t nrow_total = (size_t)NL * 2 * H.zrows;   // (layer, kind, row) triples
+  const size_t total = nrow_total * per_row;
+  const size_t chunk = (total + ILL_WG - 1) / ILL_WG;
+  const size_t lo = (size_t)blockIdx.x * chunk, hi = min(total, lo + chunk);
+  for (size_t i = lo + threadIdx.x; i < hi; i += ILL_WG_THREADS) {
+    const size_t r = i / per_row, c = i % per_row;
+    const size_t lk = r / H.zrows, t = r % H.zrows;
+    gst(a.acc + ((((size_t)other * NL) * 2 + lk) * 16 + t) * ILL_H + c, (uint64_t)0);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
-__device__ void commit(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
-  CommitLds& C = S.cm;
-  const uint32_t tag = tagof(H.epoch, a.W.layers);
+__device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
+  const uint32_t tag = tagof_lmh(H.epoch);
   const int i = threadIdx.x;
-  // every workgroup's partials (this also proves every workgroup has read the pass header)
   const bool ok = wg_wait([&]() {
     bool r = true;
     if (i < ILL_WG)
@@ -742,7 +821,7 @@ __device__ void commit(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
     return r;
   }, a.ctl, 700);
   if (!ok) return;
-  trace_mark(a, 3 * ILL_MAXLAYERS + 4);
+  trace_mark(a, ILL_TR_TAIL + 4);
   for (int t = H.lmh0; t < H.lmh0 + H.lmhn; t++) {
     if (i < ILL_WG) {
       C.v[i] = wval(aload64(a.lmp + (i * 16 + t) * 2));
@@ -781,6 +860,7 @@ __device__ void commit(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
       a.ctl->last_tok = tok;
     } else {
       // speculative pass: rows 0..nrows-1 = [last token, drafts]; accept and commit
+      // (Shaders.swift:305-333)
       const int nv = H.nrows;
       int m = 0;
       if (H.mode == ILL_MODE_TREE) {
@@ -837,19 +917,29 @@ __device__ void commit(const IllPassArgs& a, const PassHdr& H, PassLds& S) {
     }
     __syncthreads();
   }
-  if (i == 0) a.ctl->epoch = H.epoch + 1;
+  if (i == 0) {
+    a.ctl->bank_rows[H.bank] = H.nrows;   // rows of this bank to clear during the next pass
+    a.ctl->bank_rows[H.bank ^ 1] = 0;     // cleared during this pass
+    a.ctl->epoch = H.epoch + 1;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
 template <int T>
-__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs a) {
-  __shared__ PassLds S;
+__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs args) {
+  // A private copy: the roles take the arguments by reference, and a reference to the
+  // kernel-argument segment would otherwise be re-read with FLAT loads inside hot loops.
+  const IllPassArgs a = args;
+  __shared__ PassLds<T> S;
+  extern __shared__ __attribute__((aligned(16))) uint8_t ill_stage[];   // ILL_STAGE_BYTES (dynamic)
   __shared__ PassHdr H;
   if (threadIdx.x == 0) {
     const IllState* st = a.st;
     const IllCtl* c = a.ctl;
     H.done = st->done;
     H.epoch = c->epoch;
+    H.bank = c->epoch & 1;
+    H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
     H.mode = c->mode;
     H.nrows = c->nrows;
     H.pos = st->pos;
@@ -867,29 +957,47 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
         H.parent[t] = t > 0 ? t - 1 : 0;
       }
     }
+    for (int t = 0; t < 16; t++) {
+      int r = t;
+      for (int d = H.depth[t]; d >= 0; --d) {
+        H.prow[t][d] = r;
+        r = r > 0 ? H.parent[r] : 0;
+      }
+    }
   }
   __syncthreads();
   if (H.done) return;
   const int wg = blockIdx.x;
   const int NL = a.W.layers;
-  for (int l = 0; l < NL; l++) {
-    bool ok = true;
-    trace_mark(a, 3 * l);
-    if (wg < ILL_R_QKV + ILL_NQB) ok = role_qkv<T>(a, H, S, l, wg - ILL_R_QKV);
-    else if (wg >= ILL_R_ATT && wg < ILL_R_ATT + ILL_N_ATT) {
-      const int nit = H.nrows * ILL_NKV;
-      for (int it = wg - ILL_R_ATT; it < nit && ok; it += ILL_N_ATT) ok = role_att<T>(a, H, S, l, it & 1, it >> 1);
-    } else if (wg >= ILL_R_O && wg < ILL_R_O + ILL_NOT) ok = role_o<T>(a, H, S, l, wg - ILL_R_O);
-    else if (wg >= ILL_R_GUD && wg < ILL_R_GUD + ILL_NGU) ok = role_gud<T>(a, H, S, l, wg - ILL_R_GUD);
-    else if (wg >= ILL_R_RED && wg < ILL_R_RED + ILL_NOT) ok = role_red<T>(a, H, l, wg - ILL_R_RED);
-    if (!ok) return;
-    trace_mark(a, 3 * l + 2);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wg >= ILL_R_ATT0 && wg < ILL_R_ATT0 + ILL_NATT) {
+    const int h = wg - ILL_R_ATT0;
+    att_stage_qkv(a.L[0], h, w, lane, ill_stage);
+    for (int l = 0; l < NL; l++) {
+      trace_mark(a, 6 * l);
+      if (!role_att<T>(a, H, S.att, l, h, ill_stage)) return;
+      __syncthreads();   // every wave is done with the stage before it is refilled
+      if (l + 1 < NL) att_stage_qkv(a.L[l + 1], h, w, lane, ill_stage);
+      trace_mark(a, 6 * l + 5);
+    }
+  } else if (wg >= ILL_R_GUD0 && wg < ILL_R_GUD0 + ILL_NGU) {
+    const int ub = wg - ILL_R_GUD0;
+    gud_stage(a.L[0], ub, w, lane, ill_stage);
+    for (int l = 0; l < NL; l++) {
+      trace_mark(a, 6 * l);
+      if (!role_gud<T>(a, H, S.gud, l, ub, ill_stage)) return;
+      __syncthreads();
+      if (l + 1 < NL) gud_stage(a.L[l + 1], ub, w, lane, ill_stage);
+      trace_mark(a, 6 * l + 5);
+    }
   }
-  trace_mark(a, 3 * ILL_MAXLAYERS);
-  if (!role_lmh<T>(a, H, S)) return;
-  trace_mark(a, 3 * ILL_MAXLAYERS + 2);
+  trace_mark(a, ILL_TR_TAIL);
+  if (!role_lmh<T>(a, H, S.lmh)) return;
+  zero_other_bank(a, H);
+  trace_mark(a, ILL_TR_TAIL + 2);
   if (wg == 0) {
-    commit(a, H, S);
-    trace_mark(a, 3 * ILL_MAXLAYERS + 5);
+    __syncthreads();
+    commit(a, H, S.cm);
+    trace_mark(a, ILL_TR_TAIL + 5);
   }
 }

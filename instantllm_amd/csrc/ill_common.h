@@ -19,7 +19,8 @@
 // Device layout unit sizes (q4): a "block" is 16 rows x 128 columns = 2 quant groups.
 #define ILL_KST 7            // 896 / 128 column blocks per K = 896 row tile
 #define ILL_NGU 76           // 4864 / 64 hidden-unit blocks of the fused gate/up/down role
-#define ILL_GUD_N ILL_NGU    // contributions to each element of the post-MLP residual
+#define ILL_XA_N 15          // contributions to the post-attention residual: 14 heads + base
+#define ILL_XB_N 77          // contributions to the post-MLP residual: 76 unit blocks + base
 #define ILL_NOT 56           // 896 / 16 row tiles of O and down
 #define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV
 

@@ -75,32 +75,38 @@ __device__ __forceinline__ void set_err(IllCtl* ctl, int code) {
 // Workgroup-wide bounded wait: `ready()` is evaluated by every thread (it loads the words
 // the thread needs and checks their tags). Returns false (uniformly) on timeout or when
 // another workgroup has already recorded an error.
+// The error flag and the clock are consulted every 32nd poll only, so a wait that succeeds
+// early costs one memory round trip per poll and nothing else.
 template <class F>
 __device__ __forceinline__ bool wg_wait(F&& ready, IllCtl* ctl, int code) {
   const uint64_t t0 = clk();
-  for (;;) {
+  for (int it = 1;; it++) {
     const bool ok = ready();
     if (__syncthreads_and(ok)) return true;
-    int bad = 0;
-    if (threadIdx.x == 0) {
-      bad = aload32(&ctl->err) != 0;
-      if (!bad && clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); bad = 1; }
+    if ((it & 31) == 0) {
+      int bad = 0;
+      if (threadIdx.x == 0) {
+        bad = aload32(&ctl->err) != 0;
+        if (!bad && clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); bad = 1; }
+      }
+      if (__syncthreads_or(bad)) return false;
     }
-    if (__syncthreads_or(bad)) return false;
     __builtin_amdgcn_s_sleep(1);
   }
 }
 
 // Wave-wide bounded wait (lanes of one wave only). On failure the caller must still reach
-// the next workgroup barrier and then test `wg_failed`.
+// the next workgroup barrier and report its failure there.
 template <class F>
 __device__ __forceinline__ bool wave_wait(F&& ready, IllCtl* ctl, int code) {
   const uint64_t t0 = clk();
-  for (;;) {
+  for (int it = 1;; it++) {
     const bool ok = ready();
     if (__all(ok)) return true;
-    if (aload32(&ctl->err) != 0) return false;
-    if (clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); return false; }
+    if ((it & 31) == 0) {
+      if (aload32(&ctl->err) != 0) return false;
+      if (clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); return false; }
+    }
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -150,9 +156,10 @@ __device__ __forceinline__ int q4perm(int p) {
 __device__ __forceinline__ void quant16(const float* v, float d, uint32_t hi[4], uint32_t lo[4], int& sumq) {
   int q[16];
   sumq = 0;
+  const float inv = d > 0.f ? 1.0f / d : 0.f;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    q[i] = d > 0.f ? (int)rintf(v[i] / d) : 0;
+    q[i] = (int)rintf(v[i] * inv);
     sumq += q[i];
   }
 #pragma unroll

@@ -20,7 +20,8 @@
 // top byte: each contributor adds (1 << 56) + (rint(v * 2^24) + 2^48). Integer addition
 // makes the sum independent of arrival order (deterministic, and the same for any T), and
 // a consumer knows an element is complete when its count reaches the number of
-// contributors. ATT[0] and GUD[0] fold the incoming residual into their contribution.
+// contributors. A separate BASE workgroup adds the incoming residual as one more
+// contributor.
 // Accumulators alternate between two banks by pass; the idle bank is zeroed during the
 // lm_head phase.
 //
@@ -31,6 +32,7 @@
 
 #define ILL_NATT 14          // ATT workgroups (one per query head)
 #define ILL_R_ATT0 0         // ATT WGs 0..13
+#define ILL_R_BASE 14        // the residual-copy workgroup
 #define ILL_R_GUD0 16        // GUD WGs 16..91
 
 struct IllPassArgs {
@@ -100,6 +102,11 @@ __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int
 struct SrcAcc {
   const uint64_t* base;   // row 0; rows are ILL_H apart
   int expect;
+  // One word to spin on before reading the whole row: the last row tile is written last by
+  // every contributor, so polling it keeps traffic off the lines still receiving atomics.
+  __device__ __forceinline__ bool sentinel(int t) const {
+    return fx_count(aload64(base + (size_t)t * ILL_H + ILL_H - 1)) == expect;
+  }
   __device__ __forceinline__ bool load(int t, int c0, float* v) const {
     const uint64_t* p = base + (size_t)t * ILL_H + c0;
     bool ok = true;
@@ -139,6 +146,7 @@ __device__ __forceinline__ float embed1(const IllWeights& W, int tok, int c) {
 struct SrcEmbed {
   IllWeights W;
   const int* toks;   // LDS copy of the row tokens
+  __device__ __forceinline__ bool sentinel(int) const { return true; }
   __device__ __forceinline__ bool load(int t, int c0, float* v) const {
     embed16(W, toks[t], c0, v);
     return true;
@@ -155,6 +163,9 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   const int G = lane >> 2, kg = lane & 3;
   const bool act = lane < 56;
   const int c0 = 64 * G + 16 * kg;
+  float gm[16];   // norm weights, loaded before the wait
+#pragma unroll
+  for (int i = 0; i < 16; i++) gm[i] = act ? gld(gamma + c0 + i) : 0.f;
   bool alive = true;
   for (int t = w; t < T && alive; t += ILL_WAVES) {
     if (t >= nrows) {
@@ -166,6 +177,8 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
       continue;
     }
     float v[16];
+    alive = wave_wait([&]() { return lane != 0 || src.sentinel(t); }, ctl, code);
+    if (!alive) break;
     alive = wave_wait([&]() { return !act || src.load(t, c0, v); }, ctl, code);
     if (!alive) break;
     if (!act) {
@@ -179,7 +192,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     const float scale = 1.0f / sqrtf(ss / (float)ILL_H + ILL_EPS);
     if (act) {
 #pragma unroll
-      for (int i = 0; i < 16; i++) v[i] = v[i] * scale * gld(gamma + c0 + i);
+      for (int i = 0; i < 16; i++) v[i] = v[i] * scale * gm[i];
     }
     float mx = 0.f;
 #pragma unroll
@@ -196,8 +209,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
       if (kg == 0) P.sc[G * 16 + t] = make_float2(d, d * (float)sq);
     }
   }
-  __syncthreads();
-  return !wg_failed(ctl);
+  return !__syncthreads_or(!alive);
 }
 
 __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
@@ -208,7 +220,7 @@ __device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* a
   const int lane = threadIdx.x & 63;
   const float mx = wmax_xor(fabsf(h), 1, 32);
   const float d = mx / ILL_QMAX;
-  const int qv = d > 0.f ? (int)rintf(h / d) : 0;
+  const int qv = (int)rintf(h * (d > 0.f ? 1.0f / d : 0.f));
   const int sq = isum_xor(qv, 1, 32);
   const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
   const int gi = lane >> 4, p = q4perm_inv(lane & 15);
@@ -472,22 +484,35 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   const IllLayerW& L = a.L[l];
   constexpr int RPL = T >= 4 ? 4 : T;
   const int nrows = H.nrows;
+  // QKV epilogue constants (independent of the input): bias and RoPE (cos, sin) per row
+  const int d = (att_block(h, w < 6 ? w : 0) & 1) * 16 + n;
+  float bias0 = 0.f, bias1 = 0.f;
+  float2 rope[4] = {};
+  if (w < 6) {
+    const int b = att_block(h, w);
+    bias0 = gld(L.bqkv + 32 * b + n);
+    bias1 = gld(L.bqkv + 32 * b + 16 + n);
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int t = 4 * kg + j;
+      if (t < nrows) rope[j] = gld(a.rope + (H.pos + H.depth[t]) * 32 + d);
+    }
+  }
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
-  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_GUD_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
+  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_XB_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
   if (!ok) return false;
   trace_mark(a, 6 * l + 1);
   // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
   if (w < 6) {
     const int b = att_block(h, w);
     float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
-    wait_vm();   // this wave's staged QKV block
+    wait_vm();   // this wave's staged QKV block and the epilogue constants below
     const uint8_t* st = stage + w * ILL_ST_QKV;
     q4_tile896_lds<T>(st, st + 2 * ILL_KST * 1024, A.u.prep, lane, acc0);
     q4_tile896_lds<T>(st + ILL_KST * 1024, st + 2 * ILL_KST * 1024 + ILL_KST * 128, A.u.prep, lane, acc1);
-    const int head = b >> 1, d = (b & 1) * 16 + n;
-    const float bias0 = gld(L.bqkv + 32 * b + n), bias1 = gld(L.bqkv + 32 * b + 16 + n);
+    const int head = b >> 1;
     const bool writer = (h % 7) == 0;   // one query head per group writes the K/V cache
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
@@ -495,7 +520,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       if (t >= nrows) continue;
       float x0 = acc0[j] + bias0, x1 = acc1[j] + bias1;
       if (head < ILL_NH + ILL_NKV) {
-        const float2 cs = gld(a.rope + (H.pos + H.depth[t]) * 32 + d);
+        const float2 cs = rope[j];
         const float r0 = x0 * cs.x - x1 * cs.y;
         const float r1 = x1 * cs.x + x0 * cs.y;
         x0 = r0;
@@ -627,13 +652,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
         float y = 0.f;
         y = fmaf(sw, dx.x * (float)Sv, y);
         y = fmaf(mw, dx.y, y);
-        int64_t qv = fx_of(y);
-        if (h == 0) {
-          // fold in the incoming residual x_l (exactly, as an integer)
-          if (l == 0) qv += fx_of(embed1(a.W, H.tok[t], row));
-          else qv += fx_value(aload64(acc_ptr(a, H.bank, l - 1, 1, t) + row));
-        }
-        fx_add(acc_ptr(a, H.bank, l, 0, t) + row, fx_word(qv));
+        fx_add(acc_ptr(a, H.bank, l, 0, t) + row, fx_word(fx_of(y)));
       }
     }
   }
@@ -657,7 +676,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   const IllLayerW& L = a.L[l];
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
-  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_NATT}, L.ln2, nrows, G.prep, a.ctl, 400 + l)) return false;
+  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_XA_N}, L.ln2, nrows, G.prep, a.ctl, 400 + l)) return false;
   trace_mark(a, 6 * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -711,13 +730,57 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
         float y = 0.f;
         y = fmaf(sw, dx.x * (float)Sv, y);
         y = fmaf(mw, dx.y, y);
-        int64_t qv = fx_of(y);
-        if (ub == 0) qv += fx_value(aload64(acc_ptr(a, H.bank, l, 0, t) + row));
-        fx_add(acc_ptr(a, H.bank, l, 1, t) + row, fx_word(qv));
+        fx_add(acc_ptr(a, H.bank, l, 1, t) + row, fx_word(fx_of(y)));
       }
     }
   }
   trace_mark(a, 6 * l + 4);
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------
+// BASE (one workgroup): the residual itself is the last contributor of each accumulator.
+// It adds x_l (the embedding at layer 0, else the completed XB[l-1]) into XA[l], then the
+// completed XA[l] into XB[l]. It runs beside the ATT and GUD work of the same layer, so
+// the copies stay off the critical path.
+template <int T>
+__device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H, int l) {
+  constexpr int PER = (T * ILL_H + ILL_WG_THREADS - 1) / ILL_WG_THREADS;
+  const int n = H.nrows * ILL_H;
+  auto wait_full = [&](const uint64_t* src, int expect, int code) {
+    return wg_wait([&]() {
+      bool r = true;
+#pragma unroll
+      for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + k * ILL_WG_THREADS;
+        if (i < n) r &= fx_count(aload64(src + i)) == expect;
+      }
+      return r;
+    }, a.ctl, code);
+  };
+  uint64_t* xa = acc_ptr(a, H.bank, l, 0, 0);
+  uint64_t* xb = acc_ptr(a, H.bank, l, 1, 0);
+  if (l == 0) {
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int i = threadIdx.x + k * ILL_WG_THREADS;
+      if (i < n) fx_add(xa + i, fx_word(fx_of(embed1(a.W, H.tok[i / ILL_H], i % ILL_H))));
+    }
+  } else {
+    const uint64_t* prev = acc_ptr(a, H.bank, l - 1, 1, 0);
+    if (!wait_full(prev, ILL_XB_N, 800 + l)) return false;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int i = threadIdx.x + k * ILL_WG_THREADS;
+      if (i < n) fx_add(xa + i, fx_word(fx_value(aload64(prev + i))));
+    }
+  }
+  if (!wait_full(xa, ILL_XA_N, 850 + l)) return false;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = threadIdx.x + k * ILL_WG_THREADS;
+    if (i < n) fx_add(xb + i, fx_word(fx_value(aload64(xa + i))));
+  }
   return true;
 }
 
@@ -742,7 +805,7 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_GUD_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600)) return false;
+    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_XB_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600)) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {
@@ -814,10 +877,16 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
   const uint32_t tag = tagof_lmh(H.epoch);
   const int i = threadIdx.x;
+  // every workgroup's partials for the rows in use (row 0 when the pass has no lm_head rows):
+  // this also proves that every workgroup has read the pass header
+  const int r0 = H.lmhn > 0 ? H.lmh0 : 0, nr = H.lmhn > 0 ? H.lmhn : 1;
   const bool ok = wg_wait([&]() {
     bool r = true;
-    if (i < ILL_WG)
-      for (int t = 0; t < 16; t++) r &= wok(aload64(a.lmp + (i * 16 + t) * 2), tag) & wok(aload64(a.lmp + (i * 16 + t) * 2 + 1), tag);
+#pragma unroll 8
+    for (int k = i; k < ILL_WG * nr; k += ILL_WG_THREADS) {
+      const int wgi = k % ILL_WG, t = r0 + k / ILL_WG;
+      r &= wok(aload64(a.lmp + (wgi * 16 + t) * 2), tag) & wok(aload64(a.lmp + (wgi * 16 + t) * 2 + 1), tag);
+    }
     return r;
   }, a.ctl, 700);
   if (!ok) return;
@@ -988,6 +1057,12 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       if (!role_gud<T>(a, H, S.gud, l, ub, ill_stage)) return;
       __syncthreads();
       if (l + 1 < NL) gud_stage(a.L[l + 1], ub, w, lane, ill_stage);
+      trace_mark(a, 6 * l + 5);
+    }
+  } else if (wg == ILL_R_BASE) {
+    for (int l = 0; l < NL; l++) {
+      trace_mark(a, 6 * l);
+      if (!role_base<T>(a, H, l)) return;
       trace_mark(a, 6 * l + 5);
     }
   }

@@ -85,11 +85,24 @@ def main() -> int:
     ap.add_argument("--prefix", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (the reference dispatch "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (the decode step does not shard; "
-              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (the decode step does not shard); "
+              "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.calib_copy_mib > 0:
+        import torch
+        n = args.calib_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": n, "dispatches": 4}), flush=True)
+        return 0
     from instantllm_amd import illfile as F
     from instantllm_amd.engine import Engine
     from oracle.tree import random_tree
@@ -159,7 +172,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4 weights, int8 MFMA (exact int32) + fp32 epilogues",
+        "dtype": "int8 MFMA (q4 weights, 16-bit fixed-point activations) + f32",
         "data": "synthetic (seeded random weights and token ids)",
         "config": {"workload": "config 2: q4 1-row greedy decode, Qwen2.5-0.5B shape (24L, d896, 14/2 heads, "
                                "FFN 4864, vocab 151936), prefix KV 256, each step one persistent kernel in a hipGraph",

@@ -7,6 +7,7 @@
 // epoch * 32 + layer + 1; the epoch advances once per pass, so a word from an earlier
 // pass or layer never passes the check.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include "ill_common.h"
@@ -117,23 +118,62 @@ __device__ __forceinline__ bool wg_failed(IllCtl* ctl) {
   return __syncthreads_or(bad);
 }
 
-// ---- wave reductions (xor butterflies: every lane ends with the same, order-fixed value)
-__device__ __forceinline__ float wsum64(float v) {
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---- wave reductions ---------------------------------------------------------------------
+// Reductions over aligned lane groups of 2^k lanes with cross-lane moves that stay out of
+// LDS: DPP quad permutes (partners l^1, l^2), row half-mirror and row mirror (partners
+// within 8 and 16 lanes), then permlane16/32 swaps (the other row / the other half-wave).
+// Every stage combines a lane's value with one partner's and both partners compute the
+// same commutative operation, so every lane of the group ends with the same value, and
+// the association order is fixed.
+#define ILL_DPP_XOR1 0xB1    // quad_perm [1,0,3,2]
+#define ILL_DPP_XOR2 0x4E    // quad_perm [2,3,0,1]
+#define ILL_DPP_HMIR 0x141   // row_half_mirror
+#define ILL_DPP_MIR 0x140    // row_mirror
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+
+// Combine over groups of N lanes (N = 2, 4, ..., 64) with operation `op`.
+template <int N, class V, class Op>
+__device__ __forceinline__ V group_reduce(V v, Op op) {
+  auto dpp = [](V x, auto ctrl_tag) {
+    constexpr int C = decltype(ctrl_tag)::value;
+    if constexpr (sizeof(V) == 4 && __is_same(V, float)) return dpp_f<C>(x);
+    else return (V)dpp_i<C>((int)x);
+  };
+  v = op(v, dpp(v, std::integral_constant<int, ILL_DPP_XOR1>{}));
+  if constexpr (N >= 4) v = op(v, dpp(v, std::integral_constant<int, ILL_DPP_XOR2>{}));
+  if constexpr (N >= 8) v = op(v, dpp(v, std::integral_constant<int, ILL_DPP_HMIR>{}));
+  if constexpr (N >= 16) v = op(v, dpp(v, std::integral_constant<int, ILL_DPP_MIR>{}));
+  if constexpr (N >= 32) {
+    int bits;
+    __builtin_memcpy(&bits, &v, 4);
+    const auto r = __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+    V a, b;
+    const int r0 = (int)r[0], r1 = (int)r[1];
+    __builtin_memcpy(&a, &r0, 4);
+    __builtin_memcpy(&b, &r1, 4);
+    v = op(a, b);
+  }
+  if constexpr (N >= 64) {
+    int bits;
+    __builtin_memcpy(&bits, &v, 4);
+    const auto r = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+    V a, b;
+    const int r0 = (int)r[0], r1 = (int)r[1];
+    __builtin_memcpy(&a, &r0, 4);
+    __builtin_memcpy(&b, &r1, 4);
+    v = op(a, b);
+  }
   return v;
 }
-__device__ __forceinline__ float wmax_xor(float v, int lo, int hi) {
-  for (int o = hi; o >= lo; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wsum_xor(float v, int lo, int hi) {
-  for (int o = hi; o >= lo; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ int isum_xor(int v, int lo, int hi) {
-  for (int o = hi; o >= lo; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+struct OpAddF { __device__ float operator()(float a, float b) const { return a + b; } };
+struct OpMaxF { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpAddI { __device__ int operator()(int a, int b) const { return a + b; } };
+template <int N> __device__ __forceinline__ float gsum(float v) { return group_reduce<N>(v, OpAddF{}); }
+template <int N> __device__ __forceinline__ float gmax(float v) { return group_reduce<N>(v, OpMaxF{}); }
+template <int N> __device__ __forceinline__ int gsumi(int v) { return group_reduce<N>(v, OpAddI{}); }
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
@@ -218,64 +258,80 @@ __device__ __forceinline__ v4i q4_unpack(uint32_t a, uint32_t b) {
 
 // Prepared activations of a K = 896 input in LDS (see prep896): A operands per group G,
 // lane-group kg and row m, and per (G, row) the pair (d, X = d * sum(v)).
+template <int T>
 struct PrepLds {
-  uint4 ahi[14 * 4 * 16];
-  uint4 alo[14 * 4 * 16];
-  float2 sc[14 * 16];
+  uint4 ahi[14 * 4 * T];
+  uint4 alo[14 * 4 * T];
+  float2 sc[14 * T];
 };
+
+// MFMA A-operand row read by lane row m: at T = 1 every lane row aliases row 0, so the
+// tile's 16 output rows are copies of row 0 and no lane reads outside the T rows held.
+template <int T>
+__device__ __forceinline__ int arow(int m) { return T == 1 ? 0 : (m & (T - 1)); }
 
 // Accumulate one 16-row tile over K = 896: acc[j] (rows t = 4*kg + j of the pass, weight
 // row n) += sum_G s*d*S + m*X. The per-value operation sequence is independent of T.
 // `fetch(cb, w, s)` supplies block cb's 16 weight bytes and (scale, min) pairs for this lane.
+// The body has no branches, so the compiler can issue every operand read of the tile
+// before the first MFMA; rows >= nrows produce values that callers ignore.
+// Opaque copy of a per-lane value: address arithmetic derived from it is redone at each use
+// instead of being hoisted out of enclosing loops into long-lived registers.
+__device__ __forceinline__ int opq(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 template <int T, class Fetch>
-__device__ __forceinline__ void q4_tile896f(Fetch fetch, const PrepLds& P, int lane, float acc[4]) {
-  const int kg = lane >> 4, m = lane & 15;
+__device__ __forceinline__ void q4_tile896f(Fetch fetch, const PrepLds<T>& P, int lane_, float acc[4]) {
+  const int lane = opq(lane_);
+  const int kg = lane >> 4, m = arow<T>(lane & 15);
   constexpr int RPL = T >= 4 ? 4 : T;
+  uint4 wv[ILL_KST];
+  uint2 sv[ILL_KST];
 #pragma unroll
-  for (int cb = 0; cb < ILL_KST; cb++) {
-    uint4 wv;
-    uint2 sv;
-    fetch(cb, wv, sv);
+  for (int cb = 0; cb < ILL_KST; cb++) fetch(cb, wv[cb], sv[cb]);
 #pragma unroll
-    for (int gi = 0; gi < 2; gi++) {
-      const int G = 2 * cb + gi;
-      const v4i b = gi == 0 ? q4_unpack(wv.x, wv.y) : q4_unpack(wv.z, wv.w);
-      v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
-      if (m < T) {
-        const uint4 h = P.ahi[(G * 4 + kg) * 16 + m];
-        const uint4 l = P.alo[(G * 4 + kg) * 16 + m];
-        ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
-        al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
-      }
-      const v4i z = {0, 0, 0, 0};
-      const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
-      const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-      const uint32_t sm = gi == 0 ? sv.x : sv.y;
-      const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+  for (int G = 0; G < 2 * ILL_KST; G++) {
+    const int cb = G >> 1, gi = G & 1;
+    const v4i b = gi == 0 ? q4_unpack(wv[cb].x, wv[cb].y) : q4_unpack(wv[cb].z, wv[cb].w);
+    const uint4 h = P.ahi[(G * 4 + kg) * T + m];
+    const uint4 l = P.alo[(G * 4 + kg) * T + m];
+    const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
+    const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
+    const v4i z = {0, 0, 0, 0};
+    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+    const uint32_t sm = gi == 0 ? sv[cb].x : sv[cb].y;
+    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
 #pragma unroll
-      for (int j = 0; j < RPL; j++) {
-        const int row = 4 * kg + j;
-        if (row < T) {
-          const float2 dx = P.sc[G * 16 + row];
-          const int S = (dh[j] << 8) + dl[j];
-          const float t1 = dx.x * (float)S;
-          acc[j] = fmaf(sw, t1, acc[j]);
-          acc[j] = fmaf(mw, dx.y, acc[j]);
-        }
-      }
+    for (int j = 0; j < RPL; j++) {
+      const float2 dx = P.sc[G * T + arow<T>(4 * kg + j)];
+      const int S = (dh[j] << 8) + dl[j];
+      const float t1 = dx.x * (float)S;
+      acc[j] = fmaf(sw, t1, acc[j]);
+      acc[j] = fmaf(mw, dx.y, acc[j]);
+    }
+    // At T > 1 each group needs 4 rows of (d, X): pin each group's epilogue to its group
+    // and bound the scheduler's read-ahead to two groups, so the operands and MFMA results
+    // of a whole tile are not held in registers at once.
+    if (T > 1) {
+#pragma unroll
+      for (int j = 0; j < RPL; j++) asm volatile("" : "+v"(acc[j]));
+      if (G & 1) __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
 // Tile held in registers (lm_head stream).
 template <int T>
-__device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds& P, int lane, float acc[4]) {
+__device__ __forceinline__ void q4_tile896(const Q4Tile& t, const PrepLds<T>& P, int lane, float acc[4]) {
   q4_tile896f<T>([&](int cb, uint4& w, uint2& s) { w = t.w[cb]; s = t.s[cb]; }, P, lane, acc);
 }
 
 // Tile staged in LDS in the HBM block layout: 7 x 1 KiB weights at `w`, 7 x 128 B scales at `s`.
 template <int T>
-__device__ __forceinline__ void q4_tile896_lds(const uint8_t* w, const uint8_t* s, const PrepLds& P, int lane, float acc[4]) {
+__device__ __forceinline__ void q4_tile896_lds(const uint8_t* w, const uint8_t* s, const PrepLds<T>& P, int lane, float acc[4]) {
   const int n = lane & 15;
   q4_tile896f<T>([&](int cb, uint4& wv, uint2& sv) {
     wv = *(const uint4*)(w + cb * 1024 + lane * 16);

@@ -142,8 +142,8 @@ int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, in
 
 int launch(ill_engine* e, int T) {
   HCK(hipEventRecord(e->ev0, e->stream));
-  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
-  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
+  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
+  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
   HCK(hipGetLastError());
   HCK(hipEventRecord(e->ev1, e->stream));
   return 0;
@@ -306,12 +306,15 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   }
 
   if (hipSetDevice(0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "no HIP device"));
-  int maxb = 0;
-  if (hipFuncSetAttribute((const void*)ill_pass_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, ILL_STAGE_BYTES) != hipSuccess ||
-      hipFuncSetAttribute((const void*)ill_pass_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, ILL_STAGE_BYTES) != hipSuccess)
-    return cleanup(fail(ILL_E_HIP, "cannot raise the pass kernel's LDS limit to %d B", ILL_STAGE_BYTES));
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, ILL_STAGE_BYTES) != hipSuccess || maxb < 1)
-    return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d)", maxb));
+  int maxb = 0, maxb1 = 0;
+  if (hipFuncSetAttribute((const void*)ill_pass_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, ill_stage_bytes(1)) != hipSuccess ||
+      hipFuncSetAttribute((const void*)ill_pass_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, ill_stage_bytes(16)) != hipSuccess)
+    return cleanup(fail(ILL_E_HIP, "cannot raise the pass kernel's LDS limit to %d B", ill_stage_bytes(1)));
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, ill_stage_bytes(16)) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb1, ill_pass_kernel<1>, ILL_WG_THREADS, ill_stage_bytes(1)) != hipSuccess ||
+      maxb < 1 || maxb1 < 1)
+    return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d / %d)", maxb1, maxb));
+  maxb = std::min(maxb, maxb1);
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipGetDeviceProperties failed"));
   if (prop.multiProcessorCount * maxb < ILL_WG)
@@ -537,7 +540,7 @@ int ill_capture_steps(ill_engine* e, int nsteps) {
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   for (int i = 0; i < nsteps; i++)
-    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ILL_STAGE_BYTES, e->stream, e->args);
+    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = nsteps;

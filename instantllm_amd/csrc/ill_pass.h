@@ -55,10 +55,11 @@ struct IllPassArgs {
   int maxsteps;
 };
 
-// Trace slots per workgroup: 6 per layer (role start, input ready, three role-specific
-// intermediate points, done) and 6 for the lm_head / commit tail.
-#define ILL_TR_TAIL (6 * ILL_MAXLAYERS)
-#define ILL_TRACE_SLOTS (ILL_TR_TAIL + 6)
+// Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10
+// role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail.
+#define ILL_TRL 12
+#define ILL_TR_TAIL (ILL_TRL * ILL_MAXLAYERS)
+#define ILL_TRACE_SLOTS (ILL_TR_TAIL + 12)
 __device__ __forceinline__ void trace_mark(const IllPassArgs& a, int slot) {
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * ILL_TRACE_SLOTS + slot] = wall_clock64();
 }
@@ -69,6 +70,15 @@ struct PassHdr {
   int tok[16], depth[16], parent[16];
   int prow[16][16];        // prow[t][d]: pass row on row t's path at depth d
 };
+
+// threadIdx.x passed through an opaque move. Address arithmetic derived from it then stays
+// inside the role that uses it: without this the compiler hoists every per-lane address
+// out of the layer loop, where the values occupy registers for the whole kernel.
+__device__ __forceinline__ int tid_opaque() {
+  int v = threadIdx.x;
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 // ---- residual fixed point --------------------------------------------------------------
 #define FX_COUNT (1ull << 56)
@@ -157,9 +167,9 @@ struct SrcEmbed {
 // operands. Row t is handled by wave t % 8 with the same instruction sequence for every
 // T: lane (G, kg) = (lane / 4, lane % 4), lanes 56-63 idle.
 template <int T, class Src>
-__device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds& P,
+__device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds<T>& P,
                                         IllCtl* ctl, int code) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int G = lane >> 2, kg = lane & 3;
   const bool act = lane < 56;
   const int c0 = 64 * G + 16 * kg;
@@ -170,9 +180,9 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   for (int t = w; t < T && alive; t += ILL_WAVES) {
     if (t >= nrows) {
       if (act) {
-        P.ahi[(G * 4 + kg) * 16 + t] = make_uint4(0, 0, 0, 0);
-        P.alo[(G * 4 + kg) * 16 + t] = make_uint4(0, 0, 0, 0);
-        if (kg == 0) P.sc[G * 16 + t] = make_float2(0.f, 0.f);
+        P.ahi[(G * 4 + kg) * T + t] = make_uint4(0, 0, 0, 0);
+        P.alo[(G * 4 + kg) * T + t] = make_uint4(0, 0, 0, 0);
+        if (kg == 0) P.sc[G * T + t] = make_float2(0.f, 0.f);
       }
       continue;
     }
@@ -188,7 +198,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) ss = fmaf(v[i], v[i], ss);
-    ss = wsum64(ss);
+    ss = gsum<64>(ss);
     const float scale = 1.0f / sqrtf(ss / (float)ILL_H + ILL_EPS);
     if (act) {
 #pragma unroll
@@ -197,16 +207,16 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     float mx = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
-    mx = wmax_xor(mx, 1, 2);
+    mx = gmax<4>(mx);
     const float d = mx / ILL_QMAX;
     uint32_t hi[4], lo[4];
     int sq;
     quant16(v, d, hi, lo, sq);
-    sq = isum_xor(sq, 1, 2);
+    sq = gsumi<4>(sq);
     if (act) {
-      P.ahi[(G * 4 + kg) * 16 + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-      P.alo[(G * 4 + kg) * 16 + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-      if (kg == 0) P.sc[G * 16 + t] = make_float2(d, d * (float)sq);
+      P.ahi[(G * 4 + kg) * T + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      P.alo[(G * 4 + kg) * T + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      if (kg == 0) P.sc[G * T + t] = make_float2(d, d * (float)sq);
     }
   }
   return !__syncthreads_or(!alive);
@@ -215,17 +225,19 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
 __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
 
 // One row (64 values, one per lane) -> 16-bit coding as a K = 64 MFMA operand:
-// lane (kg, m = row) of the operand holds units 16 kg + q4perm(p).
+// lane (kg, m = row) of the operand holds units 16 kg + q4perm(p); operand k-group gi of
+// row t is at [gi * T + t].
+template <int T>
 __device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* alo, float2* dsc) {
-  const int lane = threadIdx.x & 63;
-  const float mx = wmax_xor(fabsf(h), 1, 32);
+  const int lane = tid_opaque() & 63;
+  const float mx = gmax<64>(fabsf(h));
   const float d = mx / ILL_QMAX;
   const int qv = (int)rintf(h * (d > 0.f ? 1.0f / d : 0.f));
-  const int sq = isum_xor(qv, 1, 32);
+  const int sq = gsumi<64>(qv);
   const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
   const int gi = lane >> 4, p = q4perm_inv(lane & 15);
-  ((uint8_t*)&ahi[gi * 16 + t])[p] = (uint8_t)(hi & 0xff);
-  ((uint8_t*)&alo[gi * 16 + t])[p] = (uint8_t)(lo & 0xff);
+  ((uint8_t*)&ahi[gi * T + t])[p] = (uint8_t)(hi & 0xff);
+  ((uint8_t*)&alo[gi * T + t])[p] = (uint8_t)(lo & 0xff);
   if (lane == 0) dsc[t] = make_float2(d, d * (float)sq);
 }
 
@@ -238,6 +250,10 @@ __device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* a
 //        down: wave w at 64512 + w * 4032: [7 x 512 B][7 x 64 B]
 #define ILL_STAGE_BYTES 96768
 #define ILL_ST_QKV 16128
+// At T = 1 the static LDS is small, so the ATT role keeps its O weights in a region of
+// their own after the QKV block and stages both at the end of the previous layer.
+__host__ __device__ constexpr int ill_stage_bytes(int T) { return T == 1 ? ILL_STAGE_BYTES + 8 * 4032 : ILL_STAGE_BYTES; }
+__host__ __device__ constexpr int ill_st_o(int T) { return T == 1 ? ILL_STAGE_BYTES : 0; }
 #define ILL_ST_SPLIT 4032
 #define ILL_ST_GU 8064
 #define ILL_ST_DOWN0 64512
@@ -253,7 +269,7 @@ __device__ __forceinline__ void split_stage(const uint8_t* wg, const uint32_t* s
 template <int T>
 struct AttLds {
   union {
-    PrepLds prep;
+    PrepLds<T> prep;
     float P[ILL_WAVES][T][64];
     struct {
       float cm[ILL_WAVES][T], cl[ILL_WAVES][T];
@@ -264,20 +280,23 @@ struct AttLds {
   uint16_t k[T][64];
   uint16_t v[T][64];
   float o[T][64];
-  uint4 ahi[4 * 16], alo[4 * 16];
-  float2 dsc[16];
+  float pm[2][T], pl[2][T];   // statistics of the partial chunks ns + i per row
+  float po[2][T][64];
+  uint4 ahi[4 * T], alo[4 * T];
+  float2 dsc[T];
 };
 
 template <int T>
 struct GudLds {
-  PrepLds prep;
+  PrepLds<T> prep;
   float gu[8][T][16];
-  uint4 ahi[4 * 16], alo[4 * 16];
-  float2 dsc[16];
+  uint4 ahi[4 * T], alo[4 * T];
+  float2 dsc[T];
 };
 
+template <int T>
 struct LmhLds {
-  PrepLds prep;
+  PrepLds<T> prep;
   float bv[ILL_WAVES][16];
   int bi[ILL_WAVES][16];
 };
@@ -294,7 +313,7 @@ template <int T>
 union PassLds {
   AttLds<T> att;
   GudLds<T> gud;
-  LmhLds lmh;
+  LmhLds<T> lmh;
   CommitLds cm;
 };
 
@@ -314,9 +333,14 @@ __device__ __forceinline__ void att_stage_qkv(const IllLayerW& L, int h, int w, 
   }
 }
 
+template <int T>
 __device__ __forceinline__ void att_stage_o(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
-  split_stage(L.wo + (size_t)h * ILL_NOT * 512, L.so + h * ILL_NOT * 16, w, lane, stage + w * ILL_ST_SPLIT);
+  split_stage(L.wo + (size_t)h * ILL_NOT * 512, L.so + h * ILL_NOT * 16, w, lane, stage + ill_st_o(T) + w * ILL_ST_SPLIT);
 }
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations but not for
+// its outstanding global loads, stores, atomics or LDS DMA (which __syncthreads would).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -334,84 +358,114 @@ __device__ __forceinline__ v8h u4_to_v8h(uint4 u) {
   }
   return r;
 }
-__device__ __forceinline__ _Float16 hbits(uint32_t b) { return __builtin_bit_cast(_Float16, (unsigned short)(b & 0xffff)); }
+// Bitwise select (m = all ones or zero): keeps the compiler from turning a select of a
+// loaded value into a branch around the load.
+__device__ __forceinline__ uint32_t msel(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
+__device__ __forceinline__ uint4 msel4(uint32_t m, uint4 a, uint4 b) {
+  return make_uint4(msel(m, a.x, b.x), msel(m, a.y, b.y), msel(m, a.z, b.z), msel(m, a.w, b.w));
+}
+__device__ __forceinline__ uint32_t mask_of(bool c) { return 0u - (uint32_t)c; }
 
-// One 64-position attention chunk for the rows selected by `rmask` (bit t = row t).
-// Positions p < pos come from the caches; positions pos <= p < L_t (this pass's rows on row
-// t's path) come from LDS. `shared`: every selected row maps positions identically (the
-// chunk lies below pos), so one MFMA serves all rows; otherwise `rmask` holds one row.
-// Lane layout of results: lane (g4, n) holds rows 4 g4 + j.
+// e^x for the softmax as 2^(x log2 e) on the hardware exp2 (exp(-inf) = 0).
+__device__ __forceinline__ float att_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+// Pass-row V along each row's path, [T][64 dims][16 depths] u16 (zero beyond the row's
+// depth), built in the free part of the weight stage before attention.
+#define ILL_ST_VPT 32256
+
+// ---- attention ------------------------------------------------------------------------
+// Positions are split into 64-position chunks by virtual position (the position a key has
+// on the row's own path), so a row's arithmetic depends only on its path and not on how
+// the path is split between the cache and the rows of the current pass:
+//   chunks c < ns = pos / 64 lie below pos and are shared by every row; chunk c goes to
+//     wave c % 8, which folds its chunks into a running (max, sum, output) in order of c;
+//   chunks c >= ns ("partial") hold pass rows. Each (chunk, row) pair is evaluated on its
+//     own by some wave; its statistics are folded into wave c % 8's running state at the
+//     combine, after that wave's shared chunks, i.e. still in order of c.
+// At T = 1 the chunk holding the new position is the only partial chunk.
+
+// One cache chunk as MFMA operands for this lane (kg, n):
+// k[b][hf]: key 64c + 16b + n, dims 32 hf + 8 kg .. +8; v[nb][ks]: dim 16 nb + n,
+// positions 64c + 32 ks + 8 kg .. +8 (from the transposed V layout).
+struct KVFrag {
+  uint4 k[4][2];
+  uint4 v[4][2];
+};
+
+__device__ __forceinline__ void kv_fetch(const uint16_t* kbase, const uint16_t* vbase, int c, int lane, KVFrag& f) {
+  const int kg = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const uint4* kr = (const uint4*)(kbase + (size_t)(64 * c + 16 * b + n) * 64);
+    f.k[b][0] = gld(kr + kg);
+    f.k[b][1] = gld(kr + 4 + kg);
+  }
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+      f.v[nb][ks] = gld((const uint4*)(vbase + ((size_t)c * 64 + 16 * nb + n) * 64 + 32 * ks + 8 * kg));
+  }
+}
+
+// Chunk-local attention over positions 64c .. 64c+63. With `part`, keys at positions
+// >= pos come from the pass rows on row t1's path and keys at positions >= L(t1) are
+// masked; without it every key is a valid cache key. Results for rows 4 kg + j of this
+// lane: mx = max score, ls = sum exp(s - mx), o[nb] = sum exp(s - mx) v (dims 16 nb + n).
 template <int T>
-__device__ __forceinline__ void att_chunk(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int g, int c,
-                                          uint32_t rmask, bool shared, const v8h qa[2][2],
-                                          float M[4], float Lw[4], float O[4][4]) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const uint8_t* stage, const KVFrag& f, int c, bool part,
+                                           int t1, const v8h qa[2][2], float mx[4], float ls[4], float o[4][4]) {
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int pos = H.pos;
-  const int t1 = shared ? 0 : __builtin_ctz(rmask);   // the single row of a per-row chunk
-  const int Lt = shared ? pos : pos + H.depth[t1] + 1;
-  const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
-  const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
-  // query operands restricted to the selected rows
-  v8h qh[2], ql[2];
-  const bool rowsel = (rmask >> n) & 1;
+  const int Lt = part ? pos + H.depth[t1] + 1 : 0x7fffffff;
+  const uint4 zz = make_uint4(0, 0, 0, 0);
+  // pass rows on row t1's path for this lane's key positions
+  int rk[4];
+  if (part) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      qh[ks][i] = rowsel ? qa[ks][0][i] : (_Float16)0.f;
-      ql[ks][i] = rowsel ? qa[ks][1][i] : (_Float16)0.f;
-    }
+    for (int b = 0; b < 4; b++) rk[b] = min(H.prow[t1][min(max(64 * c + 16 * b + n - pos, 0), 15)], T - 1);
   }
   float sc[4][4];
 #pragma unroll
   for (int b = 0; b < 4; b++) {
     const int vp = 64 * c + 16 * b + n;
-    v8h k0, k1;
-    if (vp < pos) {
-      const uint4* kr = (const uint4*)(kbase + (size_t)vp * 64);
-      k0 = u4_to_v8h(gld(kr + kg));
-      k1 = u4_to_v8h(gld(kr + 4 + kg));
-    } else if (vp < Lt) {
-      const uint16_t* kr = A.k[H.prow[t1][vp - pos]];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        k0[i] = hbits(kr[8 * kg + i]);
-        k1[i] = hbits(kr[32 + 8 * kg + i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) { k0[i] = (_Float16)0.f; k1[i] = (_Float16)0.f; }
+    uint4 k0 = f.k[b][0], k1 = f.k[b][1];
+    if (part) {
+      const uint4 l0 = *(const uint4*)&A.k[rk[b]][8 * kg];
+      const uint4 l1 = *(const uint4*)&A.k[rk[b]][32 + 8 * kg];
+      const uint32_t mc = mask_of(vp < pos), ml = mask_of(vp >= pos && vp < Lt);
+      k0 = msel4(mc, k0, msel4(ml, l0, zz));
+      k1 = msel4(mc, k1, msel4(ml, l1, zz));
     }
     v4f s = {0.f, 0.f, 0.f, 0.f};
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[0], k0, s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[0], k0, s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[1], k1, s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[1], k1, s, 0, 0, 0);
-    const bool valid = shared || vp < Lt;
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], u4_to_v8h(k0), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], u4_to_v8h(k0), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], u4_to_v8h(k1), s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(k1), s, 0, 0, 0);
+    const bool valid = vp < Lt;
 #pragma unroll
     for (int j = 0; j < 4; j++) sc[b][j] = valid ? s[j] : -INFINITY;
   }
-  float mx[4], ls[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const float m = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
-    mx[j] = wmax_xor(m, 1, 8);
+    mx[j] = gmax<16>(m);
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    float s = 0.f;
+    float sum = 0.f;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-      sc[b][j] = expf(sc[b][j] - mx[j]);
-      s += sc[b][j];
+      sc[b][j] = att_exp(sc[b][j] - mx[j]);
+      sum += sc[b][j];
     }
-    ls[j] = wsum_xor(s, 1, 8);
+    ls[j] = gsum<16>(sum);
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int t = 4 * kg + j;
-    if (t < T && ((rmask >> t) & 1)) {
+    if (t < T) {
 #pragma unroll
       for (int b = 0; b < 4; b++) A.u.P[w][t][16 * b + n] = sc[b][j];
     }
@@ -422,7 +476,7 @@ __device__ __forceinline__ void att_chunk(const IllPassArgs& a, const PassHdr& H
   for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float p = (n < T && rowsel) ? A.u.P[w][n < T ? n : 0][32 * ks + 8 * kg + i] : 0.f;
+      const float p = A.u.P[w][arow<T>(n)][32 * ks + 8 * kg + i];
       const _Float16 hi = (_Float16)p;
       ph[ks][i] = hi;
       pl[ks][i] = (_Float16)(p - (float)hi);
@@ -435,55 +489,120 @@ __device__ __forceinline__ void att_chunk(const IllPassArgs& a, const PassHdr& H
     v8h vv[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const int p0 = 64 * c + 32 * ks + 8 * kg;
-      if (p0 + 7 < pos) {
-        vv[ks] = u4_to_v8h(gld((const uint4*)(vbase + ((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg)));
-      } else {
+      uint4 u = f.v[nb][ks];
+      if (part) {
+        // positions >= pos: row t1's path table (zero beyond its depth); positions >= pos + 16 hold no key
+        const uint16_t* vpt = (const uint16_t*)(stage + ILL_ST_VPT) + ((size_t)t1 * 64 + dim) * 16;
+        uint32_t e[8];
+        const uint32_t x[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-          const int vp = p0 + i;
-          uint32_t bits = 0;
-          if (vp < pos) bits = gld(vbase + ((size_t)c * 64 + dim) * 64 + 32 * ks + 8 * kg + i);
-          else if (vp < Lt) bits = A.v[H.prow[t1][vp - pos]][dim];
-          vv[ks][i] = hbits(bits);
+          const int d = 64 * c + 32 * ks + 8 * kg + i - pos;
+          const uint32_t lv = vpt[min(max(d, 0), 15)];
+          const uint32_t cv = (x[i >> 1] >> (16 * (i & 1))) & 0xffff;
+          e[i] = msel(mask_of(d < 0), cv, lv & mask_of(d < 16));
         }
+        u = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
       }
+      vv[ks] = u4_to_v8h(u);
     }
-    v4f o = {0.f, 0.f, 0.f, 0.f};
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], o, 0, 0, 0);
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], o, 0, 0, 0);
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], o, 0, 0, 0);
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], o, 0, 0, 0);
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], acc, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int t = 4 * kg + j;
-      if (t < T && ((rmask >> t) & 1)) {
-        const float mn = fmaxf(M[j], mx[j]);
-        const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
-        O[nb][j] = O[nb][j] * sa + o[j] * sb;
-      }
+    for (int j = 0; j < 4; j++) o[nb][j] = acc[j];
+  }
+}
+
+// Folding chunk statistics (m2, l2, o2) into a running state (m, l, o) is the one rule
+// used for every chunk of every row: mn = max(m, m2), sa = exp(m - mn), sb = exp(m2 - mn),
+// o' = o sa + o2 sb, l' = l sa + l2 sb.
+struct AttScale {
+  float mn, sa, sb;
+};
+__device__ __forceinline__ AttScale att_scale(float m, float m2) {
+  AttScale r;
+  r.mn = fmaxf(m, m2);
+  r.sa = att_exp(m - r.mn);
+  r.sb = att_exp(m2 - r.mn);
+  return r;
+}
+__device__ __forceinline__ float att_fold(float x, float x2, const AttScale& k) { return x * k.sa + x2 * k.sb; }
+
+// Split-K partial of an 896-row projection over one 64-column input group (O: one head,
+// down: 64 hidden units), from this wave's 7 staged row tiles (rows 112 w .. +112, LDS
+// layout [7 x 512 B codes][7 x 64 B scales]). Each output y = s*d*S + m*X is added to
+// row t < nrows of the accumulator (`accw` = row 0, element 112 w) as a fixed-point
+// contribution. All operand reads and MFMAs come before the atomics.
+template <int T>
+__device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, const uint4* alo, const float2* dsc,
+                                           int lane, int nrows, uint64_t* accw) {
+  const int kg = lane >> 4, n = lane & 15;
+  constexpr int RPL = T >= 4 ? 4 : T;
+  const uint4 xh = ahi[kg * T + arow<T>(n)], xl = alo[kg * T + arow<T>(n)];
+  const v4i ah = (v4i){(int)xh.x, (int)xh.y, (int)xh.z, (int)xh.w};
+  const v4i al = (v4i){(int)xl.x, (int)xl.y, (int)xl.z, (int)xl.w};
+  const v4i z = {0, 0, 0, 0};
+  uint2 wv[7];
+  uint32_t sm[7];
+#pragma unroll
+  for (int k = 0; k < 7; k++) {
+    wv[k] = *(const uint2*)(so + k * 512 + lane * 8);
+    sm[k] = *(const uint32_t*)(so + 7 * 512 + k * 64 + n * 4);
+  }
+  float2 dx[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; j++) dx[j] = dsc[arow<T>(4 * kg + j)];
+  float y[7][RPL];
+#pragma unroll
+  for (int k = 0; k < 7; k++) {
+    const v4i bq = q4_unpack(wv[k].x, wv[k].y);
+    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
+    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
+    const float sw = h2f(sm[k] & 0xffff), mw = h2f(sm[k] >> 16);
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int Sv = (dh[j] << 8) + dl[j];
+      float v = 0.f;
+      v = fmaf(sw, dx[j].x * (float)Sv, v);
+      v = fmaf(mw, dx[j].y, v);
+      y[k][j] = v;
     }
   }
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+  for (int j = 0; j < RPL; j++) {
     const int t = 4 * kg + j;
-    if (t < T && ((rmask >> t) & 1)) {
-      const float mn = fmaxf(M[j], mx[j]);
-      const float sa = expf(M[j] - mn), sb = expf(mx[j] - mn);
-      Lw[j] = Lw[j] * sa + ls[j] * sb;
-      M[j] = mn;
+    if (t < nrows) {
+#pragma unroll
+      for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_H + 16 * k + n, fx_word(fx_of(y[k][j])));
     }
   }
 }
 
+// Chunk of the partial (chunk, row) pair number `idx` (pairs run over chunks c >= ns, then
+// rows t with L(t) > 64 c), or -1.
+__device__ __forceinline__ int att_pair_chunk(const PassHdr& H, int ns, int cmax, int idx) {
+  int k = 0;
+  for (int c = ns; c <= cmax; c++)
+    for (int t = 0; t < H.nrows; t++)
+      if (H.pos + H.depth[t] + 1 > 64 * c) {
+        if (k == idx) return c;
+        k++;
+      }
+  return -1;
+}
+
 template <int T>
 __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int h, uint8_t* stage) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int g = h / 7;
   const IllLayerW& L = a.L[l];
   constexpr int RPL = T >= 4 ? 4 : T;
   const int nrows = H.nrows;
+  const int pos = H.pos;
   // QKV epilogue constants (independent of the input): bias and RoPE (cos, sin) per row
   const int d = (att_block(h, w < 6 ? w : 0) & 1) * 16 + n;
   float bias0 = 0.f, bias1 = 0.f;
@@ -495,23 +614,42 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
-      if (t < nrows) rope[j] = gld(a.rope + (H.pos + H.depth[t]) * 32 + d);
+      if (t < nrows) rope[j] = gld(a.rope + (pos + H.depth[t]) * 32 + d);
     }
   }
+  // ---- attention work of this wave: shared chunks w, w + 8, ... < ns, then the partial
+  // pairs idx = w - ns (mod 8), + 8, ...
+  int maxL = 0;
+  for (int t = 0; t < nrows; t++) maxL = max(maxL, pos + H.depth[t] + 1);
+  const int ns = pos >> 6, cmax = (maxL - 1) >> 6;
+  const int pidx0 = (w - ns) & 7;
+  const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
+  const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
+  const int cfirst = w < ns ? w : att_pair_chunk(H, ns, cmax, pidx0);
+  KVFrag f;
+  int fc = -1;   // cache chunk held in f
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
   else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_XB_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
   if (!ok) return false;
-  trace_mark(a, 6 * l + 1);
+  trace_mark(a, ILL_TRL * l + 1);
   // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
+  float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
+  wait_vm();   // every wave: its staged weights and the epilogue constants (nothing else is in flight)
+  trace_mark(a, ILL_TRL * l + 2);
   if (w < 6) {
-    const int b = att_block(h, w);
-    float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
-    wait_vm();   // this wave's staged QKV block and the epilogue constants below
     const uint8_t* st = stage + w * ILL_ST_QKV;
     q4_tile896_lds<T>(st, st + 2 * ILL_KST * 1024, A.u.prep, lane, acc0);
     q4_tile896_lds<T>(st + ILL_KST * 1024, st + 2 * ILL_KST * 1024 + ILL_KST * 128, A.u.prep, lane, acc1);
+    trace_mark(a, ILL_TRL * l + 3);
+  }
+  // the wave's first cache chunk streams in while the QKV epilogue runs (always issued, so
+  // later waits can count the loads in flight; chunk 0 stands in when the wave has none)
+  kv_fetch(kbase, vbase, cfirst >= 0 ? cfirst : 0, lane, f);
+  fc = cfirst;
+  if (w < 6) {
+    const int b = att_block(h, w);
     const int head = b >> 1;
     const bool writer = (h % 7) == 0;   // one query head per group writes the K/V cache
 #pragma unroll
@@ -526,7 +664,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
         x0 = r0;
         x1 = r1;
       }
-      const int slot = H.pos + t;
+      const int slot = pos + t;
       if (head < ILL_NH) {
         A.q[t][d] = x0;
         A.q[t][d + 32] = x1;
@@ -551,16 +689,26 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       }
     }
   }
-  __syncthreads();
-  att_stage_o(L, h, w, lane, stage);   // O weights stream in while attention runs
-  trace_mark(a, 6 * l + 2);
-  // ---- attention for head h over T rows
+  lds_barrier();
+  trace_mark(a, ILL_TRL * l + 4);
+  if (T != 1) att_stage_o<T>(L, h, w, lane, stage);   // O weights stream in while attention runs
+  if (cmax >= ns) {   // partial chunks exist: path table of the pass rows' V
+    uint16_t* vpt = (uint16_t*)(stage + ILL_ST_VPT);
+    for (int i = tid; i < T * 64 * 16; i += ILL_WG_THREADS) {
+      const int t1 = i >> 10, dim = (i >> 4) & 63, dd = i & 15;
+      const bool on = t1 < nrows && dd <= H.depth[t1];
+      vpt[i] = on ? A.v[min(H.prow[t1][dd], T - 1)][dim] : (uint16_t)0;
+    }
+    lds_barrier();
+  }
+  trace_mark(a, ILL_TRL * l + 5);
+  // ---- attention for head h
   v8h qa[2][2];   // [ks][hi/lo], lane (kg, m = row), dims 32 ks + 8 kg + i, q * 0.125
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float v = (n < T && n < nrows) ? A.q[n < T ? n : 0][32 * ks + 8 * kg + i] * 0.125f : 0.f;
+      const float v = A.q[arow<T>(n)][32 * ks + 8 * kg + i] * 0.125f;
       const _Float16 hi = (_Float16)v;
       qa[ks][0][i] = hi;
       qa[ks][1][i] = (_Float16)(v - (float)hi);
@@ -574,19 +722,51 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
-  int maxL = 0;
-  for (int t = 0; t < nrows; t++) maxL = max(maxL, H.pos + H.depth[t] + 1);
-  const int nch = (maxL + 63) >> 6;
-  const uint32_t allrows = (nrows >= 32) ? 0xffffffffu : ((1u << nrows) - 1u);
-  for (int c = w; c < nch; c += ILL_WAVES) {
-    if (64 * c + 63 < H.pos) {
-      att_chunk<T>(a, H, A, l, g, c, allrows, true, qa, M, Lw, O);
-    } else {
-      for (int t = 0; t < nrows; t++)
-        if (H.pos + H.depth[t] + 1 > 64 * c) att_chunk<T>(a, H, A, l, g, c, 1u << t, false, qa, M, Lw, O);
+  for (int c = w; c < ns; c += ILL_WAVES) {
+    if (c != fc) {
+      kv_fetch(kbase, vbase, c, lane, f);
+      fc = c;
+    }
+    float mx[4], ls[4], o[4][4];
+    chunk_eval<T>(H, A, stage, f, c, false, 0, qa, mx, ls, o);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const AttScale k = att_scale(M[j], mx[j]);
+#pragma unroll
+      for (int nb = 0; nb < 4; nb++) O[nb][j] = att_fold(O[nb][j], o[nb][j], k);
+      Lw[j] = att_fold(Lw[j], ls[j], k);
+      M[j] = k.mn;
     }
   }
-  __syncthreads();   // LDS: P region becomes the combine region
+  {
+    int idx = 0;
+    for (int c = ns; c <= cmax; c++) {
+      for (int t1 = 0; t1 < nrows; t1++) {
+        if (pos + H.depth[t1] + 1 <= 64 * c) continue;
+        if (((idx++) & 7) != pidx0) continue;
+        if (c != fc) {
+          kv_fetch(kbase, vbase, c, lane, f);
+          fc = c;
+        }
+        float mx[4], ls[4], o[4][4];
+        chunk_eval<T>(H, A, stage, f, c, true, t1, qa, mx, ls, o);
+        if (kg == (t1 >> 2)) {
+          const int j = t1 & 3;
+#pragma unroll
+          for (int nb = 0; nb < 4; nb++) {
+            const float ov = j == 0 ? o[nb][0] : j == 1 ? o[nb][1] : j == 2 ? o[nb][2] : o[nb][3];
+            A.po[c - ns][t1][16 * nb + n] = ov;
+          }
+          if (n == 0) {
+            A.pm[c - ns][t1] = j == 0 ? mx[0] : j == 1 ? mx[1] : j == 2 ? mx[2] : mx[3];
+            A.pl[c - ns][t1] = j == 0 ? ls[0] : j == 1 ? ls[1] : j == 2 ? ls[2] : ls[3];
+          }
+        }
+      }
+    }
+  }
+  trace_mark(a, ILL_TRL * l + 6);
+  lds_barrier();   // LDS: P region becomes the combine region
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int t = 4 * kg + j;
@@ -599,64 +779,57 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       for (int nb = 0; nb < 4; nb++) A.u.c.co[w][t][16 * nb + n] = O[nb][j];
     }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < nrows * 64; i += ILL_WG_THREADS) {
+  lds_barrier();
+  // combine: wave states (+ the partial chunks of each wave, in chunk order), then across
+  // waves against the global maximum
+  for (int i = tid_opaque(); i < nrows * 64; i += ILL_WG_THREADS) {
     const int t = i >> 6, dim = i & 63;
-    float m = -INFINITY, s = 0.f, o = 0.f;
+    const int Lt = pos + H.depth[t] + 1;
+    float sm[ILL_WAVES], sl[ILL_WAVES], so[ILL_WAVES];
+#pragma unroll
     for (int ww = 0; ww < ILL_WAVES; ww++) {
-      const float mw = A.u.c.cm[ww][t];
-      if (mw == -INFINITY) continue;
-      const float mn = fmaxf(m, mw);
-      const float sa = expf(m - mn), sb = expf(mw - mn);
-      s = s * sa + A.u.c.cl[ww][t] * sb;
-      o = o * sa + A.u.c.co[ww][t][dim] * sb;
-      m = mn;
-    }
-    A.o[t][dim] = o / s;
-  }
-  __syncthreads();
-  trace_mark(a, 6 * l + 3);
-  // ---- O projection restricted to head h's columns (one quant group): rows t by wave t % 8
-  for (int t = w; t < T; t += ILL_WAVES) {
-    if (t < nrows) quant_row64(A.o[t][lane], t, A.ahi, A.alo, A.dsc);
-    else if (lane < 4) {
-      A.ahi[lane * 16 + t] = make_uint4(0, 0, 0, 0);
-      A.alo[lane * 16 + t] = make_uint4(0, 0, 0, 0);
-    }
-  }
-  __syncthreads();
-  v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
-  if (n < T) {
-    const uint4 x = A.ahi[kg * 16 + n], y = A.alo[kg * 16 + n];
-    ah = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
-    al = (v4i){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
-  }
-  const v4i z = {0, 0, 0, 0};
-  wait_vm();   // this wave's staged O tiles
-  const uint8_t* so = stage + w * ILL_ST_SPLIT;
+      sm[ww] = A.u.c.cm[ww][t];
+      sl[ww] = A.u.c.cl[ww][t];
+      so[ww] = A.u.c.co[ww][t][dim];
 #pragma unroll
-  for (int k = 0; k < 7; k++) {
-    const int rt = 7 * w + k, row = 16 * rt + n;
-    const uint2 wv = *(const uint2*)(so + k * 512 + lane * 8);
-    const uint32_t sm = *(const uint32_t*)(so + 7 * 512 + k * 64 + n * 4);
-    const v4i bq = q4_unpack(wv.x, wv.y);
-    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
-    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
-    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
-#pragma unroll
-    for (int j = 0; j < RPL; j++) {
-      const int t = 4 * kg + j;
-      if (t < nrows) {
-        const float2 dx = A.dsc[t];
-        const int Sv = (dh[j] << 8) + dl[j];
-        float y = 0.f;
-        y = fmaf(sw, dx.x * (float)Sv, y);
-        y = fmaf(mw, dx.y, y);
-        fx_add(acc_ptr(a, H.bank, l, 0, t) + row, fx_word(fx_of(y)));
+      for (int ci = 0; ci < 2; ci++) {
+        const int c = ns + ci;
+        if ((c & 7) == ww && c <= cmax && Lt > 64 * c) {
+          const AttScale k = att_scale(sm[ww], A.pm[ci][t]);
+          so[ww] = att_fold(so[ww], A.po[ci][t][dim], k);
+          sl[ww] = att_fold(sl[ww], A.pl[ci][t], k);
+          sm[ww] = k.mn;
+        }
       }
     }
+    float m = sm[0];
+#pragma unroll
+    for (int ww = 1; ww < ILL_WAVES; ww++) m = fmaxf(m, sm[ww]);
+    float sum = 0.f, o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < ILL_WAVES; ww++) {
+      const float e = att_exp(sm[ww] - m);
+      sum = sum + sl[ww] * e;
+      o = o + so[ww] * e;
+    }
+    A.o[t][dim] = o / sum;
   }
-  trace_mark(a, 6 * l + 4);
+  lds_barrier();
+  trace_mark(a, ILL_TRL * l + 7);
+  // ---- O projection restricted to head h's columns (one quant group): rows t by wave t % 8
+  for (int t = w; t < T; t += ILL_WAVES) {
+    if (t < nrows) quant_row64<T>(A.o[t][lane], t, A.ahi, A.alo, A.dsc);
+    else if (lane < 4) {
+      A.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
+      A.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  lds_barrier();
+  trace_mark(a, ILL_TRL * l + 8);
+  wait_vm();   // this wave's staged O tiles
+  trace_mark(a, ILL_TRL * l + 9);
+  split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows, acc_ptr(a, H.bank, l, 0, 0) + 16 * 7 * w);
+  trace_mark(a, ILL_TRL * l + 10);
   return true;
 }
 
@@ -671,70 +844,44 @@ __device__ __forceinline__ void gud_stage(const IllLayerW& L, int ub, int w, int
 
 template <int T>
 __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H, GudLds<T>& G, int l, int ub, uint8_t* stage) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const IllLayerW& L = a.L[l];
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
   if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_XA_N}, L.ln2, nrows, G.prep, a.ctl, 400 + l)) return false;
-  trace_mark(a, 6 * l + 1);
+  trace_mark(a, ILL_TRL * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     wait_vm();   // this wave's staged gate/up tile and down tiles
+    trace_mark(a, ILL_TRL * l + 2);
     const uint8_t* sg = stage + w * ILL_ST_GU;
     q4_tile896_lds<T>(sg, sg + ILL_KST * 1024, G.prep, lane, acc);
+    trace_mark(a, ILL_TRL * l + 3);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
       if (t < T) G.gu[w][t][n] = acc[j];
     }
   }
-  __syncthreads();
-  trace_mark(a, 6 * l + 2);
+  lds_barrier();
+  trace_mark(a, ILL_TRL * l + 4);
   // SiLU(gate) * up for the block's 64 units; each row coded as one 64-wide group
   for (int t = w; t < T; t += ILL_WAVES) {
     if (t < nrows) {
       const int gi = lane >> 4, nn = lane & 15;
       const float gv = G.gu[gi][t][nn], up = G.gu[4 + gi][t][nn];
-      quant_row64(gv / (1.0f + expf(-gv)) * up, t, G.ahi, G.alo, G.dsc);
+      quant_row64<T>(gv / (1.0f + expf(-gv)) * up, t, G.ahi, G.alo, G.dsc);
     } else if (lane < 4) {
-      G.ahi[lane * 16 + t] = make_uint4(0, 0, 0, 0);
-      G.alo[lane * 16 + t] = make_uint4(0, 0, 0, 0);
+      G.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
+      G.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
     }
   }
-  __syncthreads();
-  trace_mark(a, 6 * l + 3);
-  v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
-  if (n < T) {
-    const uint4 x = G.ahi[kg * 16 + n], y = G.alo[kg * 16 + n];
-    ah = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
-    al = (v4i){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
-  }
-  const v4i z = {0, 0, 0, 0};
-  const uint8_t* sd = stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT;
-#pragma unroll
-  for (int k = 0; k < 7; k++) {
-    const int rt = 7 * w + k, row = 16 * rt + n;
-    const uint2 wv = *(const uint2*)(sd + k * 512 + lane * 8);
-    const uint32_t sm = *(const uint32_t*)(sd + 7 * 512 + k * 64 + n * 4);
-    const v4i b = q4_unpack(wv.x, wv.y);
-    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
-    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
-#pragma unroll
-    for (int j = 0; j < RPL; j++) {
-      const int t = 4 * kg + j;
-      if (t < nrows) {
-        const float2 dx = G.dsc[t];
-        const int Sv = (dh[j] << 8) + dl[j];
-        float y = 0.f;
-        y = fmaf(sw, dx.x * (float)Sv, y);
-        y = fmaf(mw, dx.y, y);
-        fx_add(acc_ptr(a, H.bank, l, 1, t) + row, fx_word(fx_of(y)));
-      }
-    }
-  }
-  trace_mark(a, 6 * l + 4);
+  lds_barrier();
+  trace_mark(a, ILL_TRL * l + 5);
+  split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
+                acc_ptr(a, H.bank, l, 1, 0) + 16 * 7 * w);
+  trace_mark(a, ILL_TRL * l + 10);
   return true;
 }
 
@@ -745,6 +892,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
 // the copies stay off the critical path.
 template <int T>
 __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H, int l) {
+  const int tid = tid_opaque();
   constexpr int PER = (T * ILL_H + ILL_WG_THREADS - 1) / ILL_WG_THREADS;
   const int n = H.nrows * ILL_H;
   auto wait_full = [&](const uint64_t* src, int expect, int code) {
@@ -752,7 +900,7 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
       bool r = true;
 #pragma unroll
       for (int k = 0; k < PER; k++) {
-        const int i = threadIdx.x + k * ILL_WG_THREADS;
+        const int i = tid + k * ILL_WG_THREADS;
         if (i < n) r &= fx_count(aload64(src + i)) == expect;
       }
       return r;
@@ -763,7 +911,7 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
   if (l == 0) {
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-      const int i = threadIdx.x + k * ILL_WG_THREADS;
+      const int i = tid + k * ILL_WG_THREADS;
       if (i < n) fx_add(xa + i, fx_word(fx_of(embed1(a.W, H.tok[i / ILL_H], i % ILL_H))));
     }
   } else {
@@ -771,14 +919,14 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
     if (!wait_full(prev, ILL_XB_N, 800 + l)) return false;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-      const int i = threadIdx.x + k * ILL_WG_THREADS;
+      const int i = tid + k * ILL_WG_THREADS;
       if (i < n) fx_add(xa + i, fx_word(fx_value(aload64(prev + i))));
     }
   }
   if (!wait_full(xa, ILL_XA_N, 850 + l)) return false;
 #pragma unroll
   for (int k = 0; k < PER; k++) {
-    const int i = threadIdx.x + k * ILL_WG_THREADS;
+    const int i = tid + k * ILL_WG_THREADS;
     if (i < n) fx_add(xb + i, fx_word(fx_value(aload64(xa + i))));
   }
   return true;
@@ -790,8 +938,8 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float ov, int oi) {
 }
 
 template <int T>
-__device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, LmhLds& Lm) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, LmhLds<T>& Lm) {
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int NL = a.W.layers;
   const uint32_t tag = tagof_lmh(H.epoch);
@@ -866,7 +1014,7 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
   const size_t total = nrow_total * per_row;
   const size_t chunk = (total + ILL_WG - 1) / ILL_WG;
   const size_t lo = (size_t)blockIdx.x * chunk, hi = min(total, lo + chunk);
-  for (size_t i = lo + threadIdx.x; i < hi; i += ILL_WG_THREADS) {
+  for (size_t i = lo + tid_opaque(); i < hi; i += ILL_WG_THREADS) {
     const size_t r = i / per_row, c = i % per_row;
     const size_t lk = r / H.zrows, t = r % H.zrows;
     gst(a.acc + ((((size_t)other * NL) * 2 + lk) * 16 + t) * ILL_H + c, (uint64_t)0);
@@ -876,7 +1024,7 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
   const uint32_t tag = tagof_lmh(H.epoch);
-  const int i = threadIdx.x;
+  const int i = tid_opaque();
   // every workgroup's partials for the rows in use (row 0 when the pass has no lm_head rows):
   // this also proves that every workgroup has read the pass header
   const int r0 = H.lmhn > 0 ? H.lmh0 : 0, nr = H.lmhn > 0 ? H.lmhn : 1;
@@ -1027,6 +1175,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       }
     }
     for (int t = 0; t < 16; t++) {
+      for (int d = 0; d < 16; d++) H.prow[t][d] = 0;
       int r = t;
       for (int d = H.depth[t]; d >= 0; --d) {
         H.prow[t][d] = r;
@@ -1038,32 +1187,36 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   if (H.done) return;
   const int wg = blockIdx.x;
   const int NL = a.W.layers;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   if (wg >= ILL_R_ATT0 && wg < ILL_R_ATT0 + ILL_NATT) {
     const int h = wg - ILL_R_ATT0;
     att_stage_qkv(a.L[0], h, w, lane, ill_stage);
+    if (T == 1) att_stage_o<T>(a.L[0], h, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
-      trace_mark(a, 6 * l);
+      trace_mark(a, ILL_TRL * l);
       if (!role_att<T>(a, H, S.att, l, h, ill_stage)) return;
-      __syncthreads();   // every wave is done with the stage before it is refilled
-      if (l + 1 < NL) att_stage_qkv(a.L[l + 1], h, w, lane, ill_stage);
-      trace_mark(a, 6 * l + 5);
+      lds_barrier();   // every wave is done with the stage before it is refilled
+      if (l + 1 < NL) {
+        att_stage_qkv(a.L[l + 1], h, w, lane, ill_stage);
+        if (T == 1) att_stage_o<T>(a.L[l + 1], h, w, lane, ill_stage);
+      }
+      trace_mark(a, ILL_TRL * l + 11);
     }
   } else if (wg >= ILL_R_GUD0 && wg < ILL_R_GUD0 + ILL_NGU) {
     const int ub = wg - ILL_R_GUD0;
     gud_stage(a.L[0], ub, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
-      trace_mark(a, 6 * l);
+      trace_mark(a, ILL_TRL * l);
       if (!role_gud<T>(a, H, S.gud, l, ub, ill_stage)) return;
-      __syncthreads();
+      lds_barrier();
       if (l + 1 < NL) gud_stage(a.L[l + 1], ub, w, lane, ill_stage);
-      trace_mark(a, 6 * l + 5);
+      trace_mark(a, ILL_TRL * l + 11);
     }
   } else if (wg == ILL_R_BASE) {
     for (int l = 0; l < NL; l++) {
-      trace_mark(a, 6 * l);
+      trace_mark(a, ILL_TRL * l);
       if (!role_base<T>(a, H, l)) return;
-      trace_mark(a, 6 * l + 5);
+      trace_mark(a, ILL_TRL * l + 11);
     }
   }
   trace_mark(a, ILL_TR_TAIL);

@@ -201,7 +201,7 @@ class Engine:
 
     def trace_read(self) -> np.ndarray:
         """[256, slots] device-clock ticks (100 MHz) of the last pass; 0 = not reached."""
-        out = np.zeros(256 * 192, np.uint64)
+        out = np.zeros(256 * 1024, np.uint64)
         n = C.c_int(0)
         self._check(self.lib.ill_trace_read(self.h, _ptr(out, C.c_uint64), C.byref(n)))
         return out[: 256 * n.value].reshape(256, n.value)

@@ -196,7 +196,7 @@ __device__ __forceinline__ int q4perm(int p) {
 __device__ __forceinline__ void quant16(const float* v, float d, uint32_t hi[4], uint32_t lo[4], int& sumq) {
   int q[16];
   sumq = 0;
-  const float inv = d > 0.f ? 1.0f / d : 0.f;
+  const float inv = d > 0.f ? __builtin_amdgcn_rcpf(d) : 0.f;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     q[i] = (int)rintf(v[i] * inv);
@@ -263,6 +263,8 @@ struct PrepLds {
   uint4 ahi[14 * 4 * T];
   uint4 alo[14 * 4 * T];
   float2 sc[14 * T];
+  float red[ILL_WAVES][T];   // per-wave partial sums of squares
+  int ok[ILL_WAVES];         // per-wave "input complete" votes
 };
 
 // MFMA A-operand row read by lane row m: at T = 1 every lane row aliases row 0, so the

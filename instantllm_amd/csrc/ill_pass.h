@@ -55,9 +55,9 @@ struct IllPassArgs {
   int maxsteps;
 };
 
-// Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10
-// role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail.
-#define ILL_TRL 12
+// Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10 and
+// 12-15 role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail.
+#define ILL_TRL 16
 #define ILL_TR_TAIL (ILL_TRL * ILL_MAXLAYERS)
 #define ILL_TRACE_SLOTS (ILL_TR_TAIL + 12)
 __device__ __forceinline__ void trace_mark(const IllPassArgs& a, int slot) {
@@ -79,6 +79,10 @@ __device__ __forceinline__ int tid_opaque() {
   asm volatile("" : "+v"(v));
   return v;
 }
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations but not for
+// its outstanding global loads, stores, atomics or LDS DMA (which __syncthreads would).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---- residual fixed point --------------------------------------------------------------
 #define FX_COUNT (1ull << 56)
@@ -112,21 +116,10 @@ __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int
 struct SrcAcc {
   const uint64_t* base;   // row 0; rows are ILL_H apart
   int expect;
-  // One word to spin on before reading the whole row: the last row tile is written last by
-  // every contributor, so polling it keeps traffic off the lines still receiving atomics.
-  __device__ __forceinline__ bool sentinel(int t) const {
-    return fx_count(aload64(base + (size_t)t * ILL_H + ILL_H - 1)) == expect;
-  }
-  __device__ __forceinline__ bool load(int t, int c0, float* v) const {
-    const uint64_t* p = base + (size_t)t * ILL_H + c0;
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const uint64_t w = aload64(p + i);
-      ok &= fx_count(w) == expect;
-      v[i] = fx_float(fx_value(w));
-    }
-    return ok;
+  __device__ __forceinline__ bool load1(int t, int c, float& v) const {
+    const uint64_t w = aload64(base + (size_t)t * ILL_H + c);
+    v = fx_float(fx_value(w));
+    return fx_count(w) == expect;
   }
 };
 
@@ -156,71 +149,11 @@ __device__ __forceinline__ float embed1(const IllWeights& W, int tok, int c) {
 struct SrcEmbed {
   IllWeights W;
   const int* toks;   // LDS copy of the row tokens
-  __device__ __forceinline__ bool sentinel(int) const { return true; }
-  __device__ __forceinline__ bool load(int t, int c0, float* v) const {
-    embed16(W, toks[t], c0, v);
+  __device__ __forceinline__ bool load1(int t, int c, float& v) const {
+    v = embed1(W, toks[t], c);
     return true;
   }
 };
-
-// RMSNorm + 16-bit fixed-point coding of rows 0..nrows-1 of a K = 896 input into MFMA
-// operands. Row t is handled by wave t % 8 with the same instruction sequence for every
-// T: lane (G, kg) = (lane / 4, lane % 4), lanes 56-63 idle.
-template <int T, class Src>
-__device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds<T>& P,
-                                        IllCtl* ctl, int code) {
-  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int G = lane >> 2, kg = lane & 3;
-  const bool act = lane < 56;
-  const int c0 = 64 * G + 16 * kg;
-  float gm[16];   // norm weights, loaded before the wait
-#pragma unroll
-  for (int i = 0; i < 16; i++) gm[i] = act ? gld(gamma + c0 + i) : 0.f;
-  bool alive = true;
-  for (int t = w; t < T && alive; t += ILL_WAVES) {
-    if (t >= nrows) {
-      if (act) {
-        P.ahi[(G * 4 + kg) * T + t] = make_uint4(0, 0, 0, 0);
-        P.alo[(G * 4 + kg) * T + t] = make_uint4(0, 0, 0, 0);
-        if (kg == 0) P.sc[G * T + t] = make_float2(0.f, 0.f);
-      }
-      continue;
-    }
-    float v[16];
-    alive = wave_wait([&]() { return lane != 0 || src.sentinel(t); }, ctl, code);
-    if (!alive) break;
-    alive = wave_wait([&]() { return !act || src.load(t, c0, v); }, ctl, code);
-    if (!alive) break;
-    if (!act) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) v[i] = 0.f;
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) ss = fmaf(v[i], v[i], ss);
-    ss = gsum<64>(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)ILL_H + ILL_EPS);
-    if (act) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) v[i] = v[i] * scale * gm[i];
-    }
-    float mx = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
-    mx = gmax<4>(mx);
-    const float d = mx / ILL_QMAX;
-    uint32_t hi[4], lo[4];
-    int sq;
-    quant16(v, d, hi, lo, sq);
-    sq = gsumi<4>(sq);
-    if (act) {
-      P.ahi[(G * 4 + kg) * T + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-      P.alo[(G * 4 + kg) * T + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-      if (kg == 0) P.sc[G * T + t] = make_float2(d, d * (float)sq);
-    }
-  }
-  return !__syncthreads_or(!alive);
-}
 
 __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
 
@@ -228,18 +161,95 @@ __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 
 // lane (kg, m = row) of the operand holds units 16 kg + q4perm(p); operand k-group gi of
 // row t is at [gi * T + t].
 template <int T>
-__device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* alo, float2* dsc) {
-  const int lane = tid_opaque() & 63;
-  const float mx = gmax<64>(fabsf(h));
-  const float d = mx / ILL_QMAX;
-  const int qv = (int)rintf(h * (d > 0.f ? 1.0f / d : 0.f));
-  const int sq = gsumi<64>(qv);
+__device__ __forceinline__ void quant_store(int qv, float d, int sq, int t, uint4* ahi, uint4* alo, float2* dsc, int gi, int p, int lane) {
   const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
-  const int gi = lane >> 4, p = q4perm_inv(lane & 15);
   ((uint8_t*)&ahi[gi * T + t])[p] = (uint8_t)(hi & 0xff);
   ((uint8_t*)&alo[gi * T + t])[p] = (uint8_t)(lo & 0xff);
   if (lane == 0) dsc[t] = make_float2(d, d * (float)sq);
 }
+template <int T>
+__device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* alo, float2* dsc, int lane) {
+  const float mx = gmax<64>(fabsf(h));
+  const float d = mx * (1.0f / ILL_QMAX);
+  const int qv = (int)rintf(h * (d > 0.f ? __builtin_amdgcn_rcpf(d) : 0.f));
+  const int sq = gsumi<64>(qv);
+  quant_store<T>(qv, d, sq, t, ahi, alo, dsc, lane >> 4, q4perm_inv(lane & 15), lane);
+}
+
+// RMSNorm + 16-bit fixed-point coding of rows 0..nrows-1 of a K = 896 input into MFMA
+// operands, spread over the whole workgroup: wave w owns column groups w and w + 8 (< 14)
+// of every row, one column per lane. Every wave polls its own columns until they are
+// complete, so the input is taken one memory round trip after its last contribution
+// lands. Rows >= nrows are coded as zeros. Per row: ss = sum over waves (in order) of the
+// wave's sum of squares; x * rsqrt(ss / 896 + eps) * gamma; each group coded as in
+// quant_row64. The sequence for a row does not depend on T.
+template <int T, class Src>
+__device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds<T>& P,
+                                        IllCtl* ctl, int code, const IllPassArgs& a, int trs = -1) {
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int G1 = w + ILL_WAVES;
+  const bool two = G1 < 14;   // wave-uniform
+  const int c0 = 64 * w + lane, c1 = 64 * (two ? G1 : w) + lane;
+  const float g0 = gld(gamma + c0), g1 = gld(gamma + c1);
+  float v0[T], v1[T];
+  const bool alive = wave_wait([&]() {
+    bool ok = true;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      v0[t] = 0.f;
+      v1[t] = 0.f;
+      if (t < nrows) {
+        ok &= src.load1(t, c0, v0[t]);
+        if (two) ok &= src.load1(t, c1, v1[t]);
+      }
+    }
+    return ok;
+  }, ctl, code);
+  if (trs >= 0) trace_mark(a, trs);
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const float s = gsum<64>(v0[t] * v0[t] + v1[t] * v1[t]);
+    if (lane == 0) P.red[w][t] = s;
+  }
+  if (lane == 0) P.ok[w] = alive;
+  lds_barrier();
+  bool all = true;
+#pragma unroll
+  for (int ww = 0; ww < ILL_WAVES; ww++) all &= P.ok[ww] != 0;
+  if (!all) return false;
+  // stage by stage over all rows, so the rows' reduction chains interleave
+  float m0[T], m1[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    float ss = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < ILL_WAVES; ww++) ss += P.red[ww][t];
+    const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / (float)ILL_H) + ILL_EPS);
+    v0[t] = v0[t] * scale * g0;
+    v1[t] = v1[t] * scale * g1;
+    m0[t] = gmax<64>(fabsf(v0[t]));
+    m1[t] = gmax<64>(fabsf(v1[t]));
+  }
+  int q0[T], q1[T], s0[T], s1[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const float d0 = m0[t] * (1.0f / ILL_QMAX), d1 = m1[t] * (1.0f / ILL_QMAX);
+    q0[t] = (int)rintf(v0[t] * (d0 > 0.f ? __builtin_amdgcn_rcpf(d0) : 0.f));
+    q1[t] = (int)rintf(v1[t] * (d1 > 0.f ? __builtin_amdgcn_rcpf(d1) : 0.f));
+    s0[t] = gsumi<64>(q0[t]);
+    s1[t] = gsumi<64>(q1[t]);
+  }
+  const int gi = lane >> 4, p = q4perm_inv(lane & 15);
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    quant_store<T>(q0[t], m0[t] * (1.0f / ILL_QMAX), s0[t], t, P.ahi + w * 4 * T, P.alo + w * 4 * T, P.sc + w * T, gi, p, lane);
+    if (two) quant_store<T>(q1[t], m1[t] * (1.0f / ILL_QMAX), s1[t], t, P.ahi + G1 * 4 * T, P.alo + G1 * 4 * T, P.sc + G1 * T, gi, p, lane);
+  }
+  if (trs >= 0) trace_mark(a, trs + 1);
+  lds_barrier();
+  return true;
+}
+
 
 // ---- weight staging in LDS ----------------------------------------------------------------
 // Each role copies the next layer's weights HBM -> LDS (global_load_lds) as soon as it has
@@ -338,10 +348,6 @@ __device__ __forceinline__ void att_stage_o(const IllLayerW& L, int h, int w, in
   split_stage(L.wo + (size_t)h * ILL_NOT * 512, L.so + h * ILL_NOT * 16, w, lane, stage + ill_st_o(T) + w * ILL_ST_SPLIT);
 }
 
-// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations but not for
-// its outstanding global loads, stores, atomics or LDS DMA (which __syncthreads would).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -421,8 +427,8 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
   const int Lt = part ? pos + H.depth[t1] + 1 : 0x7fffffff;
   const uint4 zz = make_uint4(0, 0, 0, 0);
   // pass rows on row t1's path for this lane's key positions
-  int rk[4];
-  if (part) {
+  int rk[4] = {0, 0, 0, 0};   // at T = 1 the only pass row is row 0 at position pos
+  if (T > 1 && part) {
 #pragma unroll
     for (int b = 0; b < 4; b++) rk[b] = min(H.prow[t1][min(max(64 * c + 16 * b + n - pos, 0), 15)], T - 1);
   }
@@ -490,7 +496,19 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       uint4 u = f.v[nb][ks];
-      if (part) {
+      if (T == 1 && part) {
+        // the new position pos holds the pass row; later positions hold no key
+        const uint32_t lv = A.v[0][dim];
+        uint32_t e[8];
+        const uint32_t x[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int d = 64 * c + 32 * ks + 8 * kg + i - pos;
+          const uint32_t cv = (x[i >> 1] >> (16 * (i & 1))) & 0xffff;
+          e[i] = msel(mask_of(d < 0), cv, lv & mask_of(d == 0));
+        }
+        u = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+      } else if (part) {
         // positions >= pos: row t1's path table (zero beyond its depth); positions >= pos + 16 hold no key
         const uint16_t* vpt = (const uint16_t*)(stage + ILL_ST_VPT) + ((size_t)t1 * 64 + dim) * 16;
         uint32_t e[8];
@@ -630,13 +648,18 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   int fc = -1;   // cache chunk held in f
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
-  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
-  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_XB_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l);
+  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
+  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_XB_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
   // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
   float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
   wait_vm();   // every wave: its staged weights and the epilogue constants (nothing else is in flight)
+  // pin the epilogue constants here: a load sunk to its use would be issued after the K/V
+  // fetch below, and waiting for it would then wait for the whole fetch
+  asm volatile("" ::"v"(bias0), "v"(bias1));
+#pragma unroll
+  for (int j = 0; j < RPL; j++) asm volatile("" ::"v"(rope[j].x), "v"(rope[j].y));
   trace_mark(a, ILL_TRL * l + 2);
   if (w < 6) {
     const uint8_t* st = stage + w * ILL_ST_QKV;
@@ -692,12 +715,16 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 4);
   if (T != 1) att_stage_o<T>(L, h, w, lane, stage);   // O weights stream in while attention runs
-  if (cmax >= ns) {   // partial chunks exist: path table of the pass rows' V
-    uint16_t* vpt = (uint16_t*)(stage + ILL_ST_VPT);
-    for (int i = tid; i < T * 64 * 16; i += ILL_WG_THREADS) {
-      const int t1 = i >> 10, dim = (i >> 4) & 63, dd = i & 15;
-      const bool on = t1 < nrows && dd <= H.depth[t1];
-      vpt[i] = on ? A.v[min(H.prow[t1][dd], T - 1)][dim] : (uint16_t)0;
+  if (T > 1 && cmax >= ns) {   // partial chunks exist: path table of the pass rows' V
+    uint4* vpt = (uint4*)(stage + ILL_ST_VPT);
+    for (int i = tid; i < T * 64; i += ILL_WG_THREADS) {   // (row t1, dim): 16 depths
+      const int t1 = i >> 6, dim = i & 63;
+      const int dep = t1 < nrows ? H.depth[t1] : -1;
+      uint32_t e[16];
+#pragma unroll
+      for (int dd = 0; dd < 16; dd++) e[dd] = dd <= dep ? (uint32_t)A.v[min(H.prow[t1][dd], T - 1)][dim] : 0u;
+      vpt[2 * i] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+      vpt[2 * i + 1] = make_uint4(e[8] | (e[9] << 16), e[10] | (e[11] << 16), e[12] | (e[13] << 16), e[14] | (e[15] << 16));
     }
     lds_barrier();
   }
@@ -767,6 +794,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   }
   trace_mark(a, ILL_TRL * l + 6);
   lds_barrier();   // LDS: P region becomes the combine region
+  trace_mark(a, ILL_TRL * l + 13);
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int t = 4 * kg + j;
@@ -780,6 +808,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     }
   }
   lds_barrier();
+  trace_mark(a, ILL_TRL * l + 14);
   // combine: wave states (+ the partial chunks of each wave, in chunk order), then across
   // waves against the global maximum
   for (int i = tid_opaque(); i < nrows * 64; i += ILL_WG_THREADS) {
@@ -818,7 +847,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   trace_mark(a, ILL_TRL * l + 7);
   // ---- O projection restricted to head h's columns (one quant group): rows t by wave t % 8
   for (int t = w; t < T; t += ILL_WAVES) {
-    if (t < nrows) quant_row64<T>(A.o[t][lane], t, A.ahi, A.alo, A.dsc);
+    if (t < nrows) quant_row64<T>(A.o[t][lane], t, A.ahi, A.alo, A.dsc, lane);
     else if (lane < 4) {
       A.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
       A.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
@@ -830,6 +859,10 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   trace_mark(a, ILL_TRL * l + 9);
   split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows, acc_ptr(a, H.bank, l, 0, 0) + 16 * 7 * w);
   trace_mark(a, ILL_TRL * l + 10);
+  if (a.trace) {   // traced runs only: when this wave's contributions have landed
+    wait_vm();
+    trace_mark(a, ILL_TRL * l + 12);
+  }
   return true;
 }
 
@@ -849,7 +882,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   const IllLayerW& L = a.L[l];
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
-  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_XA_N}, L.ln2, nrows, G.prep, a.ctl, 400 + l)) return false;
+  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_XA_N}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, ILL_TRL * l + 6)) return false;
   trace_mark(a, ILL_TRL * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -871,7 +904,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
     if (t < nrows) {
       const int gi = lane >> 4, nn = lane & 15;
       const float gv = G.gu[gi][t][nn], up = G.gu[4 + gi][t][nn];
-      quant_row64<T>(gv / (1.0f + expf(-gv)) * up, t, G.ahi, G.alo, G.dsc);
+      quant_row64<T>(gv / (1.0f + expf(-gv)) * up, t, G.ahi, G.alo, G.dsc, lane);
     } else if (lane < 4) {
       G.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
       G.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
@@ -882,6 +915,10 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
                 acc_ptr(a, H.bank, l, 1, 0) + 16 * 7 * w);
   trace_mark(a, ILL_TRL * l + 10);
+  if (a.trace) {   // traced runs only: when this wave's contributions have landed
+    wait_vm();
+    trace_mark(a, ILL_TRL * l + 12);
+  }
   return true;
 }
 
@@ -953,7 +990,7 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_XB_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600)) return false;
+    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_XB_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {

@@ -35,6 +35,11 @@ Q4_MATRIX_BYTES = 277_853_184     # q4 codes + scales of every matrix incl. the 
 F32_NORM_BIAS_BYTES = 286_208     # f32 norms + QKV biases as stored in .ill v1
 EMBED_ROW_BYTES = 504             # one q4 embedding row (448 B codes + 56 B scales)
 KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
+# HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
+# a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
+# (165,954.4 x 2 + 16,022.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 356_281_280
 
 
 def step_bytes(L: float) -> float:
@@ -44,12 +49,7 @@ def step_bytes(L: float) -> float:
 
 def model_path(fmt: int, seed: int) -> str:
     from instantllm_amd import synth
-    d = Path(os.environ.get("ILL_MODEL_DIR", "/tmp/ill_models"))
-    d.mkdir(parents=True, exist_ok=True)
-    p = d / f"qwen05b_fmt{fmt}_seed{seed}.ill"
-    if not p.exists():
-        synth.build_model(str(p), fmt, seed)
-    return str(p)
+    return synth.cached_model(fmt, seed)
 
 
 def cpu_baseline(path: str, prompt: list[int], n_decode: int) -> dict:
@@ -105,7 +105,7 @@ def main() -> int:
         return 0
     from instantllm_amd import illfile as F
     from instantllm_amd.engine import Engine
-    from oracle.tree import random_tree
+    from instantllm_amd.synth import random_tree
 
     path = model_path(F.FMT_Q4, 2)
     rng = np.random.default_rng(2)
@@ -178,9 +178,11 @@ def main() -> int:
                                "FFN 4864, vocab 151936), prefix KV 256, each step one persistent kernel in a hipGraph",
                    "prefix": len(prompt), "model_seed": 2, "first_tokens": toks[:8]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_STEP,
                      "note": f"bytes(L)={step_bytes(L_avg):.0f} at mean L={L_avg:.1f}; dominant kernel "
-                             "ill_pass_kernel<1> (the whole step), duration from HIP events over the timed graph"},
+                             "ill_pass_kernel<1> (the whole step), duration from HIP events over the timed graph; "
+                             "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE "
+                             "(profiles/pass_kernel_q4_decode_config2.md)"},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(path, prompt[:48], args.cpu_steps)

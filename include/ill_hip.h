@@ -103,8 +103,9 @@ int ill_last_pass_ms(ill_engine* e, float* ms);
 
 /* Per-workgroup timeline of the pass kernel (the persistent-kernel counterpart of
  * Engine.profile's per-kernel times): when on, thread 0 of every workgroup stores the
- * 100 MHz device clock at the start, input-ready and done points of its role in every
- * layer (slots 3l, 3l+1, 3l+2), of the lm_head (3*30 .. +2) and of the commit (+3 .. +5).
+ * 100 MHz device clock at points of its role in every layer l (slot 16 l + k: k = 0 role
+ * start, 1 input ready, 11 done, 2-10 and 12-15 role-specific intermediate points), and
+ * of the lm_head and commit tail (slots 480 + k). Unreached slots stay 0.
  * ill_trace_read copies [256][slots] u64 values of the last pass and returns `slots`. */
 int ill_trace_enable(ill_engine* e, int on);
 int ill_trace_read(ill_engine* e, uint64_t* out, int* slots);

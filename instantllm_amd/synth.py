@@ -192,3 +192,47 @@ def microbench_x(seed: int, cols: int, rows: int = 1) -> tuple[np.ndarray, np.nd
     x = g.standard_normal((rows, cols), dtype=np.float32).astype(np.float16).astype(np.float32)
     gamma = (1.0 + 0.1 * g.standard_normal(cols, dtype=np.float32)).astype(np.float32)
     return x, gamma
+
+
+def tree_buffer(parent: list[int], tok: list[int]) -> np.ndarray:
+    """The 65-int tree buffer of a verify pass, [n, depth[16], parent[16], tok[16], anc[16]]
+    (Sources/Engine/Shaders.swift:23-30), from parent indices (parent[0] ignored)."""
+    n = len(tok)
+    if not (1 <= n <= 16 and len(parent) == n):
+        raise ValueError("a tree has 1..16 rows")
+    t = np.zeros(65, np.int32)
+    t[0] = n
+    depth, anc = [0] * n, [1] * n
+    for i in range(1, n):
+        p = parent[i]
+        if not 0 <= p < i:
+            raise ValueError(f"parent[{i}] = {p} is not an earlier row")
+        depth[i] = depth[p] + 1
+        anc[i] = anc[p] | (1 << i)
+    t[1:1 + n] = depth
+    t[17:17 + n] = [0] + list(parent[1:])
+    t[33:33 + n] = tok
+    t[49:49 + n] = anc
+    return t
+
+
+def random_tree(rng: np.random.Generator, n: int, vocab: int) -> np.ndarray:
+    """Config 3 tree: parent[i] uniform over rows 0..i-1, tokens uniform in [0, vocab)."""
+    parent = [0] + [int(rng.integers(0, i)) for i in range(1, n)]
+    tok = [int(t) for t in rng.integers(0, vocab, size=n)]
+    return tree_buffer(parent, tok)
+
+
+def cached_model(fmt: int, seed: int, shape: ModelShape = ModelShape(), directory: str | None = None) -> str:
+    """Path of the seeded synthetic model, generated once into `directory`
+    (default $ILL_MODEL_DIR or /tmp/ill_models)."""
+    import os
+    d = directory or os.environ.get("ILL_MODEL_DIR", "/tmp/ill_models")
+    os.makedirs(d, exist_ok=True)
+    tag = "" if shape == ModelShape() else f"_L{shape.layers}_V{shape.vocab}"
+    p = os.path.join(d, f"qwen05b_fmt{fmt}_seed{seed}{tag}.ill")
+    if not os.path.exists(p):
+        tmp = p + f".tmp{os.getpid()}"
+        build_model(tmp, fmt, seed, shape=shape)
+        os.replace(tmp, p)
+    return p

@@ -1,0 +1,108 @@
+"""GPU checks on the full Qwen2.5-0.5B-shaped q4 model (24 layers, vocabulary 151936),
+through the C ABI.
+
+* a short greedy decode against the fp32 oracle on the same dequantized weights
+  (per-step logits relative L2 <= 1e-2, commits equal the argmax of the row's logits);
+* config 3: a 16-row tree-verify pass at prefix 512 whose every row's logits equal, bit
+  for bit, the 1-row step of the same token after its ancestors;
+* a hipGraph of decode steps equals the same steps launched one by one.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from instantllm_amd import synth, illfile as F
+from oracle import illread, qwen, metrics, tree as T
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 1e-2
+NO_EOS = (-5, -5)
+
+
+def log(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def full_q4():
+    log("full q4 model (seed 2): generate or reuse")
+    return synth.cached_model(F.FMT_Q4, 2)
+
+
+@pytest.fixture(scope="module")
+def engine(full_q4):
+    from instantllm_amd.engine import Engine
+    log("engine: create full q4")
+    e = Engine(full_q4, max_context=1024, max_pass=16, max_steps=512)
+    yield e
+    e.close()
+
+
+def test_fullsize_decode_matches_oracle(engine, full_q4):
+    log("oracle: dequantize the full model")
+    m = qwen.Model(illread.load(full_q4))
+    rng = np.random.default_rng(0)
+    prompt = [int(t) for t in rng.integers(0, F.VOCAB, size=48)]
+    engine.reset_out_tokens()
+    engine.set_state(pos=0, n=len(prompt), maxsteps=64, eos=NO_EOS)
+    log("prefill 48 + 6 decode steps")
+    engine.prefill(prompt, write_logits=True)
+    cache = m.new_cache(64)
+    ref = m.forward(prompt, cache)
+    lg = engine.read_logits(0)
+    assert metrics.rel_l2(lg, ref) <= REL_L2_TOL
+    tok = int(engine.out_tokens()[0])
+    assert tok == int(np.argmax(lg))
+    for s in range(6):
+        engine.decode_step(write_logits=True)
+        lg = engine.read_logits(0)
+        ref = m.forward([tok], cache)
+        assert metrics.rel_l2(lg, ref) <= REL_L2_TOL, s
+        nxt = int(engine.out_tokens()[s + 1])
+        assert nxt == int(np.argmax(lg))
+        tok = nxt
+
+
+def test_fullsize_tree_rows_bit_identical_prefix512(engine):
+    rng = np.random.default_rng(3)
+    ctx = [int(t) for t in rng.integers(0, F.VOCAB, size=512)]
+    engine.reset_out_tokens()
+    engine.set_state(pos=0, n=512, maxsteps=200, eos=NO_EOS)
+    log("prefill 512")
+    engine.prefill(ctx)
+    st = engine.get_state()
+    tr = synth.random_tree(rng, 16, F.VOCAB)
+    tr[T.TR_TOK] = int(engine.out_tokens()[0])
+    engine.set_state(pos=st["pos"], n=16, maxsteps=200, eos=NO_EOS)
+    log("tree verify pass at pos", st["pos"])
+    engine.verify_pass(16, tree=tr, write_logits=True)
+    rows = np.stack([engine.read_logits(r) for r in range(16)])
+    tok = tr[T.TR_TOK:T.TR_TOK + 16]
+    for p in T.paths(tr):
+        for k, r in enumerate(p):
+            engine.set_state(pos=st["pos"] + k, n=1, maxsteps=200, eos=NO_EOS)
+            engine.prefill([int(tok[r])], write_logits=True)
+            one = engine.read_logits(0)
+            assert np.array_equal(one.view(np.uint32), rows[r].view(np.uint32)), (p, k, r)
+
+
+def test_fullsize_graph_equals_single_steps(engine):
+    rng = np.random.default_rng(5)
+    prompt = [int(t) for t in rng.integers(0, F.VOCAB, size=33)]
+    outs = []
+    for graph in (True, False):
+        engine.reset_out_tokens()
+        engine.set_state(pos=0, n=len(prompt), maxsteps=17, eos=NO_EOS)
+        engine.prefill(prompt)
+        if graph:
+            engine.capture_steps(16)
+            engine.launch_graph()
+            engine.sync()
+        else:
+            for _ in range(16):
+                engine.decode_step()
+        outs.append(engine.out_tokens()[:17].copy())
+        assert engine.get_state()["pos"] == len(prompt) + 16
+    assert np.array_equal(outs[0], outs[1])

@@ -214,3 +214,14 @@ def test_q4_dequant_closed_form():
     assert np.abs(codes).max() <= 127
     deq = codes.astype(np.float32).reshape(3, 4, 32) * sc.astype(np.float32)[..., None]
     assert np.abs(deq.reshape(3, 128) - w).max() <= sc.astype(np.float32).max() * 0.5 + 1e-7
+
+
+def test_tree_buffer_builder_matches_oracle():
+    """The package's tree-buffer builder (bench inputs) encodes trees as the oracle does."""
+    from instantllm_amd import synth
+    for seed in range(20):
+        a = synth.random_tree(np.random.default_rng(seed), 16, 151936)
+        b = T.random_tree(np.random.default_rng(seed), 16, 151936)
+        assert np.array_equal(a, b)
+    with pytest.raises(ValueError):
+        synth.tree_buffer([0, 1], [5, 6])   # row 1's parent must be an earlier row

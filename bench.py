@@ -77,6 +77,35 @@ def cpu_baseline(path: str, prompt: list[int], n_decode: int) -> dict:
     }
 
 
+GEMV_SHAPES = (   # config 1: (name, rows, K, RMSNorm prologue, argmax epilogue)
+    ("qkv", 1152, 896, True, False),
+    ("gate_up", 9728, 896, True, False),
+    ("down", 896, 4864, False, False),
+    ("lm_head", 151936, 896, True, True),
+)
+
+
+def gemv_config1() -> dict:
+    """Config 1: the q4 GEMV on its own, each shape with enough rotated weight copies to
+    exceed 512 MB (past the 256 MB MALL). Bytes per run = codes + (scale, min) pairs."""
+    from instantllm_amd import synth
+    from instantllm_amd.engine import Gemv
+    out = {}
+    for name, rows, K, norm, amax in GEMV_SHAPES:
+        codes, sb = synth.microbench_q4(1, rows, K)
+        x, gamma = synth.microbench_x(1, K)
+        nbytes = rows * K // 2 + rows * (K // 64) * 4
+        copies = max(2, -(-(512 << 20) // nbytes) + 1)
+        g = Gemv(codes, np.ascontiguousarray(sb).view(np.uint32).reshape(rows, K // 64), copies=copies)
+        _, _, us = g.run(x[0], gamma if norm else None, iters=max(copies, 20), argmax=amax)
+        info = g.info()
+        g.close()
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"rows": rows, "K": K, "bytes": nbytes, "us": round(us, 2), "GBps": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies, "slices": info["slices"]}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -85,6 +114,7 @@ def main() -> int:
     ap.add_argument("--prefix", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV microbench")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (the reference dispatch "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -184,6 +214,8 @@ def main() -> int:
                              "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE "
                              "(profiles/pass_kernel_q4_decode_config2.md)"},
     }
+    if not args.no_gemv:
+        line["gemv_config1"] = gemv_config1()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(path, prompt[:48], args.cpu_steps)
     print(json.dumps(line), flush=True)

@@ -110,6 +110,21 @@ int ill_last_pass_ms(ill_engine* e, float* ms);
 int ill_trace_enable(ill_engine* e, int on);
 int ill_trace_read(ill_engine* e, uint64_t* out, int* slots);
 
+/* Stand-alone q4 GEMV, the decode step's matrix-vector product measured on its own
+ * The reference has no separate entry for it: it times the same
+ * kernels (q4_chunk_norm / q_rows, k_lm_head_T; Shaders.swift:1001-1185, :1327-1364) inside
+ * Engine.profile (Engine.swift:639-729). codes [rows][K/2] and scales [rows][K/64] (f16
+ * scale | f16 min << 16) are the .ill q4 layout; `copies` device copies of the weights are
+ * rotated through so that repeated runs stream from HBM rather than the 256 MB MALL.
+ * ill_gemv_run: y = W * rmsnorm(x) * gamma (gamma NULL: y = W * x), `iters` timed runs;
+ * y (host [rows], optional) and argmax (host, optional: lowest index of the maximum,
+ * which also enables the argmax epilogue) are from the last run. */
+typedef struct ill_gemv ill_gemv;
+int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* scales, int copies, ill_gemv** out);
+int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, float* y, int32_t* argmax, float* us_per_iter);
+int ill_gemv_info(const ill_gemv* g, int* slices, int* blocks_per_slice, int64_t* bytes_per_copy);
+int ill_gemv_destroy(ill_gemv* g);
+
 #ifdef __cplusplus
 }
 #endif

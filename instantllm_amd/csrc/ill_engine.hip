@@ -19,6 +19,7 @@
 
 #include "../../include/ill_hip.h"
 #include "ill_pass.h"
+#include "ill_gemv.h"
 
 namespace {
 
@@ -701,6 +702,136 @@ int ill_last_pass_ms(ill_engine* e, float* ms) {
   if (!e || !ms) return fail(ILL_E_ARG, "null argument");
   HCK(hipEventSynchronize(e->ev1));
   HCK(hipEventElapsedTime(ms, e->ev0, e->ev1));
+  return ILL_OK;
+}
+
+// ---- stand-alone q4 GEMV (microbench of the decode step's matrix-vector product) -------
+struct ill_gemv {
+  int rows = 0, K = 0, nb = 0, bps = 1, ks = 1, copies = 0;
+  std::vector<uint8_t*> w;
+  std::vector<uint32_t*> s;
+  float* x = nullptr;
+  float* gamma = nullptr;
+  float* part = nullptr;
+  float* y = nullptr;
+  uint64_t* key = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+};
+
+int ill_gemv_destroy(ill_gemv* g) {
+  if (!g) return ILL_OK;
+  if (g->stream) hipStreamSynchronize(g->stream);
+  for (auto p : g->w) hipFree(p);
+  for (auto p : g->s) hipFree(p);
+  hipFree(g->x);
+  hipFree(g->gamma);
+  hipFree(g->part);
+  hipFree(g->y);
+  hipFree(g->key);
+  if (g->e0) hipEventDestroy(g->e0);
+  if (g->e1) hipEventDestroy(g->e1);
+  if (g->stream) hipStreamDestroy(g->stream);
+  delete g;
+  return ILL_OK;
+}
+
+int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* sb, int copies, ill_gemv** out) {
+  if (!out) return fail(ILL_E_ARG, "null output handle");
+  *out = nullptr;
+  if (!codes || !sb || rows < 16 || rows % 16 || K < 128 || K % 128 || K > 64 * ILL_GEMV_MAXG || copies < 1)
+    return fail(ILL_E_ARG, "gemv shape %d x %d (rows: multiple of 16; K: multiple of 128, <= %d), copies %d",
+                rows, K, 64 * ILL_GEMV_MAXG, copies);
+  ill_gemv* g = new ill_gemv();
+  auto bad = [&](int rc) { ill_gemv_destroy(g); return rc; };
+  g->rows = rows;
+  g->K = K;
+  g->nb = K / 128;
+  g->copies = copies;
+  const int ntile = rows / 16;
+  // enough (tile, slice) items for every wave of the grid, at most 8 blocks per slice
+  int ks = std::min(g->nb, (ILL_WG * ILL_WAVES + ntile - 1) / ntile);
+  int bps = (g->nb + ks - 1) / ks;
+  if (bps > ILL_GEMV_MAXBPS) bps = ILL_GEMV_MAXBPS;
+  g->bps = bps;
+  g->ks = (g->nb + bps - 1) / bps;
+  std::vector<int> order(rows);
+  for (int i = 0; i < rows; i++) order[i] = i;
+  std::vector<uint8_t> hw((size_t)ntile * g->nb * 1024);
+  std::vector<uint32_t> hs((size_t)ntile * g->nb * 32);
+  repack_rows(codes, sb, K, order, hw.data(), hs.data());
+  if (hipSetDevice(0) != hipSuccess) return bad(fail(ILL_E_HIP, "no HIP device"));
+  for (int c = 0; c < copies; c++) {
+    uint8_t* pw = nullptr;
+    uint32_t* ps = nullptr;
+    if (hipMalloc(&pw, hw.size()) != hipSuccess || hipMalloc(&ps, hs.size() * 4) != hipSuccess) {
+      if (pw) hipFree(pw);
+      return bad(fail(ILL_E_HIP, "weight copy %d allocation failed", c));
+    }
+    g->w.push_back(pw);
+    g->s.push_back(ps);
+    if (hipMemcpy(pw, hw.data(), hw.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ps, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bad(fail(ILL_E_HIP, "weight copy %d upload failed", c));
+  }
+  if (hipMalloc(&g->x, (size_t)K * 4) != hipSuccess || hipMalloc(&g->gamma, (size_t)K * 4) != hipSuccess ||
+      hipMalloc(&g->part, (size_t)g->ks * rows * 4) != hipSuccess || hipMalloc(&g->y, (size_t)rows * 4) != hipSuccess ||
+      hipMalloc(&g->key, 8) != hipSuccess)
+    return bad(fail(ILL_E_HIP, "gemv buffer allocation failed"));
+  if (hipStreamCreate(&g->stream) != hipSuccess || hipEventCreate(&g->e0) != hipSuccess || hipEventCreate(&g->e1) != hipSuccess)
+    return bad(fail(ILL_E_HIP, "stream / event creation failed"));
+  *out = g;
+  return ILL_OK;
+}
+
+int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, float* y, int32_t* amax, float* us_per_iter) {
+  if (!g || !x || iters < 1) return fail(ILL_E_ARG, "bad gemv run arguments");
+  HCK(hipMemcpyAsync(g->x, x, (size_t)g->K * 4, hipMemcpyHostToDevice, g->stream));
+  if (gamma) HCK(hipMemcpyAsync(g->gamma, gamma, (size_t)g->K * 4, hipMemcpyHostToDevice, g->stream));
+  HCK(hipStreamSynchronize(g->stream));
+  IllGemvArgs a{};
+  a.x = g->x;
+  a.gamma = gamma ? g->gamma : nullptr;
+  a.part = g->part;
+  a.rows = g->rows;
+  a.K = g->K;
+  a.bps = g->bps;
+  a.ks = g->ks;
+  const int fin_blocks = (g->rows + 255) / 256;
+  auto one = [&](int c) -> int {
+    a.w = g->w[c];
+    a.s = g->s[c];
+    if (amax) HCK(hipMemsetAsync(g->key, 0, 8, g->stream));
+    hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
+    hipLaunchKernelGGL(ill_gemv_finish_kernel, dim3(fin_blocks), dim3(256), 0, g->stream, (const float*)g->part, g->ks,
+                       g->rows, g->y, amax ? g->key : (uint64_t*)nullptr);
+    HCK(hipGetLastError());
+    return 0;
+  };
+  int rc = one(0);   // warm
+  if (rc) return rc;
+  HCK(hipEventRecord(g->e0, g->stream));
+  for (int i = 0; i < iters; i++)
+    if ((rc = one(i % g->copies))) return rc;
+  HCK(hipEventRecord(g->e1, g->stream));
+  HCK(hipEventSynchronize(g->e1));
+  float ms = 0.f;
+  HCK(hipEventElapsedTime(&ms, g->e0, g->e1));
+  if (us_per_iter) *us_per_iter = ms * 1e3f / (float)iters;
+  if (y) HCK(hipMemcpy(y, g->y, (size_t)g->rows * 4, hipMemcpyDeviceToHost));
+  if (amax) {
+    uint64_t k = 0;
+    HCK(hipMemcpy(&k, g->key, 8, hipMemcpyDeviceToHost));
+    *amax = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
+  }
+  return ILL_OK;
+}
+
+int ill_gemv_info(const ill_gemv* g, int* slices, int* blocks_per_slice, int64_t* bytes_per_copy) {
+  if (!g) return fail(ILL_E_ARG, "null gemv");
+  if (slices) *slices = g->ks;
+  if (blocks_per_slice) *blocks_per_slice = g->bps;
+  if (bytes_per_copy) *bytes_per_copy = (int64_t)g->rows * g->K / 2 + (int64_t)g->rows * (g->K / 64) * 4;
   return ILL_OK;
 }
 

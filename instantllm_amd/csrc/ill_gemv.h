@@ -1,0 +1,167 @@
+// Stand-alone q4 GEMV (the matrix-vector product of the decode step, measured on its own):
+// y = W x for a q4 affine group-64 matrix W [rows][K] in the row-tile layout of the pass
+// kernel, with the RMSNorm of x fused into the prologue (or a plain input, as the down
+// projection takes) and an optional argmax epilogue (value, lowest index), as the lm_head
+// uses it.
+//
+// Reference semantics: q4_chunk_norm / q_rows / reduce8 and k_lm_head_T
+// (Sources/Engine/Shaders.swift:1001-1054, :1143-1185, :1327-1364). Arithmetic is the pass
+// kernel's: x coded per 64-column group as 16-bit fixed point (int8 hi/lo), int8 MFMA
+// against the nibbles (exact int32), fp32 group epilogue s*d*S + m*d*sum(v).
+//
+// Work split: a wave takes one (row tile, K slice) item at a time and keeps the next
+// item's weight loads in flight while it computes the current one. With more than one
+// slice per tile the slices write fp32 partials [slice][row] and a second kernel sums them
+// in slice order (deterministic) and reduces the argmax.
+#pragma once
+#include "ill_device.h"
+
+#define ILL_GEMV_MAXG 128           // K <= 8192
+#define ILL_GEMV_MAXBPS 8           // blocks (128 columns) per slice
+
+struct IllGemvArgs {
+  const uint8_t* w;      // [ntile][nb] 1 KiB blocks
+  const uint32_t* s;     // [ntile][nb][16][2] (scale, min) f16 pairs
+  const float* x;        // [K]
+  const float* gamma;    // [K] or nullptr (plain input)
+  float* part;           // [ks][rows]
+  int rows, K, bps, ks;  // blocks per slice, slices per tile
+};
+
+struct GemvLds {
+  uint4 ahi[ILL_GEMV_MAXG * 4];
+  uint4 alo[ILL_GEMV_MAXG * 4];
+  float2 sc[ILL_GEMV_MAXG];
+  float red[ILL_WAVES];
+};
+
+struct GemvItem {
+  uint4 w[ILL_GEMV_MAXBPS];
+  uint2 s[ILL_GEMV_MAXBPS];
+};
+
+__device__ __forceinline__ void gemv_fetch(const IllGemvArgs& a, int item, int lane, GemvItem& it) {
+  const int nb = a.K >> 7;
+  const int tile = item / a.ks, slice = item - tile * a.ks;
+  const int cb0 = slice * a.bps;
+  const int n = lane & 15;
+#pragma unroll
+  for (int i = 0; i < ILL_GEMV_MAXBPS; i++) {
+    const int cb = min(cb0 + i, nb - 1);   // in bounds; blocks past the slice are not used
+    if (i < a.bps) {
+      it.w[i] = gld((const uint4*)(a.w + ((size_t)tile * nb + cb) * 1024) + lane);
+      it.s[i] = gld((const uint2*)(a.s + ((size_t)tile * nb + cb) * 32) + n);
+    }
+  }
+}
+
+__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvArgs a) {
+  __shared__ GemvLds L;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int nb = a.K >> 7, ng = a.K >> 6;
+  const int nitems = (a.rows >> 4) * a.ks;
+  const int stride = gridDim.x * ILL_WAVES;
+  int item = blockIdx.x * ILL_WAVES + w;
+  GemvItem cur;
+  if (item < nitems) gemv_fetch(a, item, lane, cur);   // weights stream while x is prepared
+  // ---- x: RMSNorm (sum of squares in a fixed order) and 16-bit coding per 64-column group
+  float scale = 1.f;
+  if (a.gamma) {
+    float ss = 0.f;
+    for (int c = tid; c < a.K; c += ILL_WG_THREADS) {
+      const float v = gld(a.x + c);
+      ss += v * v;
+    }
+    ss = gsum<64>(ss);
+    if (lane == 0) L.red[w] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < ILL_WAVES; ww++) tot += L.red[ww];
+    scale = __builtin_amdgcn_rsqf(tot / (float)a.K + ILL_EPS);
+  }
+  for (int g = w; g < ng; g += ILL_WAVES) {
+    const int c = 64 * g + lane;
+    float v = gld(a.x + c);
+    if (a.gamma) v = v * scale * gld(a.gamma + c);
+    const float mx = gmax<64>(fabsf(v));
+    const float d = mx * (1.0f / ILL_QMAX);
+    const int qv = (int)rintf(v * (d > 0.f ? __builtin_amdgcn_rcpf(d) : 0.f));
+    const int sq = gsumi<64>(qv);
+    const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
+    const int gi = lane >> 4;
+    const int p = (lane & 8) | ((lane & 1) << 2) | ((lane >> 1) & 3);   // inverse of q4perm
+    ((uint8_t*)&L.ahi[g * 4 + gi])[p] = (uint8_t)(hi & 0xff);
+    ((uint8_t*)&L.alo[g * 4 + gi])[p] = (uint8_t)(lo & 0xff);
+    if (lane == 0) L.sc[g] = make_float2(d, d * (float)sq);
+  }
+  __syncthreads();
+  // ---- items
+  const v4i z = {0, 0, 0, 0};
+  while (item < nitems) {
+    const int nxt = item + stride;
+    GemvItem nx;
+    if (nxt < nitems) gemv_fetch(a, nxt, lane, nx);
+    const int tile = item / a.ks, slice = item - tile * a.ks;
+    const int cb0 = slice * a.bps;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < ILL_GEMV_MAXBPS; i++) {
+      const int cb = cb0 + i;
+      if (i < a.bps && cb < nb) {
+#pragma unroll
+        for (int gi = 0; gi < 2; gi++) {
+          const int G = 2 * cb + gi;
+          const v4i b = gi == 0 ? q4_unpack(cur.w[i].x, cur.w[i].y) : q4_unpack(cur.w[i].z, cur.w[i].w);
+          const uint4 h = L.ahi[G * 4 + kg], l = L.alo[G * 4 + kg];
+          const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
+          const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
+          const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+          const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+          const uint32_t sm = gi == 0 ? cur.s[i].x : cur.s[i].y;
+          const float2 dx = L.sc[G];
+          const int S = (dh[0] << 8) + dl[0];
+          acc = fmaf(h2f(sm & 0xffff), dx.x * (float)S, acc);
+          acc = fmaf(h2f(sm >> 16), dx.y, acc);
+        }
+      }
+    }
+    if (kg == 0) gst(a.part + (size_t)slice * a.rows + 16 * tile + n, acc);
+    cur = nx;
+    item = nxt;
+  }
+}
+
+// Order-preserving 64-bit key of (value, index): larger value first, then lower index.
+__device__ __forceinline__ uint64_t amax_key(float v, int idx) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// y[r] = sum over slices in order; optional argmax into *key (atomic max of amax_key).
+__global__ __launch_bounds__(256) void ill_gemv_finish_kernel(const float* part, int ks, int rows, float* y, uint64_t* key) {
+  __shared__ uint64_t best[4];
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  uint64_t k = 0;
+  if (r < rows) {
+    float v = 0.f;
+    for (int s = 0; s < ks; s++) v += gld(part + (size_t)s * rows + r);
+    gst(y + r, v);
+    k = amax_key(v, r);
+  }
+  if (key) {
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t ok = __shfl_xor(k, o, 64);
+      k = ok > k ? ok : k;
+    }
+    if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t m = best[0];
+      for (int i = 1; i < 4; i++) m = best[i] > m ? best[i] : m;
+      __hip_atomic_fetch_max((GAS unsigned long long*)key, (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}

@@ -67,6 +67,10 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_last_pass_ms": (C.c_int, [P, C.POINTER(F32)]),
         "ill_trace_enable": (C.c_int, [P, C.c_int]),
         "ill_trace_read": (C.c_int, [P, C.POINTER(C.c_uint64), C.POINTER(C.c_int)]),
+        "ill_gemv_create": (C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_uint8), C.POINTER(C.c_uint32), C.c_int, C.POINTER(P)]),
+        "ill_gemv_run": (C.c_int, [P, C.POINTER(F32), C.POINTER(F32), C.c_int, C.POINTER(F32), ip, C.POINTER(F32)]),
+        "ill_gemv_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
+        "ill_gemv_destroy": (C.c_int, [P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -210,3 +214,49 @@ class Engine:
         ms = C.c_float(0)
         self._check(self.lib.ill_time_graph(self.h, iters, C.byref(ms)))
         return ms.value
+
+
+class Gemv:
+    """Stand-alone q4 GEMV (config-1 microbench) over the C ABI: y = W rmsnorm(x) gamma
+    (or W x), optional argmax epilogue; `copies` rotated device copies of W."""
+
+    def __init__(self, codes: np.ndarray, scales: np.ndarray, copies: int = 1):
+        self.lib = load_library()
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint32)
+        self.rows, half = codes.shape
+        self.K = 2 * half
+        self.h = C.c_void_p()
+        rc = self.lib.ill_gemv_create(self.rows, self.K, _ptr(codes, C.c_uint8), _ptr(scales, C.c_uint32), copies,
+                                      C.byref(self.h))
+        if rc != ILL_OK:
+            raise IllError(rc, self.lib.ill_last_error().decode())
+
+    def run(self, x: np.ndarray, gamma: np.ndarray | None = None, iters: int = 1, argmax: bool = False):
+        """Returns (y, argmax or None, microseconds per run)."""
+        x = np.ascontiguousarray(x, np.float32)
+        g = None if gamma is None else np.ascontiguousarray(gamma, np.float32)
+        y = np.zeros(self.rows, np.float32)
+        am = C.c_int32(-1)
+        us = C.c_float(0)
+        rc = self.lib.ill_gemv_run(self.h, _ptr(x, C.c_float), None if g is None else _ptr(g, C.c_float), iters,
+                                   _ptr(y, C.c_float), C.byref(am) if argmax else None, C.byref(us))
+        if rc != ILL_OK:
+            raise IllError(rc, self.lib.ill_last_error().decode())
+        return y, (int(am.value) if argmax else None), float(us.value)
+
+    def info(self) -> dict:
+        ks, bps, nbytes = C.c_int(0), C.c_int(0), C.c_int64(0)
+        self.lib.ill_gemv_info(self.h, C.byref(ks), C.byref(bps), C.byref(nbytes))
+        return {"slices": ks.value, "blocks_per_slice": bps.value, "bytes": int(nbytes.value)}
+
+    def close(self):
+        if self.h:
+            self.lib.ill_gemv_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -41,11 +41,20 @@ def _mat(buf, fmt, off, size, sboff, sbsize, rows, cols) -> np.ndarray:
         return (q.reshape(rows, ngroups, group) * s[..., None]).reshape(rows, cols)
     assert fmt == 2 and size == rows * cols // 2
     b = np.frombuffer(buf, np.uint8, rows * cols // 2, off).reshape(rows, cols // 2)
+    sb = np.frombuffer(buf, "<f2", rows * cols // 64 * 2, sboff).reshape(rows, cols // 64, 2)
+    return dequant_q4(b, sb)
+
+
+def dequant_q4(codes: np.ndarray, sb: np.ndarray) -> np.ndarray:
+    """q4 affine group-64: codes [rows][K/2] (low nibble = even column), sb [rows][K/64][2]
+    f16 (scale, min); w = scale * q + min (Shaders.swift:114-126, Convert.swift:67-88)."""
+    rows, half = codes.shape
+    cols = 2 * half
     q = np.empty((rows, cols), np.float32)
-    q[:, 0::2] = b & 0xF
-    q[:, 1::2] = b >> 4
-    sb = np.frombuffer(buf, "<f2", rows * cols // 64 * 2, sboff).astype(np.float32).reshape(rows, cols // 64, 2)
-    w = q.reshape(rows, cols // 64, 64) * sb[..., 0:1] + sb[..., 1:2]
+    q[:, 0::2] = codes & 0xF
+    q[:, 1::2] = codes >> 4
+    s = np.asarray(sb).astype(np.float32).reshape(rows, cols // 64, 2)
+    w = q.reshape(rows, cols // 64, 64) * s[..., 0:1] + s[..., 1:2]
     return w.reshape(rows, cols).astype(np.float32)
 
 

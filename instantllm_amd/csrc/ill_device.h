@@ -175,6 +175,13 @@ template <int N> __device__ __forceinline__ float gsum(float v) { return group_r
 template <int N> __device__ __forceinline__ float gmax(float v) { return group_reduce<N>(v, OpMaxF{}); }
 template <int N> __device__ __forceinline__ int gsumi(int v) { return group_reduce<N>(v, OpAddI{}); }
 
+// Order-preserving 64-bit key of (value, index): larger value first, then lower index.
+__device__ __forceinline__ uint64_t amax_key(float v, int idx) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }

@@ -20,6 +20,7 @@
 #include "../../include/ill_hip.h"
 #include "ill_pass.h"
 #include "ill_gemv.h"
+#include "ill_ops.h"
 
 namespace {
 
@@ -121,6 +122,12 @@ struct ill_engine {
   IllCtl hctl{};
   IllPassArgs args{};
   int logits_rows_valid = 0;
+  // layer-by-layer path (prefill chunks > 16 rows; every pass of q8 / f16 models)
+  uint8_t* oweights = nullptr;
+  OpLayerW* dolayers = nullptr;
+  std::vector<OpLayerW> holayers;
+  OpCtx octx{};
+  int q8g = 64;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;   // bracket the last single-pass launch
 };
 
@@ -178,6 +185,63 @@ int write_pos_n(ill_engine* e, int pos, int n) {
   return 0;
 }
 
+// ---- layer-by-layer path -----------------------------------------------------------------
+template <int FMT, int EPI>
+void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, float* resid) {
+  OpGemmArgs g;
+  g.c = e->octx;
+  g.A = A;
+  g.W = W;
+  g.M = M;
+  g.layer = layer;
+  g.resid = resid;
+  if constexpr (EPI != OP_LMH) {
+    if (M > 16) {
+      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI>), dim3(W.N / OP_BN, (M + 63) / 64), dim3(256), 0, e->stream, g);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), dim3(W.N / OP_BN, (M + 15) / 16), dim3(256), 0, e->stream, g);
+}
+
+// The kernels of one pass over M rows (control block and State already written): layers,
+// lm_head on the last lm_rows rows (0: none), commit.
+template <int FMT>
+void op_seq(ill_engine* e, int M, int lm_rows) {
+  const OpCtx& c = e->octx;
+  hipStream_t s = e->stream;
+  hipLaunchKernelGGL(op_embed_kernel<FMT>, dim3((M * ILL_H + 255) / 256), dim3(256), 0, s, c, M);
+  for (int l = 0; l < e->layers; l++) {
+    const OpLayerW& L = e->holayers[l];
+    hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
+    op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
+    hipLaunchKernelGGL(op_attn_kernel, dim3((M * ILL_NH + 3) / 4), dim3(256), 0, s, c, l, M);
+    op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x);
+    hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
+    op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr);
+    op_gemm<FMT, OP_RESID>(e, c.h, L.d, M, l, c.x);
+  }
+  if (lm_rows > 0) {
+    hipLaunchKernelGGL(op_norm_kernel, dim3((lm_rows + 3) / 4), dim3(256), 0, s, c, c.fnorm, M - lm_rows, lm_rows);
+    op_gemm<FMT, OP_LMH>(e, c.xn, c.emb, lm_rows, 0, nullptr);
+  }
+  hipLaunchKernelGGL(op_commit_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, s, e->args, (const uint64_t*)c.amax, e->vocab / OP_BN);
+}
+
+void op_seq_fmt(ill_engine* e, int M, int lm_rows) {
+  if (e->fmt == 2) op_seq<2>(e, M, lm_rows);
+  else if (e->fmt == 1) op_seq<1>(e, M, lm_rows);
+  else op_seq<0>(e, M, lm_rows);
+}
+
+int op_launch(ill_engine* e, int M, int lm_rows) {
+  HCK(hipEventRecord(e->ev0, e->stream));
+  op_seq_fmt(e, M, lm_rows);
+  HCK(hipGetLastError());
+  HCK(hipEventRecord(e->ev1, e->stream));
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -220,7 +284,6 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   if (count < 16 || (count - 4) % 12 || 16 + (size_t)count * 16 > (size_t)kHeader) return fail(ILL_E_FILE, "%s: tensor table mismatch", path);
   const int layers = (count - 4) / 12;
   if (layers > ILL_MAXLAYERS) return fail(ILL_E_FILE, "%s: %d layers (max %d)", path, layers, ILL_MAXLAYERS);
-  if (fmt != 2) return fail(ILL_E_FORMAT, "%s: weight format %d (only q4 is built into this engine so far)", path, fmt);
   std::vector<uint64_t> tab(2 * (size_t)count);
   memcpy(tab.data(), base + 16, tab.size() * 8);
   auto off = [&](int id) { return tab[2 * id]; };
@@ -228,21 +291,37 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   for (int id = 0; id < count; id++)
     if (size(id) && off(id) + size(id) > m.len) return fail(ILL_E_FILE, "%s: tensor %d out of range", path, id);
   auto need = [&](int id, size_t bytes) { return size(id) == bytes; };
-  const int vocab = (int)(size(0) * 2 / ILL_H);
-  if (vocab < 16 || vocab % 16 || !need(0, (size_t)vocab * ILL_H / 2) || !need(1, (size_t)vocab * (ILL_H / 64) * 4) ||
-      !need(2, ILL_H * 4))
+  // matrix [rows][K]: q4 codes + (scale, min) per 64; q8 int8 + f16 scale per group
+  // (32 or 64, read from the file, the same for every matrix); f16 values
+  int q8g = 0;
+  auto mat_ok = [&](int idw, int ids, int rows, int K) -> bool {
+    if (fmt == 2) return need(idw, (size_t)rows * K / 2) && need(ids, (size_t)rows * (K / 64) * 4);
+    if (fmt == 1) {
+      if (!need(idw, (size_t)rows * K) || size(ids) == 0 || size(ids) % ((size_t)2 * rows)) return false;
+      const size_t ng = size(ids) / 2 / rows;
+      if (K % ng) return false;
+      const int g = (int)(K / ng);
+      if (g != 32 && g != 64) return false;
+      if (q8g && q8g != g) return false;
+      q8g = g;
+      return true;
+    }
+    return need(idw, (size_t)rows * K * 2);
+  };
+  const int vocab = (int)(fmt == 2 ? size(0) * 2 / ILL_H : (fmt == 1 ? size(0) / ILL_H : size(0) / (2 * ILL_H)));
+  if (vocab < 128 || vocab % 128 || !mat_ok(0, 1, vocab, ILL_H) || !need(2, ILL_H * 4))
     return fail(ILL_E_FILE, "%s: bad embedding tensors", path);
   for (int l = 0; l < layers; l++) {
     const int b = 3 + 12 * l;
-    if (!need(b + 0, ILL_H * 4) || !need(b + 1, (size_t)ILL_QKV * ILL_H / 2) || !need(b + 2, (size_t)ILL_QKV * 14 * 4) ||
-        !need(b + 3, ILL_QKV * 4) || !need(b + 4, (size_t)ILL_H * ILL_H / 2) || !need(b + 5, (size_t)ILL_H * 14 * 4) ||
-        !need(b + 6, ILL_H * 4) || !need(b + 7, (size_t)2 * ILL_FF * ILL_H / 2) || !need(b + 8, (size_t)2 * ILL_FF * 14 * 4) ||
-        !need(b + 9, (size_t)ILL_H * ILL_FF / 2) || !need(b + 10, (size_t)ILL_H * 76 * 4))
-      return fail(ILL_E_FILE, "%s: layer %d tensor sizes do not match the q4 model shape", path, l);
+    if (!need(b + 0, ILL_H * 4) || !mat_ok(b + 1, b + 2, ILL_QKV, ILL_H) || !need(b + 3, ILL_QKV * 4) ||
+        !mat_ok(b + 4, b + 5, ILL_H, ILL_H) || !need(b + 6, ILL_H * 4) || !mat_ok(b + 7, b + 8, 2 * ILL_FF, ILL_H) ||
+        !mat_ok(b + 9, b + 10, ILL_H, ILL_FF))
+      return fail(ILL_E_FILE, "%s: layer %d tensor sizes do not match the model shape (format %d)", path, l, fmt);
   }
 
   ill_engine* e = new ill_engine();
   e->fmt = fmt;
+  e->q8g = q8g ? q8g : 64;
   e->layers = layers;
   e->vocab = vocab;
   e->maxctx = (max_context + 63) / 64 * 64;
@@ -272,7 +351,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   std::vector<int> ident;
   // embedding / lm_head
   const size_t o_embW = take(embW), o_embS = take(embS), o_fn = take(ILL_H * 4);
-  {
+  if (fmt == 2) {
     ident.resize(vocab);
     for (int i = 0; i < vocab; i++) ident[i] = i;
     repack_rows(base + off(0), (const uint32_t*)(base + off(1)), ILL_H, ident, host.data() + o_embW, (uint32_t*)(host.data() + o_embS));
@@ -297,6 +376,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     L.qkvW = take(qkvW); L.qkvS = take(qkvS); L.oW = take(oW); L.oS = take(oS);
     L.guW = take(guW); L.guS = take(guS); L.dW = take(dW); L.dS = take(dS);
     L.b = take(ILL_QKV * 4); L.ln1 = take(ILL_H * 4); L.ln2 = take(ILL_H * 4);
+    if (fmt != 2) continue;   // the persistent pass kernel runs q4 models only
     repack_rows(base + off(b + 1), (const uint32_t*)(base + off(b + 2)), ILL_H, rows_qkv, host.data() + L.qkvW, (uint32_t*)(host.data() + L.qkvS));
     repack_split(base + off(b + 4), (const uint32_t*)(base + off(b + 5)), ILL_H, host.data() + L.oW, (uint32_t*)(host.data() + L.oS));
     repack_rows(base + off(b + 7), (const uint32_t*)(base + off(b + 8)), ILL_H, rows_gu, host.data() + L.guW, (uint32_t*)(host.data() + L.guS));
@@ -343,6 +423,44 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     w.wd = D + L.dW; w.sd = (const uint32_t*)(D + L.dS);
     w.bqkv = (const float*)(D + L.b); w.ln1 = (const float*)(D + L.ln1); w.ln2 = (const float*)(D + L.ln2);
   }
+  // ---- layer-by-layer path: the .ill matrices as stored (row-major, file row orders)
+  {
+    std::vector<size_t> place(count, 0);
+    size_t otot = 0;
+    for (int id = 0; id < count; id++) {
+      place[id] = otot;
+      otot += al256(size(id));
+    }
+    std::vector<uint8_t> oh(otot);
+    for (int id = 0; id < count; id++)
+      if (size(id)) memcpy(oh.data() + place[id], base + off(id), size(id));
+    if (hipMalloc(&e->oweights, otot) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights allocation failed (%zu B)", otot));
+    if (hipMemcpy(e->oweights, oh.data(), otot, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights upload failed"));
+    uint8_t* O = e->oweights;
+    auto mk = [&](int idw, int ids, int rows, int K) {
+      OpMat m;
+      m.w = O + place[idw];
+      m.s = (const uint16_t*)(O + place[ids]);
+      m.N = rows;
+      m.K = K;
+      m.qg = e->q8g;
+      return m;
+    };
+    e->holayers.resize(layers);
+    for (int l = 0; l < layers; l++) {
+      const int b = 3 + 12 * l;
+      OpLayerW& w = e->holayers[l];
+      w.qkv = mk(b + 1, b + 2, ILL_QKV, ILL_H);
+      w.o = mk(b + 4, b + 5, ILL_H, ILL_H);
+      w.gu = mk(b + 7, b + 8, 2 * ILL_FF, ILL_H);
+      w.d = mk(b + 9, b + 10, ILL_H, ILL_FF);
+      w.bqkv = (const float*)(O + place[b + 3]);
+      w.ln1 = (const float*)(O + place[b + 0]);
+      w.ln2 = (const float*)(O + place[b + 6]);
+    }
+    e->octx.emb = mk(0, 1, vocab, ILL_H);
+    e->octx.fnorm = (const float*)(O + place[2]);
+  }
   auto dalloc = [&](void** p, size_t bytes) {
     if (hipMalloc(p, bytes) != hipSuccess) return false;
     return hipMemset(*p, 0, bytes) == hipSuccess;
@@ -350,12 +468,18 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   const size_t kvb = (size_t)layers * ILL_NKV * e->maxctx * 64 * 2;
   e->acc_bytes = (size_t)2 * layers * 2 * 16 * ILL_H * 8;
   bool ok = dalloc((void**)&e->dlayers, sizeof(IllLayerW) * layers) && dalloc((void**)&e->st, 64) && dalloc((void**)&e->ctl, 64) &&
-            dalloc((void**)&e->ptoks, 64) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
+            dalloc((void**)&e->ptoks, ILL_OP_MAXM * 4) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
             dalloc((void**)&e->acc, e->acc_bytes) &&
             dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
             dalloc((void**)&e->out_dev, (size_t)max_steps * 4);
+  ok = ok && dalloc((void**)&e->dolayers, sizeof(OpLayerW) * layers) && dalloc((void**)&e->octx.x, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
+       dalloc((void**)&e->octx.xn, (size_t)ILL_OP_MAXM * ILL_H * 2) && dalloc((void**)&e->octx.q, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
+       dalloc((void**)&e->octx.ao, (size_t)ILL_OP_MAXM * ILL_H * 2) && dalloc((void**)&e->octx.h, (size_t)ILL_OP_MAXM * ILL_FF * 2) &&
+       dalloc((void**)&e->octx.amax, (size_t)(vocab / OP_BN) * 16 * 8);
   if (!ok) return cleanup(fail(ILL_E_HIP, "device buffer allocation failed"));
+  if (hipMemcpy(e->dolayers, e->holayers.data(), sizeof(OpLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
+    return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
   if (hipHostMalloc((void**)&e->out_host, (size_t)max_steps * 4, hipHostMallocDefault) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "pinned token buffer allocation failed"));
   for (int i = 0; i < max_steps; i++) e->out_host[i] = -1;
@@ -404,6 +528,19 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.out_host = e->out_host;
   a.maxctx = e->maxctx;
   a.maxsteps = max_steps;
+  OpCtx& oc = e->octx;
+  oc.L = e->dolayers;
+  oc.st = e->st;
+  oc.ctl = e->ctl;
+  oc.ptoks = e->ptoks;
+  oc.tree = e->tree;
+  oc.rope = e->rope;
+  oc.kc = e->kc;
+  oc.vt = e->vt;
+  oc.logits = e->logits;
+  oc.maxctx = e->maxctx;
+  oc.layers = layers;
+  oc.vocab = vocab;
   if (hipDeviceSynchronize() != hipSuccess) return cleanup(fail(ILL_E_HIP, "device sync failed"));
   *out = e;
   return ILL_OK;
@@ -415,7 +552,8 @@ int ill_destroy(ill_engine* e) {
   if (e->gexec) hipGraphExecDestroy(e->gexec);
   if (e->graph) hipGraphDestroy(e->graph);
   void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
-                  e->lmp, e->logits, e->out_dev, e->args.trace};
+                  e->lmp, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
+                  e->octx.q, e->octx.ao, e->octx.h, e->octx.amax};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);
@@ -461,6 +599,20 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
   for (int i = 0; i < n; i++)
     if (toks[i] < 0 || toks[i] >= e->vocab) return fail(ILL_E_ARG, "token %d out of range", toks[i]);
   int pos = s.pos;
+  if (e->fmt != 2 || n > 16) {   // layer-by-layer path, chunks of up to ILL_OP_MAXM rows
+    for (int c0 = 0; c0 < n; c0 += ILL_OP_MAXM) {
+      const int rows = n - c0 < ILL_OP_MAXM ? n - c0 : ILL_OP_MAXM;
+      const bool last = c0 + rows == n;
+      HCK(hipMemcpyAsync(e->ptoks, toks + c0, rows * 4, hipMemcpyHostToDevice, e->stream));
+      if ((rc = write_pos_n(e, pos, rows))) return rc;
+      if ((rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, last ? 1 : 0, last ? write_logits : 0, last ? 1 : 0))) return rc;
+      if ((rc = op_launch(e, rows, last ? 1 : 0))) return rc;
+      pos += rows;
+      HCK(hipStreamSynchronize(e->stream));
+    }
+    if (write_logits) e->logits_rows_valid = 1;
+    return check_err(e);
+  }
   for (int c0 = 0; c0 < n; c0 += 16) {
     const int rows = n - c0 < 16 ? n - c0 : 16;
     const bool last = c0 + rows == n;
@@ -489,7 +641,7 @@ int ill_decode_step(ill_engine* e, int write_logits) {
   if (!e) return fail(ILL_E_ARG, "null engine");
   int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits, 1);
   if (rc) return rc;
-  if ((rc = launch(e, 1))) return rc;
+  if ((rc = e->fmt == 2 ? launch(e, 1) : op_launch(e, 1, 1))) return rc;
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = 1;
   return ILL_OK;
@@ -522,7 +674,7 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
   if (tree) HCK(hipMemcpyAsync(e->tree, tree, ILL_TR_INTS * 4, hipMemcpyHostToDevice, e->stream));
   if ((rc = write_pos_n(e, s.pos, rows))) return rc;
   if ((rc = set_ctl(e, tree ? ILL_MODE_TREE : ILL_MODE_ROWS, rows, 0, rows, write_logits, 2))) return rc;
-  if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
+  if ((rc = e->fmt == 2 ? launch(e, rows == 1 ? 1 : 16) : op_launch(e, rows, rows))) return rc;
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = rows;
   return ILL_OK;
@@ -540,8 +692,10 @@ int ill_capture_steps(ill_engine* e, int nsteps) {
   }
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-  for (int i = 0; i < nsteps; i++)
-    hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
+  for (int i = 0; i < nsteps; i++) {
+    if (e->fmt == 2) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
+    else op_seq_fmt(e, 1, 1);
+  }
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = nsteps;

@@ -133,13 +133,6 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
   }
 }
 
-// Order-preserving 64-bit key of (value, index): larger value first, then lower index.
-__device__ __forceinline__ uint64_t amax_key(float v, int idx) {
-  const uint32_t b = __float_as_uint(v);
-  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((uint64_t)ord << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
-}
-
 // y[r] = sum over slices in order; optional argmax into *key (atomic max of amax_key).
 __global__ __launch_bounds__(256) void ill_gemv_finish_kernel(const float* part, int ks, int rows, float* y, uint64_t* key) {
   __shared__ uint64_t best[4];

@@ -84,6 +84,41 @@ __device__ __forceinline__ int tid_opaque() {
 // its outstanding global loads, stores, atomics or LDS DMA (which __syncthreads would).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// The pass header: State, control block and row metadata, read once by thread 0.
+__device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
+  const IllState* st = a.st;
+  const IllCtl* c = a.ctl;
+  H.done = st->done;
+  H.epoch = c->epoch;
+  H.bank = c->epoch & 1;
+  H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
+  H.mode = c->mode;
+  H.nrows = c->nrows;
+  H.pos = st->pos;
+  H.lmh0 = c->lmh_row0;
+  H.lmhn = c->lmh_rows;
+  H.wlog = c->write_logits;
+  H.commit = c->commit;
+  for (int t = 0; t < 16; t++) {
+    H.tok[t] = t < H.nrows ? a.ptoks[t] : 0;
+    if (H.mode == ILL_MODE_TREE) {
+      H.depth[t] = t < H.nrows ? a.tree[ILL_TR_DEPTH + t] : 0;
+      H.parent[t] = t < H.nrows ? a.tree[ILL_TR_PARENT + t] : 0;
+    } else {
+      H.depth[t] = t;
+      H.parent[t] = t > 0 ? t - 1 : 0;
+    }
+  }
+  for (int t = 0; t < 16; t++) {
+    for (int d = 0; d < 16; d++) H.prow[t][d] = 0;
+    int r = t;
+    for (int d = H.depth[t]; d >= 0; --d) {
+      H.prow[t][d] = r;
+      r = r > 0 ? H.parent[r] : 0;
+    }
+  }
+}
+
 // ---- residual fixed point --------------------------------------------------------------
 #define FX_COUNT (1ull << 56)
 #define FX_BIAS (1ll << 48)
@@ -1059,6 +1094,7 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 }
 
 // ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel);
 __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
   const uint32_t tag = tagof_lmh(H.epoch);
   const int i = tid_opaque();
@@ -1095,6 +1131,14 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
     if (i == 0) C.g[t] = C.i[0];
     __syncthreads();
   }
+  commit_apply(a, H, C, true);
+}
+
+// Commit of the pass's argmaxes C.g[t] (rows lmh0 ..): token record, State advance, stop
+// test, chain / tree accept walk and KV compaction (Shaders.swift:192-244, :246-418). The
+// pass kernel also advances the epoch and its accumulator-bank bookkeeping.
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel) {
+  const int i = tid_opaque();
   IllState* st = a.st;
   if (i == 0) {
     C.npath = 0;
@@ -1171,7 +1215,7 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
     }
     __syncthreads();
   }
-  if (i == 0) {
+  if (pass_kernel && i == 0) {
     a.ctl->bank_rows[H.bank] = H.nrows;   // rows of this bank to clear during the next pass
     a.ctl->bank_rows[H.bank ^ 1] = 0;     // cleared during this pass
     a.ctl->epoch = H.epoch + 1;
@@ -1187,39 +1231,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   __shared__ PassLds<T> S;
   extern __shared__ __attribute__((aligned(16))) uint8_t ill_stage[];   // ILL_STAGE_BYTES (dynamic)
   __shared__ PassHdr H;
-  if (threadIdx.x == 0) {
-    const IllState* st = a.st;
-    const IllCtl* c = a.ctl;
-    H.done = st->done;
-    H.epoch = c->epoch;
-    H.bank = c->epoch & 1;
-    H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
-    H.mode = c->mode;
-    H.nrows = c->nrows;
-    H.pos = st->pos;
-    H.lmh0 = c->lmh_row0;
-    H.lmhn = c->lmh_rows;
-    H.wlog = c->write_logits;
-    H.commit = c->commit;
-    for (int t = 0; t < 16; t++) {
-      H.tok[t] = t < H.nrows ? a.ptoks[t] : 0;
-      if (H.mode == ILL_MODE_TREE) {
-        H.depth[t] = t < H.nrows ? a.tree[ILL_TR_DEPTH + t] : 0;
-        H.parent[t] = t < H.nrows ? a.tree[ILL_TR_PARENT + t] : 0;
-      } else {
-        H.depth[t] = t;
-        H.parent[t] = t > 0 ? t - 1 : 0;
-      }
-    }
-    for (int t = 0; t < 16; t++) {
-      for (int d = 0; d < 16; d++) H.prow[t][d] = 0;
-      int r = t;
-      for (int d = H.depth[t]; d >= 0; --d) {
-        H.prow[t][d] = r;
-        r = r > 0 ? H.parent[r] : 0;
-      }
-    }
-  }
+  if (threadIdx.x == 0) load_hdr(a, H);
   __syncthreads();
   if (H.done) return;
   const int wg = blockIdx.x;

@@ -106,6 +106,54 @@ def gemv_config1() -> dict:
     return out
 
 
+# prefill work of config 4 (M = 512): 2 flops per weight and row over the 24 layers'
+# matrices, the lm_head on the last row, and causal attention (QK and PV, 64 dims, 14 heads)
+LAYER_PARAMS = 357_826_560
+LMH_PARAMS = 136_134_656
+
+
+def prefill_flops(m: int, layers: int = 24) -> float:
+    attn = layers * 14 * 2 * 2 * 64 * (m * (m + 1) / 2)
+    return 2.0 * m * LAYER_PARAMS + 2.0 * LMH_PARAMS + attn
+
+
+def config4(steps: int = 64) -> dict:
+    """Config 4: q8 (symmetric group-64) and f16 models (seed 4): a 512-token prefill on the
+    MFMA GEMMs, then `steps` graph-captured greedy decode steps; then the same after a
+    4032-token prompt, so the last step attends 4096 positions."""
+    from instantllm_amd import synth, illfile as F
+    from instantllm_amd.engine import Engine
+    no_eos = (-5, -5)
+    out = {}
+    for name, fmt in (("q8", F.FMT_Q8), ("f16", F.FMT_F16)):
+        e = Engine(synth.cached_model(fmt, 4), max_context=4160, max_pass=16, max_steps=256)
+        rng = np.random.default_rng(4)
+        prompt = [int(t) for t in rng.integers(0, F.VOCAB, size=512)]
+        pre_ms = []
+        for _ in range(3):
+            e.reset_out_tokens()
+            e.set_state(pos=0, n=512, maxsteps=steps + 1, eos=no_eos)
+            e.prefill(prompt)
+            pre_ms.append(e.last_pass_ms())
+        e.capture_steps(steps)
+        dec_ms = e.time_graph(1)
+        longp = [int(t) for t in rng.integers(0, F.VOCAB, size=4032)]
+        e.reset_out_tokens()
+        e.set_state(pos=0, n=len(longp), maxsteps=steps + 1, eos=no_eos)
+        e.prefill(longp)
+        e.capture_steps(steps)
+        long_ms = e.time_graph(1)
+        pos_end = e.get_state()["pos"]
+        e.close()
+        pm = float(np.median(pre_ms))
+        out[name] = {"prefill512_ms": round(pm, 3),
+                     "prefill512_tflops": round(prefill_flops(512) / (pm * 1e-3) / 1e12, 1),
+                     "decode_us_after_512": round(dec_ms * 1e3 / steps, 1),
+                     "decode_us_4032_to_4096": round(long_ms * 1e3 / steps, 1),
+                     "last_pos": pos_end}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +163,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV microbench")
+    ap.add_argument("--no-config4", action="store_true", help="skip the q8 / f16 prefill and decode runs")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (the reference dispatch "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -216,6 +265,8 @@ def main() -> int:
     }
     if not args.no_gemv:
         line["gemv_config1"] = gemv_config1()
+    if not args.no_config4:
+        line["config4"] = config4()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(path, prompt[:48], args.cpu_steps)
     print(json.dumps(line), flush=True)

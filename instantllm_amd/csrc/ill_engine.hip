@@ -127,6 +127,7 @@ struct ill_engine {
   OpLayerW* dolayers = nullptr;
   std::vector<OpLayerW> holayers;
   OpCtx octx{};
+  float* opart = nullptr;   // split-K partials of the layer-by-layer GEMMs
   int q8g = 64;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;   // bracket the last single-pass launch
 };
@@ -186,6 +187,8 @@ int write_pos_n(ill_engine* e, int pos, int n) {
 }
 
 // ---- layer-by-layer path -----------------------------------------------------------------
+#define ILL_OP_PART_BYTES (16u << 20)   // >= slices x rows x N x 4 of every split GEMM
+
 template <int FMT, int EPI>
 void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, float* resid) {
   OpGemmArgs g;
@@ -195,13 +198,36 @@ void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   g.M = M;
   g.layer = layer;
   g.resid = resid;
+  g.part = e->opart;
+  const int nsteps = W.K / OP_BK, ntn = W.N / OP_BN;
   if constexpr (EPI != OP_LMH) {
-    if (M > 16) {
-      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI>), dim3(W.N / OP_BN, (M + 63) / 64), dim3(256), 0, e->stream, g);
+    if (M > 16) {   // prefill chunk: 64-row tiles, K split only where the tiles are few
+      const int mt = (M + 63) / 64;
+      int S = std::max(1, std::min(256 / (ntn * mt), nsteps / 4));
+      g.ksteps = (nsteps + S - 1) / S;
+      S = (nsteps + g.ksteps - 1) / g.ksteps;
+      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
+      if (S > 1) {
+        const int per = EPI == OP_RESID ? W.N : W.N / 2;
+        hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
+      }
       return;
     }
   }
-  hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), dim3(W.N / OP_BN, (M + 15) / 16), dim3(256), 0, e->stream, g);
+  // up to 16 rows: split K so that about 256 workgroups stream the weights, at least four
+  // k-steps per slice (the split depends on the matrix only, so 1-row and 16-row passes
+  // sum the same partials in the same order)
+  int S = 1;
+  if (EPI != OP_LMH) S = std::max(1, std::min((256 + ntn - 1) / ntn, nsteps / 4));
+  g.ksteps = (nsteps + S - 1) / S;
+  S = (nsteps + g.ksteps - 1) / g.ksteps;
+  hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), dim3(ntn, (M + 15) / 16, S), dim3(256), 0, e->stream, g);
+  if constexpr (EPI != OP_LMH) {
+    if (S > 1) {
+      const int per = EPI == OP_RESID ? W.N : W.N / 2;
+      hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
+    }
+  }
 }
 
 // The kernels of one pass over M rows (control block and State already written): layers,
@@ -215,7 +241,8 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     const OpLayerW& L = e->holayers[l];
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
-    hipLaunchKernelGGL(op_attn_kernel, dim3((M * ILL_NH + 3) / 4), dim3(256), 0, s, c, l, M);
+    if (M > 16) hipLaunchKernelGGL(op_attn_kernel<2>, dim3(M * ILL_NH), dim3(128), 0, s, c, l, M);
+    else hipLaunchKernelGGL(op_attn_kernel<ILL_WAVES>, dim3(M * ILL_NH), dim3(64 * ILL_WAVES), 0, s, c, l, M);
     op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x);
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
     op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr);
@@ -476,7 +503,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   ok = ok && dalloc((void**)&e->dolayers, sizeof(OpLayerW) * layers) && dalloc((void**)&e->octx.x, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
        dalloc((void**)&e->octx.xn, (size_t)ILL_OP_MAXM * ILL_H * 2) && dalloc((void**)&e->octx.q, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
        dalloc((void**)&e->octx.ao, (size_t)ILL_OP_MAXM * ILL_H * 2) && dalloc((void**)&e->octx.h, (size_t)ILL_OP_MAXM * ILL_FF * 2) &&
-       dalloc((void**)&e->octx.amax, (size_t)(vocab / OP_BN) * 16 * 8);
+       dalloc((void**)&e->octx.amax, (size_t)(vocab / OP_BN) * 16 * 8) && dalloc((void**)&e->opart, ILL_OP_PART_BYTES);
   if (!ok) return cleanup(fail(ILL_E_HIP, "device buffer allocation failed"));
   if (hipMemcpy(e->dolayers, e->holayers.data(), sizeof(OpLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
@@ -553,7 +580,7 @@ int ill_destroy(ill_engine* e) {
   if (e->graph) hipGraphDestroy(e->graph);
   void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
                   e->lmp, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
-                  e->octx.q, e->octx.ao, e->octx.h, e->octx.amax};
+                  e->octx.q, e->octx.ao, e->octx.h, e->octx.amax, e->opart};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);

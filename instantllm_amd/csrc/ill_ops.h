@@ -122,22 +122,46 @@ struct OpGemmArgs {
   OpMat W;
   int M, layer;
   float* resid;      // OP_RESID: [M][896] += Y
+  float* part;       // split K: [slices][M][N] fp32 partials
+  int ksteps;        // 64-column steps per K slice
 };
 
 #define OP_BN 128
 #define OP_BK 64
 #define OP_LDK 72    // LDS row stride in halves (padding against bank conflicts)
 
-// Dequantize W rows n0 .. n0+127, columns k0 .. k0+63 into LDS [128][OP_LDK] f16.
+// One k-step (64 columns) of the weight tile, rows n0 .. n0+127, as loaded from HBM, and
+// its dequantization into LDS [128][OP_LDK] f16. Thread -> (row tid / 2, half tid % 2).
 template <int FMT>
-__device__ __forceinline__ void op_load_w(const OpMat& W, int n0, int k0, _Float16* Bs, int tid) {
+struct WRaw {
+  uint4 b[FMT == 2 ? 1 : (FMT == 1 ? 2 : 4)];
+  uint32_t sm;
+};
+
+template <int FMT>
+__device__ __forceinline__ void op_fetch_w(const OpMat& W, int n0, int k0, int tid, WRaw<FMT>& r) {
+  const int row = n0 + (tid >> 1), hf = tid & 1;
   if constexpr (FMT == 2) {
-    // 128 rows x 32 bytes: thread -> (row, 16-byte half)
-    const int r = tid >> 1, hf = tid & 1;
-    const uint4 b = gld((const uint4*)(W.w + (size_t)(n0 + r) * (W.K / 2) + k0 / 2 + 16 * hf));
-    const uint32_t sm = gld((const uint32_t*)(W.s + ((size_t)(n0 + r) * (W.K / 64) + k0 / 64) * 2));
-    const _Float16 s = (_Float16)h2f(sm & 0xffff), m = (_Float16)h2f(sm >> 16);
-    const uint32_t x[4] = {b.x, b.y, b.z, b.w};
+    r.b[0] = gld((const uint4*)(W.w + (size_t)row * (W.K / 2) + k0 / 2 + 16 * hf));
+    r.sm = gld((const uint32_t*)(W.s + ((size_t)row * (W.K / 64) + k0 / 64) * 2));
+  } else if constexpr (FMT == 1) {
+    const uint8_t* src = W.w + (size_t)row * W.K + k0 + 32 * hf;
+    r.b[0] = gld((const uint4*)src);
+    r.b[1] = gld((const uint4*)(src + 16));
+    r.sm = gld(W.s + (size_t)row * (W.K / W.qg) + (k0 + 32 * hf) / W.qg);
+  } else {
+    const uint4* src = (const uint4*)(W.w + ((size_t)row * W.K + k0 + 32 * hf) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.b[i] = gld(src + i);
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void op_store_w(const WRaw<FMT>& r, _Float16* Bs, int tid) {
+  _Float16* dst = Bs + (tid >> 1) * OP_LDK + 32 * (tid & 1);
+  if constexpr (FMT == 2) {
+    const _Float16 s = (_Float16)h2f(r.sm & 0xffff), m = (_Float16)h2f(r.sm >> 16);
+    const uint32_t x[4] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w};
     _Float16 o[32];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -145,35 +169,87 @@ __device__ __forceinline__ void op_load_w(const OpMat& W, int n0, int k0, _Float
       o[2 * i] = s * (_Float16)(float)(byte & 15) + m;
       o[2 * i + 1] = s * (_Float16)(float)(byte >> 4) + m;
     }
-    _Float16* dst = Bs + r * OP_LDK + 32 * hf;
 #pragma unroll
     for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = *(const uint4*)(o + 8 * i);
   } else if constexpr (FMT == 1) {
-    // 128 rows x 64 bytes: thread -> (row, 32-byte half)
-    const int r = tid >> 1, hf = tid & 1;
-    const uint8_t* src = W.w + (size_t)(n0 + r) * W.K + k0 + 32 * hf;
-    const uint4 b0 = gld((const uint4*)src), b1 = gld((const uint4*)(src + 16));
-    const int kk = k0 + 32 * hf;
-    const _Float16 s = (_Float16)h2f(gld(W.s + (size_t)(n0 + r) * (W.K / W.qg) + kk / W.qg));
-    const uint32_t x[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const _Float16 s = (_Float16)h2f(r.sm & 0xffff);
+    const uint32_t x[8] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w, r.b[1].x, r.b[1].y, r.b[1].z, r.b[1].w};
     _Float16 o[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) o[i] = s * (_Float16)(float)(int8_t)((x[i >> 2] >> (8 * (i & 3))) & 0xff);
-    _Float16* dst = Bs + r * OP_LDK + 32 * hf;
 #pragma unroll
     for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = *(const uint4*)(o + 8 * i);
   } else {
-    // 128 rows x 128 bytes: thread -> (row, 64-byte half)
-    const int r = tid >> 1, hf = tid & 1;
-    const uint4* src = (const uint4*)(W.w + ((size_t)(n0 + r) * W.K + k0 + 32 * hf) * 2);
-    _Float16* dst = Bs + r * OP_LDK + 32 * hf;
 #pragma unroll
-    for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = gld(src + i);
+    for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = r.b[i];
   }
 }
 
+// A tile: BM rows x 64 halves; thread i (< BM * 8) carries 16 bytes (rows >= M read row
+// M - 1: finite, and their outputs are unused).
+template <int BM>
+struct ARaw {
+  uint4 v[(BM * 8 + 255) / 256];
+};
+template <int BM>
+__device__ __forceinline__ void op_fetch_a(const __half* A, int M, int K, int m0, int k0, int tid, ARaw<BM>& r) {
+#pragma unroll
+  for (int u = 0; u < (BM * 8 + 255) / 256; u++) {
+    const int i = tid + 256 * u;
+    if (i < BM * 8) {
+      const int row = min(m0 + (i >> 3), M - 1);
+      r.v[u] = gld((const uint4*)(A + (size_t)row * K + k0) + (i & 7));
+    }
+  }
+}
+template <int BM>
+__device__ __forceinline__ void op_store_a(const ARaw<BM>& r, _Float16* As, int tid) {
+#pragma unroll
+  for (int u = 0; u < (BM * 8 + 255) / 256; u++) {
+    const int i = tid + 256 * u;
+    if (i < BM * 8) *(uint4*)(As + (i >> 3) * OP_LDK + 8 * (i & 7)) = r.v[u];
+  }
+}
+
+// ---- epilogues (shared by the fused GEMM and the split-K reduction) ---------------------
+// QKV: one rotary block b = columns 32 b .. +31 holds dims d (x0, columns 32 b + i) and
+// d + 32 (x1, columns 32 b + 16 + i) of head b / 2 (Convert.swift:236-244); q heads 0-13,
+// k 14-15, v 16-17: bias, RoPE at the row's position, then q or the K / V cache slot.
+__device__ __forceinline__ void epi_qkv(const OpCtx& c, int layer, int m, int b, int i, float x0, float x1) {
+  const int head = b >> 1, d = (b & 1) * 16 + i;
+  x0 += c.L[layer].bqkv[32 * b + i];
+  x1 += c.L[layer].bqkv[32 * b + 16 + i];
+  const int pos = c.st->pos;
+  if (head < ILL_NH + ILL_NKV) {
+    const float2 cs = c.rope[(pos + op_depth(c, m)) * 32 + d];
+    const float r0 = x0 * cs.x - x1 * cs.y, r1 = x1 * cs.x + x0 * cs.y;
+    x0 = r0;
+    x1 = r1;
+  }
+  const int slot = pos + m;
+  if (head < ILL_NH) {
+    c.q[(size_t)m * ILL_H + head * 64 + d] = x0;
+    c.q[(size_t)m * ILL_H + head * 64 + d + 32] = x1;
+  } else if (head < ILL_NH + ILL_NKV) {
+    uint16_t* kr = c.kc + (((size_t)layer * ILL_NKV + (head - ILL_NH)) * c.maxctx + slot) * 64;
+    kr[d] = (uint16_t)f2h(x0);
+    kr[d + 32] = (uint16_t)f2h(x1);
+  } else {
+    uint16_t* vb = c.vt + (((size_t)layer * ILL_NKV + (head - ILL_NH - ILL_NKV)) * (c.maxctx / 64) + slot / 64) * 4096;
+    vb[d * 64 + (slot & 63)] = (uint16_t)f2h(x0);
+    vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)f2h(x1);
+  }
+}
+// gate/up rows in groups of 4: g[2q], g[2q+1], u[2q], u[2q+1] (Convert.swift:134-136)
+__device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float g, float u) {
+  c.h[(size_t)m * ILL_FF + unit] = __float2half(g / (1.0f + expf(-g)) * u);
+}
+
 // Workgroup: 256 threads = 4 waves; a wave owns 32 columns (two 16-column MFMA tiles) of
-// the 128-column tile and all BM rows.
+// the 128-column tile and all BM rows. blockIdx.z selects a K slice of `ksteps` 64-column
+// steps; with more than one slice the kernel writes fp32 partials [slice][M][N] and
+// op_epi_kernel reduces them in slice order and applies the epilogue. The next k-step's
+// operands are in flight while the current one is multiplied.
 template <int FMT, int BM, int EPI>
 __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   if (a.c.st->done) return;
@@ -185,21 +261,25 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   const int kg = lane >> 4, n = lane & 15;
   const int n0 = blockIdx.x * OP_BN, m0 = blockIdx.y * BM;
   const int K = a.W.K;
+  const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
   v4f acc[TM][2];
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     acc[i][0] = (v4f){0.f, 0.f, 0.f, 0.f};
     acc[i][1] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
-  for (int k0 = 0; k0 < K; k0 += OP_BK) {
-    // A: BM rows x 64 halves (rows >= M read row M-1: finite, and their outputs are unused)
-    for (int i = tid; i < BM * 8; i += 256) {
-      const int r = i >> 3, ch = i & 7;
-      const int mr = min(m0 + r, a.M - 1);
-      *(uint4*)(As + r * OP_LDK + 8 * ch) = gld((const uint4*)(a.A + (size_t)mr * K + k0) + ch);
-    }
-    op_load_w<FMT>(a.W, n0, k0, Bs, tid);
+  WRaw<FMT> wr;
+  ARaw<BM> ar;
+  op_fetch_w<FMT>(a.W, n0, kb, tid, wr);
+  op_fetch_a<BM>(a.A, a.M, K, m0, kb, tid, ar);
+  for (int k0 = kb; k0 < ke; k0 += OP_BK) {
+    op_store_a<BM>(ar, As, tid);
+    op_store_w<FMT>(wr, Bs, tid);
     __syncthreads();
+    if (k0 + OP_BK < ke) {
+      op_fetch_w<FMT>(a.W, n0, k0 + OP_BK, tid, wr);
+      op_fetch_a<BM>(a.A, a.M, K, m0, k0 + OP_BK, tid, ar);
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       v8h bf[2];
@@ -214,8 +294,20 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
     }
     __syncthreads();
   }
-  // ---- epilogues: lane holds rows 16 i + 4 kg + r, columns n0 + 32 w + 16 j + n
   const OpCtx& c = a.c;
+  if (gridDim.z > 1) {   // split K: partials for op_epi_kernel
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + 16 * i + 4 * kg + r, col = n0 + 32 * w + 16 * j + n;
+          if (m < a.M) a.part[((size_t)blockIdx.z * a.M + m) * a.W.N + col] = acc[i][j][r];
+        }
+    return;
+  }
+  // ---- fused epilogues: lane holds rows 16 i + 4 kg + r, columns n0 + 32 w + 16 j + n
   if constexpr (EPI == OP_RESID) {
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -227,7 +319,6 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
           if (m < a.M) a.resid[(size_t)m * ILL_H + col] += acc[i][j][r];
         }
   } else if constexpr (EPI == OP_SILU) {
-    // gate/up rows in groups of 4: g[2q], g[2q+1], u[2q], u[2q+1] (Convert.swift:134-136)
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -237,44 +328,16 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
           const float v = acc[i][j][r];
           const float up = __shfl_down(v, 2, 16);
           const int m = m0 + 16 * i + 4 * kg + r, col = n0 + 32 * w + 16 * j + n;
-          if ((n & 3) < 2 && m < a.M) {
-            const int unit = (col >> 2) * 2 + (n & 3);
-            c.h[(size_t)m * ILL_FF + unit] = __float2half(v / (1.0f + expf(-v)) * up);
-          }
+          if ((n & 3) < 2 && m < a.M) epi_silu(c, m, (col >> 2) * 2 + (n & 3), v, up);
         }
   } else if constexpr (EPI == OP_QKV) {
-    // a wave's 32 columns are one rotary block b: tile 0 = dims d, tile 1 = dims d + 32
-    // (Convert.swift:236-244); head b/2: q heads 0-13, k 14-15, v 16-17
-    const int b = (n0 + 32 * w) >> 5, head = b >> 1;
-    const int d = (b & 1) * 16 + n;
-    const float b0 = c.L[a.layer].bqkv[32 * b + n], b1 = c.L[a.layer].bqkv[32 * b + 16 + n];
-    const int pos = c.st->pos;
+    const int b = (n0 + 32 * w) >> 5;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + 16 * i + 4 * kg + r;
-        if (m >= a.M) continue;
-        float x0 = acc[i][0][r] + b0, x1 = acc[i][1][r] + b1;
-        if (head < ILL_NH + ILL_NKV) {
-          const float2 cs = c.rope[(pos + op_depth(c, m)) * 32 + d];
-          const float r0 = x0 * cs.x - x1 * cs.y, r1 = x1 * cs.x + x0 * cs.y;
-          x0 = r0;
-          x1 = r1;
-        }
-        const int slot = pos + m;
-        if (head < ILL_NH) {
-          c.q[(size_t)m * ILL_H + head * 64 + d] = x0;
-          c.q[(size_t)m * ILL_H + head * 64 + d + 32] = x1;
-        } else if (head < ILL_NH + ILL_NKV) {
-          uint16_t* kr = c.kc + (((size_t)a.layer * ILL_NKV + (head - ILL_NH)) * c.maxctx + slot) * 64;
-          kr[d] = (uint16_t)f2h(x0);
-          kr[d + 32] = (uint16_t)f2h(x1);
-        } else {
-          uint16_t* vb = c.vt + (((size_t)a.layer * ILL_NKV + (head - ILL_NH - ILL_NKV)) * (c.maxctx / 64) + slot / 64) * 4096;
-          vb[d * 64 + (slot & 63)] = (uint16_t)f2h(x0);
-          vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)f2h(x1);
-        }
+        if (m < a.M) epi_qkv(c, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
       }
   } else {   // OP_LMH: logits (optional) and per-tile argmax keys per row (BM == 16)
     const int wlog = c.ctl->write_logits;
@@ -305,52 +368,91 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   }
 }
 
-// ---- attention: one wave per (row, query head) --------------------------------------
+// Split-K reduction: sum of the slices' partials in slice order, then the epilogue.
+// RESID / SILU / QKV: one thread per output column / unit / rotary pair of a row.
+template <int EPI>
+__global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
+  if (a.c.st->done) return;
+  const int N = a.W.N;
+  const int per = EPI == OP_RESID ? N : N / 2;   // SILU: units; QKV: pairs
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.M * per) return;
+  const int m = i / per, j = i % per;
+  auto sum = [&](int col) {
+    float v = a.part[(size_t)m * N + col];
+    for (int z = 1; z < S; z++) v += a.part[((size_t)z * a.M + m) * N + col];
+    return v;
+  };
+  if constexpr (EPI == OP_RESID) {
+    a.resid[(size_t)m * ILL_H + j] += sum(j);
+  } else if constexpr (EPI == OP_SILU) {
+    const int q = j >> 1, r = j & 1;
+    epi_silu(a.c, m, j, sum(4 * q + r), sum(4 * q + 2 + r));
+  } else if constexpr (EPI == OP_QKV) {
+    const int b = j >> 4, ii = j & 15;
+    epi_qkv(a.c, a.layer, m, b, ii, sum(32 * b + ii), sum(32 * b + 16 + ii));
+  }
+}
+
+// ---- attention: one workgroup of NW waves per (row, query head) ---------------------
 // Row t attends to virtual positions 0 .. L-1, L = pos + depth(t) + 1; position p lives
 // in cache slot p below pos and in slot pos + (the row on t's path at depth p - pos) above
-// (tree passes; chains use slot p). Chunks of 64 positions in order, each folded into the
-// running (max, sum, output) with the same rule as the pass kernel.
-__global__ __launch_bounds__(256) void op_attn_kernel(OpCtx c, int layer, int M) {
+// (tree passes; chains use slot p). 64-position chunk c goes to wave c % NW, which folds its
+// chunks in order with the pass kernel's rule; the waves are then combined against the
+// global maximum. Passes of up to 16 rows use NW = 8 (the split depends only on the row's
+// own path, not on M); prefill chunks use NW = 2 (short rows, many of them).
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, int M) {
   if (c.st->done) return;
-  __shared__ float qs[4][64];
-  __shared__ float ps[4][64];
-  __shared__ int path[4][16];
+  __shared__ float qs[64];
+  __shared__ float ps[NW][64];
+  __shared__ int path[16];
+  __shared__ float cm[NW], cl[NW], co[NW][64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int pair = blockIdx.x * 4 + w;
-  if (pair >= M * ILL_NH) return;
-  const int t = pair / ILL_NH, h = pair % ILL_NH, g = h / 7;
+  const int t = blockIdx.x / ILL_NH, h = blockIdx.x % ILL_NH, g = h / 7;
   const int pos = c.st->pos;
   const bool tree = c.ctl->mode == ILL_MODE_TREE;
   const int dep = op_depth(c, t);
   const int L = pos + dep + 1;
-  if (lane < 16) {   // rows on t's path by depth (tree passes)
-    int r = t, pr = 0;
-    for (int d = dep; d >= 0; --d) {
-      if (d == lane) pr = r;
-      r = r > 0 && tree ? c.tree[ILL_TR_PARENT + r] : r - 1;
+  if (w == 0) {
+    if (lane < 16) {   // rows on t's path by depth (tree passes: depth <= 15)
+      int pr = lane;
+      if (tree) {
+        int r = t;
+        for (int d = dep; d >= 0; --d) {
+          if (d == lane) pr = r;
+          r = r > 0 ? c.tree[ILL_TR_PARENT + r] : 0;
+        }
+      }
+      path[lane] = pr;
     }
-    path[w][lane] = tree ? pr : lane;
+    qs[lane] = c.q[(size_t)t * ILL_H + h * 64 + lane] * 0.125f;
   }
-  qs[w][lane] = c.q[(size_t)t * ILL_H + h * 64 + lane] * 0.125f;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __syncthreads();
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
   float Mx = -INFINITY, Ls = 0.f, O = 0.f;
   const int nch = (L + 63) >> 6;
-  for (int ch = 0; ch < nch; ch++) {
+  for (int ch = w; ch < nch; ch += NW) {
     const int vp = 64 * ch + lane;
     const bool valid = vp < L;
-    const int slot = min(vp < pos || !tree ? vp : pos + path[w][min(vp - pos, 15)], c.maxctx - 1);
+    const int slot = min(vp < pos || !tree ? vp : pos + path[min(vp - pos, 15)], c.maxctx - 1);
     // score of position vp (lane = position)
     const uint4* kr = (const uint4*)(kb + (size_t)slot * 64);
+    uint4 kv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
+    // P.V operands for dim = lane (transposed V: 64 slots per row), issued with K
+    const uint4* vr = (const uint4*)(vb + ((size_t)ch * 64 + lane) * 64);
+    uint4 vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const uint4 u = gld(kr + i);
-      const uint32_t x[4] = {u.x, u.y, u.z, u.w};
+      const uint32_t x[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
 #pragma unroll
-      for (int e = 0; e < 8; e++) s = fmaf(qs[w][8 * i + e], h2f(x[e >> 1] >> (16 * (e & 1))), s);
+      for (int e = 0; e < 8; e++) s = fmaf(qs[8 * i + e], h2f(x[e >> 1] >> (16 * (e & 1))), s);
     }
     s = valid ? s : -INFINITY;
     const float mc = gmax<64>(s);
@@ -359,20 +461,17 @@ __global__ __launch_bounds__(256) void op_attn_kernel(OpCtx c, int layer, int M)
     ps[w][lane] = p;
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // P.V for dim = lane over the chunk's 64 positions (transposed V: 64 slots per row)
-    const uint4* vr = (const uint4*)(vb + ((size_t)ch * 64 + lane) * 64);
     float oc = 0.f;
     const bool remap = tree && 64 * ch + 63 >= pos;   // wave-uniform
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const uint4 u = gld(vr + i);
-      const uint32_t x[4] = {u.x, u.y, u.z, u.w};
+      const uint32_t x[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const int pp = 8 * i + e, vq = 64 * ch + pp;
         float v = h2f(x[e >> 1] >> (16 * (e & 1)));
         if (remap && vq >= pos && vq < L) {
-          const int sl = pos + path[w][vq - pos];
+          const int sl = pos + path[vq - pos];
           v = h2f(vb[((size_t)(sl >> 6) * 64 + lane) * 64 + (sl & 63)]);
         }
         v = vq < L ? v : 0.f;
@@ -385,7 +484,25 @@ __global__ __launch_bounds__(256) void op_attn_kernel(OpCtx c, int layer, int M)
     Ls = att_fold(Ls, lc, k);
     Mx = k.mn;
   }
-  c.ao[(size_t)t * ILL_H + h * 64 + lane] = __float2half(O / Ls);
+  if (lane == 0) {
+    cm[w] = Mx;
+    cl[w] = Ls;
+  }
+  co[w][lane] = O;
+  __syncthreads();
+  if (w == 0) {
+    float m = cm[0];
+#pragma unroll
+    for (int ww = 1; ww < NW; ww++) m = fmaxf(m, cm[ww]);
+    float sum = 0.f, o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ww++) {
+      const float e = att_exp(cm[ww] - m);
+      sum = sum + cl[ww] * e;
+      o = o + co[ww][lane] * e;
+    }
+    c.ao[(size_t)t * ILL_H + h * 64 + lane] = __float2half(o / sum);
+  }
 }
 
 // ---- commit ----------------------------------------------------------------------------

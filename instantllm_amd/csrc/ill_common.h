@@ -20,7 +20,11 @@
 #define ILL_KST 7            // 896 / 128 column blocks per K = 896 row tile
 #define ILL_NGU 76           // 4864 / 64 hidden-unit blocks of the fused gate/up/down role
 #define ILL_XA_N 15          // contributions to the post-attention residual: 14 heads + base
-#define ILL_XB_N 77          // contributions to the post-MLP residual: 76 unit blocks + base
+// The post-MLP residual XB is accumulated in ILL_XB_COPIES copies (unit block ub adds into
+// copy ub % ILL_XB_COPIES, the base into copy 0) that its readers add up: fewer
+// contributors per cache line, so the atomics land sooner.
+#define ILL_XB_COPIES 4
+#define ILL_NKIND (1 + ILL_XB_COPIES)   // accumulator kinds per layer: XA, XB copies
 #define ILL_NOT 56           // 896 / 16 row tiles of O and down
 #define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV
 

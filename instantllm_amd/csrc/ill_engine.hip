@@ -493,7 +493,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     return hipMemset(*p, 0, bytes) == hipSuccess;
   };
   const size_t kvb = (size_t)layers * ILL_NKV * e->maxctx * 64 * 2;
-  e->acc_bytes = (size_t)2 * layers * 2 * 16 * ILL_H * 8;
+  e->acc_bytes = (size_t)2 * layers * ILL_NKIND * 16 * ILL_H * 8;
   bool ok = dalloc((void**)&e->dlayers, sizeof(IllLayerW) * layers) && dalloc((void**)&e->st, 64) && dalloc((void**)&e->ctl, 64) &&
             dalloc((void**)&e->ptoks, ILL_OP_MAXM * 4) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&

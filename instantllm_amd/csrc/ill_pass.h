@@ -143,8 +143,14 @@ __device__ __forceinline__ void fx_add(uint64_t* p, uint64_t w) {
 }
 
 __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int l, int kind, int t) {
-  return a.acc + ((((size_t)bank * a.W.layers + l) * 2 + kind) * 16 + t) * ILL_H;
+  return a.acc + ((((size_t)bank * a.W.layers + l) * ILL_NKIND + kind) * 16 + t) * ILL_H;
 }
+// XB copies in use: 16-row passes read every word 16 times over, so they keep one copy
+template <int T>
+__host__ __device__ constexpr int xb_copies() { return T == 1 ? ILL_XB_COPIES : 1; }
+// contributions expected in XB copy c
+template <int T>
+__device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>() + (c == 0 ? 1 : 0); }
 
 // ---- activation sources for prep896 --------------------------------------------------
 // Residual accumulator row (complete when every word has `expect` contributions).
@@ -155,6 +161,25 @@ struct SrcAcc {
     const uint64_t w = aload64(base + (size_t)t * ILL_H + c);
     v = fx_float(fx_value(w));
     return fx_count(w) == expect;
+  }
+};
+
+// Post-MLP residual XB[l]: the sum of its copies (kinds 1 .. ILL_XB_COPIES), complete when
+// every copy has its contributions.
+template <int T>
+struct SrcXB {
+  const uint64_t* base;   // copy 0, row 0; copies are 16 rows apart
+  __device__ __forceinline__ bool load1(int t, int c, float& v) const {
+    bool ok = true;
+    int64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < xb_copies<T>(); k++) {
+      const uint64_t w = aload64(base + ((size_t)k * 16 + t) * ILL_H + c);
+      ok &= fx_count(w) == xb_expect<T>(k);
+      sum += fx_value(w);
+    }
+    v = fx_float(sum);
+    return ok;
   }
 };
 
@@ -684,7 +709,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
-  else ok = prep896<T>(SrcAcc{acc_ptr(a, H.bank, l - 1, 1, 0), ILL_XB_N}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
+  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, 1, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
   // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
@@ -702,10 +727,12 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     q4_tile896_lds<T>(st + ILL_KST * 1024, st + 2 * ILL_KST * 1024 + ILL_KST * 128, A.u.prep, lane, acc1);
     trace_mark(a, ILL_TRL * l + 3);
   }
-  // the wave's first cache chunk streams in while the QKV epilogue runs (always issued, so
-  // later waits can count the loads in flight; chunk 0 stands in when the wave has none)
-  kv_fetch(kbase, vbase, cfirst >= 0 ? cfirst : 0, lane, f);
-  fc = cfirst;
+  // the wave's first cache chunk streams in while the QKV epilogue runs (waves without
+  // attention work issue nothing: the fetch costs the CU's memory-issue bandwidth)
+  if (cfirst >= 0) {
+    kv_fetch(kbase, vbase, cfirst, lane, f);
+    fc = cfirst;
+  }
   if (w < 6) {
     const int b = att_block(h, w);
     const int head = b >> 1;
@@ -948,7 +975,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 5);
   split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, 1, 0) + 16 * 7 * w);
+                acc_ptr(a, H.bank, l, 1 + ub % xb_copies<T>(), 0) + 16 * 7 * w);
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -988,11 +1015,18 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
     }
   } else {
     const uint64_t* prev = acc_ptr(a, H.bank, l - 1, 1, 0);
-    if (!wait_full(prev, ILL_XB_N, 800 + l)) return false;
+#pragma unroll
+    for (int c = 0; c < xb_copies<T>(); c++)
+      if (!wait_full(prev + (size_t)c * 16 * ILL_H, xb_expect<T>(c), 800 + l)) return false;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
       const int i = tid + k * ILL_WG_THREADS;
-      if (i < n) fx_add(xa + i, fx_word(fx_value(aload64(prev + i))));
+      if (i < n) {
+        int64_t sum = 0;
+#pragma unroll
+        for (int c = 0; c < xb_copies<T>(); c++) sum += fx_value(aload64(prev + (size_t)c * 16 * ILL_H + i));
+        fx_add(xa + i, fx_word(sum));
+      }
     }
   }
   if (!wait_full(xa, ILL_XA_N, 850 + l)) return false;
@@ -1025,7 +1059,7 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, NL - 1, 1, 0), ILL_XB_N}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
+    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, 1, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {
@@ -1082,14 +1116,14 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
   const int NL = a.W.layers;
   const size_t per_row = ILL_H;
   const int other = H.bank ^ 1;
-  const size_t nrow_total = (size_t)NL * 2 * H.zrows;   // (layer, kind, row) triples
+  const size_t nrow_total = (size_t)NL * ILL_NKIND * H.zrows;   // (layer, kind, row) triples
   const size_t total = nrow_total * per_row;
   const size_t chunk = (total + ILL_WG - 1) / ILL_WG;
   const size_t lo = (size_t)blockIdx.x * chunk, hi = min(total, lo + chunk);
   for (size_t i = lo + tid_opaque(); i < hi; i += ILL_WG_THREADS) {
     const size_t r = i / per_row, c = i % per_row;
     const size_t lk = r / H.zrows, t = r % H.zrows;
-    gst(a.acc + ((((size_t)other * NL) * 2 + lk) * 16 + t) * ILL_H + c, (uint64_t)0);
+    gst(a.acc + ((((size_t)other * NL) * ILL_NKIND + lk) * 16 + t) * ILL_H + c, (uint64_t)0);
   }
 }
 

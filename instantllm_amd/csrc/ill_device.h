@@ -279,11 +279,6 @@ struct PrepLds {
 template <int T>
 __device__ __forceinline__ int arow(int m) { return T == 1 ? 0 : (m & (T - 1)); }
 
-// Accumulate one 16-row tile over K = 896: acc[j] (rows t = 4*kg + j of the pass, weight
-// row n) += sum_G s*d*S + m*X. The per-value operation sequence is independent of T.
-// `fetch(cb, w, s)` supplies block cb's 16 weight bytes and (scale, min) pairs for this lane.
-// The body has no branches, so the compiler can issue every operand read of the tile
-// before the first MFMA; rows >= nrows produce values that callers ignore.
 // Opaque copy of a per-lane value: address arithmetic derived from it is redone at each use
 // instead of being hoisted out of enclosing loops into long-lived registers.
 __device__ __forceinline__ int opq(int v) {
@@ -291,45 +286,85 @@ __device__ __forceinline__ int opq(int v) {
   return v;
 }
 
-template <int T, class Fetch>
-__device__ __forceinline__ void q4_tile896f(Fetch fetch, const PrepLds<T>& P, int lane_, float acc[4]) {
+// A operand of group G for this lane at T = 1: the tile's 16 output rows need one input
+// row, so lane rows m = 0 and 1 carry its high and low bytes and one MFMA gives both
+// products (D row 0 = hi . W, row 1 = lo . W: the same integers as two MFMAs would).
+template <int T>
+__device__ __forceinline__ const uint4* t1_abase(const PrepLds<T>& P, int lane) {
+  return (lane & 1) ? P.alo : P.ahi;
+}
+
+// Accumulate 16-row tiles over K = 896: acc[i][j] (rows t = 4*kg + j of the pass, weight
+// row n of tile i) += sum_G s*d*S + m*X. The per-value operation sequence is independent
+// of T. `fetch(i, cb, w, s)` supplies tile i's block cb: 16 weight bytes and the (scale,
+// min) pairs for this lane. The body has no branches, so the compiler can issue every
+// operand read before the first MFMA; rows >= nrows produce values that callers ignore.
+// With NT > 1 (T = 1 only) the tiles share each group's A-operand read and their MFMA
+// chains interleave.
+template <int T, int NT, class Fetch>
+__device__ __forceinline__ void q4_tiles896f(Fetch fetch, const PrepLds<T>& P, int lane_, float (*acc)[4]) {
+  static_assert(T == 1 || NT == 1, "interleaved tiles at T = 1 only");
   const int lane = opq(lane_);
   const int kg = lane >> 4, m = arow<T>(lane & 15);
   constexpr int RPL = T >= 4 ? 4 : T;
-  uint4 wv[ILL_KST];
-  uint2 sv[ILL_KST];
+  uint4 wv[NT][ILL_KST];
+  uint2 sv[NT][ILL_KST];
 #pragma unroll
-  for (int cb = 0; cb < ILL_KST; cb++) fetch(cb, wv[cb], sv[cb]);
+  for (int i = 0; i < NT; i++) {
+#pragma unroll
+    for (int cb = 0; cb < ILL_KST; cb++) fetch(i, cb, wv[i][cb], sv[i][cb]);
+  }
+  const v4i z = {0, 0, 0, 0};
+  const uint4* a1 = t1_abase<T>(P, lane);
 #pragma unroll
   for (int G = 0; G < 2 * ILL_KST; G++) {
     const int cb = G >> 1, gi = G & 1;
-    const v4i b = gi == 0 ? q4_unpack(wv[cb].x, wv[cb].y) : q4_unpack(wv[cb].z, wv[cb].w);
-    const uint4 h = P.ahi[(G * 4 + kg) * T + m];
-    const uint4 l = P.alo[(G * 4 + kg) * T + m];
-    const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
-    const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
-    const v4i z = {0, 0, 0, 0};
-    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
-    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-    const uint32_t sm = gi == 0 ? sv[cb].x : sv[cb].y;
-    const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+    if (T == 1) {
+      const uint4 x = a1[G * 4 + kg];
+      const v4i ax = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+      const float2 dx = P.sc[G];
 #pragma unroll
-    for (int j = 0; j < RPL; j++) {
-      const float2 dx = P.sc[G * T + arow<T>(4 * kg + j)];
-      const int S = (dh[j] << 8) + dl[j];
-      const float t1 = dx.x * (float)S;
-      acc[j] = fmaf(sw, t1, acc[j]);
-      acc[j] = fmaf(mw, dx.y, acc[j]);
-    }
-    // At T > 1 each group needs 4 rows of (d, X): pin each group's epilogue to its group
-    // and bound the scheduler's read-ahead to two groups, so the operands and MFMA results
-    // of a whole tile are not held in registers at once.
-    if (T > 1) {
+      for (int i = 0; i < NT; i++) {
+        const v4i b = gi == 0 ? q4_unpack(wv[i][cb].x, wv[i][cb].y) : q4_unpack(wv[i][cb].z, wv[i][cb].w);
+        const v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, b, z, 0, 0, 0);
+        const uint32_t sm = gi == 0 ? sv[i][cb].x : sv[i][cb].y;
+        const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+        const int S = (dd[0] << 8) + dd[1];
+        const float t1 = dx.x * (float)S;
+        acc[i][0] = fmaf(sw, t1, acc[i][0]);
+        acc[i][0] = fmaf(mw, dx.y, acc[i][0]);
+      }
+    } else {
+      const v4i b = gi == 0 ? q4_unpack(wv[0][cb].x, wv[0][cb].y) : q4_unpack(wv[0][cb].z, wv[0][cb].w);
+      const uint4 h = P.ahi[(G * 4 + kg) * T + m];
+      const uint4 l = P.alo[(G * 4 + kg) * T + m];
+      const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
+      const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
+      const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+      const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+      const uint32_t sm = gi == 0 ? sv[0][cb].x : sv[0][cb].y;
+      const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
 #pragma unroll
-      for (int j = 0; j < RPL; j++) asm volatile("" : "+v"(acc[j]));
+      for (int j = 0; j < RPL; j++) {
+        const float2 dx = P.sc[G * T + arow<T>(4 * kg + j)];
+        const int S = (dh[j] << 8) + dl[j];
+        const float t1 = dx.x * (float)S;
+        acc[0][j] = fmaf(sw, t1, acc[0][j]);
+        acc[0][j] = fmaf(mw, dx.y, acc[0][j]);
+      }
+      // At T > 1 each group needs 4 rows of (d, X): pin each group's epilogue to its group
+      // and bound the scheduler's read-ahead to two groups, so the operands and MFMA
+      // results of a whole tile are not held in registers at once.
+#pragma unroll
+      for (int j = 0; j < RPL; j++) asm volatile("" : "+v"(acc[0][j]));
       if (G & 1) __builtin_amdgcn_sched_barrier(0);
     }
   }
+}
+
+template <int T, class Fetch>
+__device__ __forceinline__ void q4_tile896f(Fetch fetch, const PrepLds<T>& P, int lane, float acc[4]) {
+  q4_tiles896f<T, 1>([&](int, int cb, uint4& w, uint2& s) { fetch(cb, w, s); }, P, lane, (float(*)[4])acc);
 }
 
 // Tile held in registers (lm_head stream).
@@ -345,5 +380,16 @@ __device__ __forceinline__ void q4_tile896_lds(const uint8_t* w, const uint8_t* 
   q4_tile896f<T>([&](int cb, uint4& wv, uint2& sv) {
     wv = *(const uint4*)(w + cb * 1024 + lane * 16);
     sv = *(const uint2*)(s + cb * 128 + n * 8);
+  }, P, lane, acc);
+}
+
+// NT tiles staged in LDS one after the other, `stride` bytes apart, each as
+// [7 x 1 KiB weights][7 x 128 B scales].
+template <int T, int NT>
+__device__ __forceinline__ void q4_tiles896_lds(const uint8_t* base, int stride, const PrepLds<T>& P, int lane, float (*acc)[4]) {
+  const int n = lane & 15;
+  q4_tiles896f<T, NT>([&](int i, int cb, uint4& wv, uint2& sv) {
+    wv = *(const uint4*)(base + i * stride + cb * 1024 + lane * 16);
+    sv = *(const uint2*)(base + i * stride + ILL_KST * 1024 + cb * 128 + n * 8);
   }, P, lane, acc);
 }

@@ -305,7 +305,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     quant_store<T>(q0[t], m0[t] * (1.0f / ILL_QMAX), s0[t], t, P.ahi + w * 4 * T, P.alo + w * 4 * T, P.sc + w * T, gi, p, lane);
     if (two) quant_store<T>(q1[t], m1[t] * (1.0f / ILL_QMAX), s1[t], t, P.ahi + G1 * 4 * T, P.alo + G1 * 4 * T, P.sc + G1 * T, gi, p, lane);
   }
-  if (trs >= 0) trace_mark(a, trs + 1);
+  if (trs >= 0 && (trs + 1) % ILL_TRL != 0) trace_mark(a, trs + 1);
   lds_barrier();
   return true;
 }
@@ -314,12 +314,13 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
 // ---- weight staging in LDS ----------------------------------------------------------------
 // Each role copies the next layer's weights HBM -> LDS (global_load_lds) as soon as it has
 // finished the current layer, per wave, into a dynamic-LDS stage of ILL_STAGE_BYTES:
-//   ATT  QKV: wave w < 6 at w * 16128: [tile 2b: 7 KiB][tile 2b+1: 7 KiB][scales 2 x 896 B]
+//   ATT  QKV: row tile lt (0-11) at lt * 8064: [7 KiB codes][7 x 128 B scales], staged by
+//             the wave that computes it
 //        O:   wave w at w * 4032: [7 row tiles x 512 B][7 x 64 B scales] (loaded after QKV)
 //   GUD  GU:  wave w at w * 8064: [7 KiB][896 B]
 //        down: wave w at 64512 + w * 4032: [7 x 512 B][7 x 64 B]
 #define ILL_STAGE_BYTES 96768
-#define ILL_ST_QKV 16128
+#define ILL_ST_TILE 8064
 // At T = 1 the static LDS is small, so the ATT role keeps its O weights in a region of
 // their own after the QKV block and stages both at the end of the previous layer.
 __host__ __device__ constexpr int ill_stage_bytes(int T) { return T == 1 ? ILL_STAGE_BYTES + 8 * 4032 : ILL_STAGE_BYTES; }
@@ -387,21 +388,40 @@ union PassLds {
   CommitLds cm;
 };
 
-// ATT workgroup weights: waves 0-5 one 32-row QKV block each (q_h halves, k_g halves,
-// v_g halves); every wave 7 row tiles of O's head-h columns.
-__device__ __forceinline__ int att_block(int h, int w) {
+// ATT workgroup weights: six 32-row QKV blocks bw (q_h halves, k_g halves, v_g halves;
+// att_block gives the block of the fused matrix) and every wave 7 row tiles of O's head-h
+// columns. Row tile lt = 2 bw + hf is half hf of block bw (dims d, or d + 32, of the head,
+// d = 16 (block & 1) + n). Wave w computes qkv_nt(w) tiles from qkv_lt0(w):
+//   T = 1: waves 0-3 both halves of blocks 0-3 (q and k: a RoPE pair stays in one lane),
+//          waves 4-7 one half of a v block each, so each SIMD (waves w, w + 4) runs 3 tiles;
+//   T > 1: waves 0-5 both halves of block w.
+__device__ __forceinline__ int att_block(int h, int bw) {
   const int g = h / 7;
-  return w < 2 ? 2 * h + w : (w < 4 ? 28 + 2 * g + (w - 2) : 32 + 2 * g + (w - 4));
+  return bw < 2 ? 2 * h + bw : (bw < 4 ? 28 + 2 * g + (bw - 2) : 32 + 2 * g + (bw - 4));
 }
+template <int T>
+__device__ __forceinline__ int qkv_nt(int w) { return T == 1 ? (w < 4 ? 2 : 1) : (w < 6 ? 2 : 0); }
+template <int T>
+__device__ __forceinline__ int qkv_lt0(int w) { return T == 1 && w >= 4 ? w + 4 : 2 * w; }
 
+template <int T>
 __device__ __forceinline__ void att_stage_qkv(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
-  if (w < 6) {
-    const int b = att_block(h, w);
-    uint8_t* d = stage + w * ILL_ST_QKV;
-    wave_copy_to_lds(L.wqkv + (size_t)(2 * b) * ILL_KST * 1024, d, 2 * ILL_KST * 1024, lane);
-    wave_copy_to_lds((const uint8_t*)(L.sqkv + (2 * b) * ILL_KST * 32), d + 2 * ILL_KST * 1024, 2 * ILL_KST * 128, lane);
+  const int nt = qkv_nt<T>(w), lt0 = qkv_lt0<T>(w);
+  for (int i = 0; i < nt; i++) {
+    const int lt = lt0 + i;
+    const int r = 2 * att_block(h, lt >> 1) + (lt & 1);   // row tile of the fused QKV matrix
+    uint8_t* d = stage + lt * ILL_ST_TILE;
+    wave_copy_to_lds(L.wqkv + (size_t)r * ILL_KST * 1024, d, ILL_KST * 1024, lane);
+    wave_copy_to_lds((const uint8_t*)(L.sqkv + r * ILL_KST * 32), d + ILL_KST * 1024, ILL_KST * 128, lane);
   }
 }
+
+// Attention work is dealt out by slot: slot j holds the shared chunks c = j (mod 8) and the
+// partial pairs numbered j - ns (mod 8). At T = 1 slot j runs on wave (j + 4) % 8, so the
+// shared chunks go first to the waves with one QKV tile; at T > 1 on wave (j + 6) % 8, the
+// waves without QKV tiles first. (The mapping is its own inverse at T = 1.)
+template <int T>
+__device__ __forceinline__ int att_slot(int w) { return (w + (T == 1 ? 4 : 2)) & 7; }
 
 template <int T>
 __device__ __forceinline__ void att_stage_o(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
@@ -619,7 +639,9 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
                                            int lane, int nrows, uint64_t* accw) {
   const int kg = lane >> 4, n = lane & 15;
   constexpr int RPL = T >= 4 ? 4 : T;
-  const uint4 xh = ahi[kg * T + arow<T>(n)], xl = alo[kg * T + arow<T>(n)];
+  // at T = 1 lane rows alternate the high and low bytes of the one input row (one MFMA)
+  const uint4 xh = T == 1 ? ((lane & 1) ? alo : ahi)[kg] : ahi[kg * T + arow<T>(n)];
+  const uint4 xl = alo[kg * T + arow<T>(n)];
   const v4i ah = (v4i){(int)xh.x, (int)xh.y, (int)xh.z, (int)xh.w};
   const v4i al = (v4i){(int)xl.x, (int)xl.y, (int)xl.z, (int)xl.w};
   const v4i z = {0, 0, 0, 0};
@@ -638,11 +660,11 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
   for (int k = 0; k < 7; k++) {
     const v4i bq = q4_unpack(wv[k].x, wv[k].y);
     const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
-    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
+    const v4i dl = T == 1 ? dh : __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
     const float sw = h2f(sm[k] & 0xffff), mw = h2f(sm[k] >> 16);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
-      const int Sv = (dh[j] << 8) + dl[j];
+      const int Sv = T == 1 ? (dh[0] << 8) + dh[1] : (dh[j] << 8) + dl[j];
       float v = 0.f;
       v = fmaf(sw, dx[j].x * (float)Sv, v);
       v = fmaf(mw, dx[j].y, v);
@@ -682,12 +704,14 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   const int nrows = H.nrows;
   const int pos = H.pos;
   // QKV epilogue constants (independent of the input): bias and RoPE (cos, sin) per row
-  const int d = (att_block(h, w < 6 ? w : 0) & 1) * 16 + n;
+  const int nt = qkv_nt<T>(w), lt0 = qkv_lt0<T>(w);
+  const int bw = lt0 >> 1, hf1 = nt == 1 ? (lt0 & 1) : 0;   // block; a single tile's half
+  const int d = (att_block(h, nt > 0 ? bw : 0) & 1) * 16 + n;
   float bias0 = 0.f, bias1 = 0.f;
   float2 rope[4] = {};
-  if (w < 6) {
-    const int b = att_block(h, w);
-    bias0 = gld(L.bqkv + 32 * b + n);
+  if (nt > 0) {
+    const int b = att_block(h, bw);
+    bias0 = gld(L.bqkv + 32 * b + 16 * hf1 + n);
     bias1 = gld(L.bqkv + 32 * b + 16 + n);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
@@ -695,46 +719,67 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       if (t < nrows) rope[j] = gld(a.rope + (pos + H.depth[t]) * 32 + d);
     }
   }
-  // ---- attention work of this wave: shared chunks w, w + 8, ... < ns, then the partial
-  // pairs idx = w - ns (mod 8), + 8, ...
+  // ---- attention work of this wave's slot sj: shared chunks sj, sj + 8, ... < ns, then
+  // the partial pairs idx = sj - ns (mod 8), + 8, ...
+  const int sj = att_slot<T>(w);
   int maxL = 0;
   for (int t = 0; t < nrows; t++) maxL = max(maxL, pos + H.depth[t] + 1);
   const int ns = pos >> 6, cmax = (maxL - 1) >> 6;
-  const int pidx0 = (w - ns) & 7;
+  const int pidx0 = (sj - ns) & 7;
   const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
   const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
-  const int cfirst = w < ns ? w : att_pair_chunk(H, ns, cmax, pidx0);
+  const int cfirst = sj < ns ? sj : att_pair_chunk(H, ns, cmax, pidx0);
   KVFrag f;
   int fc = -1;   // cache chunk held in f
-  // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
-  bool ok;
-  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
-  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, 1, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
-  if (!ok) return false;
-  trace_mark(a, ILL_TRL * l + 1);
-  // ---- q_h, k_g, v_g rows (waves 0-5: one 32-row rotary block each)
-  float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
-  wait_vm();   // every wave: its staged weights and the epilogue constants (nothing else is in flight)
-  // pin the epilogue constants here: a load sunk to its use would be issued after the K/V
-  // fetch below, and waiting for it would then wait for the whole fetch
-  asm volatile("" ::"v"(bias0), "v"(bias1));
-#pragma unroll
-  for (int j = 0; j < RPL; j++) asm volatile("" ::"v"(rope[j].x), "v"(rope[j].y));
-  trace_mark(a, ILL_TRL * l + 2);
-  if (w < 6) {
-    const uint8_t* st = stage + w * ILL_ST_QKV;
-    q4_tile896_lds<T>(st, st + 2 * ILL_KST * 1024, A.u.prep, lane, acc0);
-    q4_tile896_lds<T>(st + ILL_KST * 1024, st + 2 * ILL_KST * 1024 + ILL_KST * 128, A.u.prep, lane, acc1);
-    trace_mark(a, ILL_TRL * l + 3);
-  }
-  // the wave's first cache chunk streams in while the QKV epilogue runs (waves without
-  // attention work issue nothing: the fetch costs the CU's memory-issue bandwidth)
+  // The slot's first chunk streams in while the input is awaited: cache positions below pos
+  // were written by earlier passes, and the positions of this pass are taken from LDS.
+  // (Waves without attention work issue nothing: a fetch costs the CU's memory-issue
+  // bandwidth.)
   if (cfirst >= 0) {
     kv_fetch(kbase, vbase, cfirst, lane, f);
     fc = cfirst;
   }
-  if (w < 6) {
-    const int b = att_block(h, w);
+  // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
+  bool ok;
+  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
+  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, 1, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, ILL_TRL * l + 15);
+  if (!ok) return false;
+  trace_mark(a, ILL_TRL * l + 1);
+  // ---- q_h, k_g, v_g rows (the wave's row tiles, see qkv_nt)
+  float acc0[4] = {0.f, 0.f, 0.f, 0.f}, acc1[4] = {0.f, 0.f, 0.f, 0.f};
+  wait_vm();   // every wave: its staged weights, the epilogue constants and its first chunk
+  // pin the epilogue constants here: a load sunk to its use would be waited for in the
+  // middle of the attention work
+  asm volatile("" ::"v"(bias0), "v"(bias1));
+#pragma unroll
+  for (int j = 0; j < RPL; j++) asm volatile("" ::"v"(rope[j].x), "v"(rope[j].y));
+  trace_mark(a, ILL_TRL * l + 2);
+  const uint8_t* st = stage + lt0 * ILL_ST_TILE;
+  if constexpr (T == 1) {
+    float accs[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    if (nt == 2) q4_tiles896_lds<T, 2>(st, ILL_ST_TILE, A.u.prep, lane, accs);
+    else q4_tiles896_lds<T, 1>(st, ILL_ST_TILE, A.u.prep, lane, accs);
+    acc0[0] = accs[0][0];
+    acc1[0] = accs[1][0];
+    trace_mark(a, ILL_TRL * l + 3);
+  } else if (nt > 0) {
+    q4_tile896_lds<T>(st, st + ILL_KST * 1024, A.u.prep, lane, acc0);
+    q4_tile896_lds<T>(st + ILL_ST_TILE, st + ILL_ST_TILE + ILL_KST * 1024, A.u.prep, lane, acc1);
+    trace_mark(a, ILL_TRL * l + 3);
+  }
+  if (nt == 1) {   // T = 1, one half of a v block: no RoPE
+    const int dim = d + 32 * hf1;
+    const bool writer = (h % 7) == 0;
+    if (kg == 0) {
+      const uint32_t h0 = f2h(acc0[0] + bias0);
+      A.v[0][dim] = (uint16_t)h0;
+      if (writer) {
+        uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + pos / 64) * 64 * 64;
+        gst(vb + dim * 64 + (pos & 63), (uint16_t)h0);
+      }
+    }
+  } else if (nt == 2) {
+    const int b = att_block(h, bw);
     const int head = b >> 1;
     const bool writer = (h % 7) == 0;   // one query head per group writes the K/V cache
 #pragma unroll
@@ -811,7 +856,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
-  for (int c = w; c < ns; c += ILL_WAVES) {
+  for (int c = sj; c < ns; c += ILL_WAVES) {
     if (c != fc) {
       kv_fetch(kbase, vbase, c, lane, f);
       fc = c;
@@ -862,11 +907,11 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     const int t = 4 * kg + j;
     if (t < T) {
       if (n == 0) {
-        A.u.c.cm[w][t] = M[j];
-        A.u.c.cl[w][t] = Lw[j];
+        A.u.c.cm[sj][t] = M[j];
+        A.u.c.cl[sj][t] = Lw[j];
       }
 #pragma unroll
-      for (int nb = 0; nb < 4; nb++) A.u.c.co[w][t][16 * nb + n] = O[nb][j];
+      for (int nb = 0; nb < 4; nb++) A.u.c.co[sj][t][16 * nb + n] = O[nb][j];
     }
   }
   lds_barrier();
@@ -1273,14 +1318,14 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   if (wg >= ILL_R_ATT0 && wg < ILL_R_ATT0 + ILL_NATT) {
     const int h = wg - ILL_R_ATT0;
-    att_stage_qkv(a.L[0], h, w, lane, ill_stage);
+    att_stage_qkv<T>(a.L[0], h, w, lane, ill_stage);
     if (T == 1) att_stage_o<T>(a.L[0], h, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
       trace_mark(a, ILL_TRL * l);
       if (!role_att<T>(a, H, S.att, l, h, ill_stage)) return;
       lds_barrier();   // every wave is done with the stage before it is refilled
       if (l + 1 < NL) {
-        att_stage_qkv(a.L[l + 1], h, w, lane, ill_stage);
+        att_stage_qkv<T>(a.L[l + 1], h, w, lane, ill_stage);
         if (T == 1) att_stage_o<T>(a.L[l + 1], h, w, lane, ill_stage);
       }
       trace_mark(a, ILL_TRL * l + 11);

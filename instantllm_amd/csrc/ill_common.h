@@ -19,12 +19,16 @@
 // Device layout unit sizes (q4): a "block" is 16 rows x 128 columns = 2 quant groups.
 #define ILL_KST 7            // 896 / 128 column blocks per K = 896 row tile
 #define ILL_NGU 76           // 4864 / 64 hidden-unit blocks of the fused gate/up/down role
-#define ILL_XA_N 15          // contributions to the post-attention residual: 14 heads + base
-// The post-MLP residual XB is accumulated in ILL_XB_COPIES copies (unit block ub adds into
-// copy ub % ILL_XB_COPIES, the base into copy 0) that its readers add up: fewer
-// contributors per cache line, so the atomics land sooner.
+// The residual accumulators of a 1-row pass are kept in copies that their readers add up:
+// fewer contributors per cache line, so the atomics land sooner. The post-attention
+// residual XA has ILL_XA_COPIES (head h adds into copy h % ILL_XA_COPIES), the post-MLP
+// residual XB ILL_XB_COPIES (unit block ub into copy ub % ILL_XB_COPIES); the base adds
+// into copy 0 of each.
+#ifndef ILL_XA_COPIES
+#define ILL_XA_COPIES 2
+#endif
 #define ILL_XB_COPIES 4
-#define ILL_NKIND (1 + ILL_XB_COPIES)   // accumulator kinds per layer: XA, XB copies
+#define ILL_NKIND (ILL_XA_COPIES + ILL_XB_COPIES)   // accumulator kinds per layer: XA, XB copies
 #define ILL_NOT 56           // 896 / 16 row tiles of O and down
 #define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV
 

@@ -145,43 +145,44 @@ __device__ __forceinline__ void fx_add(uint64_t* p, uint64_t w) {
 __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int l, int kind, int t) {
   return a.acc + ((((size_t)bank * a.W.layers + l) * ILL_NKIND + kind) * 16 + t) * ILL_H;
 }
-// XB copies in use: 16-row passes read every word 16 times over, so they keep one copy
+// Copies in use: 16-row passes read every word 16 times over, so they keep one of each.
+// Kinds per layer: XA copies 0 .. xa_copies - 1, XB copies from ILL_XA_COPIES on.
+template <int T>
+__host__ __device__ constexpr int xa_copies() { return T == 1 ? ILL_XA_COPIES : 1; }
 template <int T>
 __host__ __device__ constexpr int xb_copies() { return T == 1 ? ILL_XB_COPIES : 1; }
-// contributions expected in XB copy c
+#define ILL_KIND_XB ILL_XA_COPIES
+// contributions expected in XA copy c (heads, plus the base in copy 0) and XB copy c
+template <int T>
+__device__ __forceinline__ int xa_expect(int c) { return ILL_NATT / xa_copies<T>() + (c == 0 ? 1 : 0); }
 template <int T>
 __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>() + (c == 0 ? 1 : 0); }
 
 // ---- activation sources for prep896 --------------------------------------------------
-// Residual accumulator row (complete when every word has `expect` contributions).
-struct SrcAcc {
-  const uint64_t* base;   // row 0; rows are ILL_H apart
-  int expect;
+// A residual accumulator: the sum of its copies (16 rows apart), complete when every copy
+// has its contributions. XB = false: the post-attention residual XA[l] (kinds 0 ..), true:
+// the post-MLP residual XB[l] (kinds ILL_KIND_XB ..).
+template <int T, bool XB>
+struct SrcRes {
+  const uint64_t* base;   // copy 0, row 0
   __device__ __forceinline__ bool load1(int t, int c, float& v) const {
-    const uint64_t w = aload64(base + (size_t)t * ILL_H + c);
-    v = fx_float(fx_value(w));
-    return fx_count(w) == expect;
-  }
-};
-
-// Post-MLP residual XB[l]: the sum of its copies (kinds 1 .. ILL_XB_COPIES), complete when
-// every copy has its contributions.
-template <int T>
-struct SrcXB {
-  const uint64_t* base;   // copy 0, row 0; copies are 16 rows apart
-  __device__ __forceinline__ bool load1(int t, int c, float& v) const {
+    constexpr int NC = XB ? xb_copies<T>() : xa_copies<T>();
     bool ok = true;
     int64_t sum = 0;
 #pragma unroll
-    for (int k = 0; k < xb_copies<T>(); k++) {
+    for (int k = 0; k < NC; k++) {
       const uint64_t w = aload64(base + ((size_t)k * 16 + t) * ILL_H + c);
-      ok &= fx_count(w) == xb_expect<T>(k);
+      ok &= fx_count(w) == (XB ? xb_expect<T>(k) : xa_expect<T>(k));
       sum += fx_value(w);
     }
     v = fx_float(sum);
     return ok;
   }
 };
+template <int T>
+using SrcXB = SrcRes<T, true>;
+template <int T>
+using SrcXA = SrcRes<T, false>;
 
 // Embedding rows (layer-0 input), dequantized from the tiled q4 table: w = s*q + m
 // (Shaders.swift:118-126 semantics).
@@ -350,12 +351,17 @@ struct AttLds {
   float q[T][64];
   uint16_t k[T][64];
   uint16_t v[T][64];
-  float o[T][64];
   float pm[2][T], pl[2][T];   // statistics of the partial chunks ns + i per row
   float po[2][T][64];
   uint4 ahi[4 * T], alo[4 * T];
   float2 dsc[T];
+  float p1[T == 1 ? ILL_WAVES : 1][64];   // T = 1: the waves' P scratch, outside the union
 };
+
+// Per-wave scratch [T][64] for a chunk's probabilities. At T = 1 it lies outside the region
+// the combine state reuses, so no barrier separates the last chunk from the state writes.
+template <int T>
+__device__ __forceinline__ float* att_pbuf(AttLds<T>& A, int w) { return T == 1 ? &A.p1[w][0] : &A.u.P[w][0][0]; }
 
 template <int T>
 struct GudLds {
@@ -506,18 +512,30 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
   const int pos = H.pos;
   const int Lt = part ? pos + H.depth[t1] + 1 : 0x7fffffff;
   const uint4 zz = make_uint4(0, 0, 0, 0);
+  float* pb = att_pbuf<T>(A, w);
   // pass rows on row t1's path for this lane's key positions
   int rk[4] = {0, 0, 0, 0};   // at T = 1 the only pass row is row 0 at position pos
   if (T > 1 && part) {
 #pragma unroll
     for (int b = 0; b < 4; b++) rk[b] = min(H.prow[t1][min(max(64 * c + 16 * b + n - pos, 0), 15)], T - 1);
   }
+  // T = 1: the key at pos is the pass row's (from LDS); keys above pos are masked through
+  // their scores, so their cache contents are never used
+  uint4 kp0 = zz, kp1 = zz;
+  if (T == 1 && part) {
+    kp0 = *(const uint4*)&A.k[0][8 * kg];
+    kp1 = *(const uint4*)&A.k[0][32 + 8 * kg];
+  }
   float sc[4][4];
 #pragma unroll
   for (int b = 0; b < 4; b++) {
     const int vp = 64 * c + 16 * b + n;
     uint4 k0 = f.k[b][0], k1 = f.k[b][1];
-    if (part) {
+    if (T == 1 && part) {
+      const uint32_t mp = mask_of(vp == pos);
+      k0 = msel4(mp, kp0, k0);
+      k1 = msel4(mp, kp1, k1);
+    } else if (part) {
       const uint4 l0 = *(const uint4*)&A.k[rk[b]][8 * kg];
       const uint4 l1 = *(const uint4*)&A.k[rk[b]][32 + 8 * kg];
       const uint32_t mc = mask_of(vp < pos), ml = mask_of(vp >= pos && vp < Lt);
@@ -553,7 +571,7 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
     const int t = 4 * kg + j;
     if (t < T) {
 #pragma unroll
-      for (int b = 0; b < 4; b++) A.u.P[w][t][16 * b + n] = sc[b][j];
+      for (int b = 0; b < 4; b++) pb[t * 64 + 16 * b + n] = sc[b][j];
     }
   }
   wave_lds_sync();
@@ -562,32 +580,41 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
   for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float p = A.u.P[w][arow<T>(n)][32 * ks + 8 * kg + i];
+      const float p = pb[arow<T>(n) * 64 + 32 * ks + 8 * kg + i];
       const _Float16 hi = (_Float16)p;
       ph[ks][i] = hi;
       pl[ks][i] = (_Float16)(p - (float)hi);
     }
   }
   wave_lds_sync();
+  // T = 1: V at positions below pos from the cache, at pos the pass row's, above pos zero.
+  // This lane's 8 positions 32 ks + 8 kg + i of the chunk keep the first nk cache values;
+  // the one 32-bit word holding pos (wave-uniform ks, word and half) takes the pass row.
+  const int dp = pos - 64 * c;
+  uint32_t km[2][4];
+  if (T == 1 && part) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const int nk = min(max(dp - 32 * ks - 8 * kg, 0), 8);
+#pragma unroll
+      for (int wi = 0; wi < 4; wi++) km[ks][wi] = nk >= 2 * wi + 2 ? 0xffffffffu : (nk == 2 * wi + 1 ? 0xffffu : 0u);
+    }
+  }
 #pragma unroll
   for (int nb = 0; nb < 4; nb++) {
     const int dim = 16 * nb + n;
     v8h vv[2];
+    uint32_t lvs = 0;
+    if (T == 1 && part) lvs = kg == ((dp >> 3) & 3) ? (uint32_t)A.v[0][dim] << (16 * (dp & 1)) : 0u;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       uint4 u = f.v[nb][ks];
       if (T == 1 && part) {
-        // the new position pos holds the pass row; later positions hold no key
-        const uint32_t lv = A.v[0][dim];
-        uint32_t e[8];
-        const uint32_t x[4] = {u.x, u.y, u.z, u.w};
+        uint32_t x[4] = {u.x & km[ks][0], u.y & km[ks][1], u.z & km[ks][2], u.w & km[ks][3]};
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const int d = 64 * c + 32 * ks + 8 * kg + i - pos;
-          const uint32_t cv = (x[i >> 1] >> (16 * (i & 1))) & 0xffff;
-          e[i] = msel(mask_of(d < 0), cv, lv & mask_of(d == 0));
-        }
-        u = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+        for (int wi = 0; wi < 4; wi++)
+          if (ks == (dp >> 5) && wi == ((dp >> 1) & 3)) x[wi] |= lvs;
+        u = make_uint4(x[0], x[1], x[2], x[3]);
       } else if (part) {
         // positions >= pos: row t1's path table (zero beyond its depth); positions >= pos + 16 hold no key
         const uint16_t* vpt = (const uint16_t*)(stage + ILL_ST_VPT) + ((size_t)t1 * 64 + dim) * 16;
@@ -742,7 +769,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
-  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, 1, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, ILL_TRL * l + 15);
+  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, ILL_TRL * l + 15);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
   // ---- q_h, k_g, v_g rows (the wave's row tiles, see qkv_nt)
@@ -900,7 +927,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     }
   }
   trace_mark(a, ILL_TRL * l + 6);
-  lds_barrier();   // LDS: P region becomes the combine region
+  if (T > 1) lds_barrier();   // LDS: the P region becomes the combine region
   trace_mark(a, ILL_TRL * l + 13);
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -916,10 +943,18 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   }
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 14);
-  // combine: wave states (+ the partial chunks of each wave, in chunk order), then across
-  // waves against the global maximum
-  for (int i = tid_opaque(); i < nrows * 64; i += ILL_WG_THREADS) {
-    const int t = i >> 6, dim = i & 63;
+  // combine: slot states (+ the partial chunks of each slot, in chunk order), then across
+  // slots against the global maximum; row t by wave t % 8, one dim per lane, then the row
+  // is coded as the A operand of the O projection (one quant group: head h's columns)
+  for (int t = w; t < T; t += ILL_WAVES) {
+    if (t >= nrows) {
+      if (lane < 4) {
+        A.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
+        A.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
+      }
+      continue;
+    }
+    const int dim = lane;
     const int Lt = pos + H.depth[t] + 1;
     float sm[ILL_WAVES], sl[ILL_WAVES], so[ILL_WAVES];
 #pragma unroll
@@ -948,23 +983,15 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       sum = sum + sl[ww] * e;
       o = o + so[ww] * e;
     }
-    A.o[t][dim] = o / sum;
+    quant_row64<T>(o / sum, t, A.ahi, A.alo, A.dsc, lane);
   }
-  lds_barrier();
   trace_mark(a, ILL_TRL * l + 7);
-  // ---- O projection restricted to head h's columns (one quant group): rows t by wave t % 8
-  for (int t = w; t < T; t += ILL_WAVES) {
-    if (t < nrows) quant_row64<T>(A.o[t][lane], t, A.ahi, A.alo, A.dsc, lane);
-    else if (lane < 4) {
-      A.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
-      A.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
-    }
-  }
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 8);
   wait_vm();   // this wave's staged O tiles
   trace_mark(a, ILL_TRL * l + 9);
-  split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows, acc_ptr(a, H.bank, l, 0, 0) + 16 * 7 * w);
+  split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows,
+                acc_ptr(a, H.bank, l, h % xa_copies<T>(), 0) + 16 * 7 * w);
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -989,7 +1016,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   const IllLayerW& L = a.L[l];
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
-  if (!prep896<T>(SrcAcc{acc_ptr(a, H.bank, l, 0, 0), ILL_XA_N}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, ILL_TRL * l + 6)) return false;
+  if (!prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, ILL_TRL * l + 6)) return false;
   trace_mark(a, ILL_TRL * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1020,7 +1047,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 5);
   split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, 1 + ub % xb_copies<T>(), 0) + 16 * 7 * w);
+                acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + 16 * 7 * w);
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -1051,7 +1078,7 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
     }, a.ctl, code);
   };
   uint64_t* xa = acc_ptr(a, H.bank, l, 0, 0);
-  uint64_t* xb = acc_ptr(a, H.bank, l, 1, 0);
+  uint64_t* xb = acc_ptr(a, H.bank, l, ILL_KIND_XB, 0);
   if (l == 0) {
 #pragma unroll
     for (int k = 0; k < PER; k++) {
@@ -1059,7 +1086,7 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
       if (i < n) fx_add(xa + i, fx_word(fx_of(embed1(a.W, H.tok[i / ILL_H], i % ILL_H))));
     }
   } else {
-    const uint64_t* prev = acc_ptr(a, H.bank, l - 1, 1, 0);
+    const uint64_t* prev = acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0);
 #pragma unroll
     for (int c = 0; c < xb_copies<T>(); c++)
       if (!wait_full(prev + (size_t)c * 16 * ILL_H, xb_expect<T>(c), 800 + l)) return false;
@@ -1074,11 +1101,18 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
       }
     }
   }
-  if (!wait_full(xa, ILL_XA_N, 850 + l)) return false;
+#pragma unroll
+  for (int c = 0; c < xa_copies<T>(); c++)
+    if (!wait_full(xa + (size_t)c * 16 * ILL_H, xa_expect<T>(c), 850 + l)) return false;
 #pragma unroll
   for (int k = 0; k < PER; k++) {
     const int i = tid + k * ILL_WG_THREADS;
-    if (i < n) fx_add(xb + i, fx_word(fx_value(aload64(xa + i))));
+    if (i < n) {
+      int64_t sum = 0;
+#pragma unroll
+      for (int c = 0; c < xa_copies<T>(); c++) sum += fx_value(aload64(xa + (size_t)c * 16 * ILL_H + i));
+      fx_add(xb + i, fx_word(sum));
+    }
   }
   return true;
 }
@@ -1104,7 +1138,7 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, 1, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
+    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {

@@ -315,12 +315,20 @@ __device__ __forceinline__ void q4_tiles896f(Fetch fetch, const PrepLds<T>& P, i
     for (int cb = 0; cb < ILL_KST; cb++) fetch(i, cb, wv[i][cb], sv[i][cb]);
   }
   const v4i z = {0, 0, 0, 0};
-  const uint4* a1 = t1_abase<T>(P, lane);
+  // T = 1: every A operand is read before the first MFMA (the group chain would otherwise
+  // wait for each read in turn)
+  uint4 xa[T == 1 ? 2 * ILL_KST : 1];
+  if (T == 1) {
+    const uint4* a1 = t1_abase<T>(P, lane);
+#pragma unroll
+    for (int G = 0; G < 2 * ILL_KST; G++) xa[G] = a1[G * 4 + kg];
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int G = 0; G < 2 * ILL_KST; G++) {
     const int cb = G >> 1, gi = G & 1;
     if (T == 1) {
-      const uint4 x = a1[G * 4 + kg];
+      const uint4 x = xa[G];
       const v4i ax = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
       const float2 dx = P.sc[G];
 #pragma unroll

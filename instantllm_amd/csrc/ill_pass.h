@@ -600,12 +600,16 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
       for (int wi = 0; wi < 4; wi++) km[ks][wi] = nk >= 2 * wi + 2 ? 0xffffffffu : (nk == 2 * wi + 1 ? 0xffffu : 0u);
     }
   }
+  uint32_t lv1[4] = {0u, 0u, 0u, 0u};   // T = 1: the pass row's V, read by every lane
+  if (T == 1 && part) {
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) lv1[nb] = A.v[0][16 * nb + n];
+  }
 #pragma unroll
   for (int nb = 0; nb < 4; nb++) {
     const int dim = 16 * nb + n;
     v8h vv[2];
-    uint32_t lvs = 0;
-    if (T == 1 && part) lvs = kg == ((dp >> 3) & 3) ? (uint32_t)A.v[0][dim] << (16 * (dp & 1)) : 0u;
+    const uint32_t lvs = msel(mask_of(kg == ((dp >> 3) & 3)), lv1[nb] << (16 * (dp & 1)), 0u);
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       uint4 u = f.v[nb][ks];
@@ -883,13 +887,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
-  for (int c = sj; c < ns; c += ILL_WAVES) {
-    if (c != fc) {
-      kv_fetch(kbase, vbase, c, lane, f);
-      fc = c;
-    }
-    float mx[4], ls[4], o[4][4];
-    chunk_eval<T>(H, A, stage, f, c, false, 0, qa, mx, ls, o);
+  auto fold = [&](const float mx[4], const float ls[4], const float o[4][4]) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const AttScale k = att_scale(M[j], mx[j]);
@@ -898,8 +896,29 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       Lw[j] = att_fold(Lw[j], ls[j], k);
       M[j] = k.mn;
     }
+  };
+  for (int c = sj; c < ns; c += ILL_WAVES) {
+    if (c != fc) {
+      kv_fetch(kbase, vbase, c, lane, f);
+      fc = c;
+    }
+    float mx[4], ls[4], o[4][4];
+    chunk_eval<T>(H, A, stage, f, c, false, 0, qa, mx, ls, o);
+    fold(mx, ls, o);
   }
-  {
+  if constexpr (T == 1) {
+    // the one partial pair (chunk ns, row 0) belongs to slot ns % 8, whose wave folds it
+    // into the slot state after the slot's shared chunks, as the combine would
+    if (sj == (ns & 7)) {
+      if (ns != fc) {
+        kv_fetch(kbase, vbase, ns, lane, f);
+        fc = ns;
+      }
+      float mx[4], ls[4], o[4][4];
+      chunk_eval<T>(H, A, stage, f, ns, true, 0, qa, mx, ls, o);
+      fold(mx, ls, o);
+    }
+  } else {
     int idx = 0;
     for (int c = ns; c <= cmax; c++) {
       for (int t1 = 0; t1 < nrows; t1++) {
@@ -963,7 +982,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       sl[ww] = A.u.c.cl[ww][t];
       so[ww] = A.u.c.co[ww][t][dim];
 #pragma unroll
-      for (int ci = 0; ci < 2; ci++) {
+      for (int ci = 0; ci < (T > 1 ? 2 : 0); ci++) {   // at T = 1 the slot's wave folded it
         const int c = ns + ci;
         if ((c & 7) == ww && c <= cmax && Lt > 64 * c) {
           const AttScale k = att_scale(sm[ww], A.pm[ci][t]);

@@ -125,10 +125,13 @@ __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
 #define FX_SCALE 16777216.0f        // 2^24
 #define FX_INV (1.0f / 16777216.0f)
 
+// round(v * 2^24), clamped to |q| <= 2^47, as hi * 2^31 + lo with |lo| < 2^31: both parts
+// are exact in float (lo is a sub-range of the 24 significant bits of the scaled value).
 __device__ __forceinline__ int64_t fx_of(float v) {
-  int64_t q = __float2ll_rn(v * FX_SCALE);
-  const int64_t lim = FX_BIAS - 1;
-  return q > lim ? lim : (q < -lim ? -lim : q);
+  const float x = rintf(__builtin_amdgcn_fmed3f(v * FX_SCALE, -140737488355328.0f, 140737488355328.0f));
+  const float hf = truncf(x * 4.656612873077393e-10f);   // 2^-31
+  const float lf = fmaf(hf, -2147483648.0f, x);
+  return (int64_t)(int)hf * 2147483648ll + (int64_t)(int)lf;
 }
 __device__ __forceinline__ uint64_t fx_word(int64_t q) { return FX_COUNT + (uint64_t)(q + FX_BIAS); }
 // value of a completed accumulator word (count = n contributions)
@@ -665,13 +668,46 @@ __device__ __forceinline__ float att_fold(float x, float x2, const AttScale& k) 
 // layout [7 x 512 B codes][7 x 64 B scales]). Each output y = s*d*S + m*X is added to
 // row t < nrows of the accumulator (`accw` = row 0, element 112 w) as a fixed-point
 // contribution. All operand reads and MFMAs come before the atomics.
+// At T = 1 the lane rows alternate the high and low bytes of the one input row, so one
+// MFMA per tile gives S in every lane: lane (kg, n) finishes only tiles kg and 4 + kg
+// (< 7), two outputs and two atomics per lane where the 16-row form has seven of each.
+// The arithmetic of each output is the same in both forms.
 template <int T>
 __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, const uint4* alo, const float2* dsc,
                                            int lane, int nrows, uint64_t* accw) {
   const int kg = lane >> 4, n = lane & 15;
   constexpr int RPL = T >= 4 ? 4 : T;
-  // at T = 1 lane rows alternate the high and low bytes of the one input row (one MFMA)
-  const uint4 xh = T == 1 ? ((lane & 1) ? alo : ahi)[kg] : ahi[kg * T + arow<T>(n)];
+  if constexpr (T == 1) {
+    const uint4 x = ((lane & 1) ? alo : ahi)[kg];
+    const v4i ax = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+    const v4i z = {0, 0, 0, 0};
+    uint2 wv[7];
+#pragma unroll
+    for (int k = 0; k < 7; k++) wv[k] = *(const uint2*)(so + k * 512 + lane * 8);
+    const int ka = kg, kb = 4 + min(kg, 2);
+    const uint32_t sa = *(const uint32_t*)(so + 7 * 512 + ka * 64 + n * 4);
+    const uint32_t sb = *(const uint32_t*)(so + 7 * 512 + kb * 64 + n * 4);
+    const float2 dx = dsc[0];
+    int S[7];
+#pragma unroll
+    for (int k = 0; k < 7; k++) {
+      const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, q4_unpack(wv[k].x, wv[k].y), z, 0, 0, 0);
+      S[k] = (d[0] << 8) + d[1];
+    }
+    const int Sa = kg == 0 ? S[0] : kg == 1 ? S[1] : kg == 2 ? S[2] : S[3];
+    const int Sb = kg == 0 ? S[4] : kg == 1 ? S[5] : S[6];
+    auto out = [&](int Sv, uint32_t smv) {
+      float v = 0.f;
+      v = fmaf(h2f(smv & 0xffff), dx.x * (float)Sv, v);
+      v = fmaf(h2f(smv >> 16), dx.y, v);
+      return v;
+    };
+    const float ya = out(Sa, sa), yb = out(Sb, sb);
+    fx_add(accw + 16 * ka + n, fx_word(fx_of(ya)));
+    if (kg < 3) fx_add(accw + 16 * kb + n, fx_word(fx_of(yb)));
+    return;
+  }
+  const uint4 xh = ahi[kg * T + arow<T>(n)];
   const uint4 xl = alo[kg * T + arow<T>(n)];
   const v4i ah = (v4i){(int)xh.x, (int)xh.y, (int)xh.z, (int)xh.w};
   const v4i al = (v4i){(int)xl.x, (int)xl.y, (int)xl.z, (int)xl.w};
@@ -691,11 +727,11 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
   for (int k = 0; k < 7; k++) {
     const v4i bq = q4_unpack(wv[k].x, wv[k].y);
     const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
-    const v4i dl = T == 1 ? dh : __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
+    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
     const float sw = h2f(sm[k] & 0xffff), mw = h2f(sm[k] >> 16);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
-      const int Sv = T == 1 ? (dh[0] << 8) + dh[1] : (dh[j] << 8) + dl[j];
+      const int Sv = (dh[j] << 8) + dl[j];
       float v = 0.f;
       v = fmaf(sw, dx[j].x * (float)Sv, v);
       v = fmaf(mw, dx[j].y, v);

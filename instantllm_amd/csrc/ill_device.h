@@ -171,9 +171,15 @@ __device__ __forceinline__ V group_reduce(V v, Op op) {
 struct OpAddF { __device__ float operator()(float a, float b) const { return a + b; } };
 struct OpMaxF { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
 struct OpAddI { __device__ int operator()(int a, int b) const { return a + b; } };
+struct OpMaxU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
 template <int N> __device__ __forceinline__ float gsum(float v) { return group_reduce<N>(v, OpAddF{}); }
 template <int N> __device__ __forceinline__ float gmax(float v) { return group_reduce<N>(v, OpMaxF{}); }
 template <int N> __device__ __forceinline__ int gsumi(int v) { return group_reduce<N>(v, OpAddI{}); }
+// max |v| over the group, as an integer maximum of the magnitudes' bit patterns (ordered
+// like the values for non-negative floats)
+template <int N> __device__ __forceinline__ float gmaxabs(float v) {
+  return __uint_as_float(group_reduce<N>(__float_as_uint(v) & 0x7fffffffu, OpMaxU{}));
+}
 
 // Order-preserving 64-bit key of (value, index): larger value first, then lower index.
 __device__ __forceinline__ uint64_t amax_key(float v, int idx) {
@@ -271,7 +277,9 @@ struct PrepLds {
   uint4 alo[14 * 4 * T];
   float2 sc[14 * T];
   float red[ILL_WAVES][T];   // per-wave partial sums of squares
-  int ok[ILL_WAVES];         // per-wave "input complete" votes
+  float gm[14][T];           // per-group max |x * gamma|
+  int gq[14][T];             // per-group sum of the codes
+  alignas(16) int ok[ILL_WAVES];   // per-wave "input complete" votes
 };
 
 // MFMA A-operand row read by lane row m: at T = 1 every lane row aliases row 0, so the

@@ -223,30 +223,50 @@ __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 
 
 // One row (64 values, one per lane) -> 16-bit coding as a K = 64 MFMA operand:
 // lane (kg, m = row) of the operand holds units 16 kg + q4perm(p); operand k-group gi of
-// row t is at [gi * T + t].
+// row t is at [gi * T + t]. Lane c of a 16-lane row codes unit c, byte p = q4perm_inv(c)
+// of its row's 16 bytes: the lanes c, c + 2, c + 4, c + 6 ((c & 6) == 0) fill bytes 0-3
+// of dword ((c & 8) >> 2) | (c & 1), so two DPP row shifts gather each dword into one lane,
+// which stores it.
+#define ILL_DPP_SHL2 0x102   // row_shl:2 (lane l reads lane l + 2 of its row)
+#define ILL_DPP_SHL4 0x104   // row_shl:4
 template <int T>
-__device__ __forceinline__ void quant_store(int qv, float d, int sq, int t, uint4* ahi, uint4* alo, float2* dsc, int gi, int p, int lane) {
+__device__ __forceinline__ void quant_store(int qv, int t, uint4* ahi, uint4* alo, int lane) {
   const int hi = (qv + 128) >> 8, lo = qv - (hi << 8);
-  ((uint8_t*)&ahi[gi * T + t])[p] = (uint8_t)(hi & 0xff);
-  ((uint8_t*)&alo[gi * T + t])[p] = (uint8_t)(lo & 0xff);
-  if (lane == 0) dsc[t] = make_float2(d, d * (float)sq);
+  uint32_t h = (uint32_t)hi & 0xff, l = (uint32_t)lo & 0xff;
+  h |= (uint32_t)dpp_i<ILL_DPP_SHL2>((int)h) << 8;
+  l |= (uint32_t)dpp_i<ILL_DPP_SHL2>((int)l) << 8;
+  h |= (uint32_t)dpp_i<ILL_DPP_SHL4>((int)h) << 16;
+  l |= (uint32_t)dpp_i<ILL_DPP_SHL4>((int)l) << 16;
+  if ((lane & 6) == 0) {
+    const int gi = lane >> 4, dw = ((lane & 8) >> 2) | (lane & 1);
+    ((uint32_t*)&ahi[gi * T + t])[dw] = h;
+    ((uint32_t*)&alo[gi * T + t])[dw] = l;
+  }
+}
+// The codes of a group: v = rint(x * 32639 / max|x|) (0 for an all-zero group).
+__device__ __forceinline__ int quant_code(float x, float mx) {
+  return (int)rintf(x * (mx > 0.f ? ILL_QMAX * __builtin_amdgcn_rcpf(mx) : 0.f));
 }
 template <int T>
 __device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* alo, float2* dsc, int lane) {
-  const float mx = gmax<64>(fabsf(h));
-  const float d = mx * (1.0f / ILL_QMAX);
-  const int qv = (int)rintf(h * (d > 0.f ? __builtin_amdgcn_rcpf(d) : 0.f));
+  const float mx = gmaxabs<64>(h);
+  const int qv = quant_code(h, mx);
   const int sq = gsumi<64>(qv);
-  quant_store<T>(qv, d, sq, t, ahi, alo, dsc, lane >> 4, q4perm_inv(lane & 15), lane);
+  quant_store<T>(qv, t, ahi, alo, lane);
+  const float d = mx * (1.0f / ILL_QMAX);
+  if (lane == 0) dsc[t] = make_float2(d, d * (float)sq);
 }
 
 // RMSNorm + 16-bit fixed-point coding of rows 0..nrows-1 of a K = 896 input into MFMA
 // operands, spread over the whole workgroup: wave w owns column groups w and w + 8 (< 14)
 // of every row, one column per lane. Every wave polls its own columns until they are
 // complete, so the input is taken one memory round trip after its last contribution
-// lands. Rows >= nrows are coded as zeros. Per row: ss = sum over waves (in order) of the
-// wave's sum of squares; x * rsqrt(ss / 896 + eps) * gamma; each group coded as in
-// quant_row64. The sequence for a row does not depend on T.
+// lands. Rows >= nrows are coded as zeros. The norm scale of a row is one positive factor,
+// so it only scales each group's step: per row, u = x * gamma is coded per group as
+// v = rint(u * 32639 / max|u|) before the workgroup barrier, together with the wave's sum
+// of squares of x; after it every wave forms the group steps
+// d = max|u| * rsqrt(ss / 896 + eps) / 32639 itself (ss = sum over waves in order), so no
+// second barrier is needed. The sequence for a row does not depend on T.
 template <int T, class Src>
 __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds<T>& P,
                                         IllCtl* ctl, int code, const IllPassArgs& a, int trs = -1) {
@@ -270,50 +290,62 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     return ok;
   }, ctl, code);
   if (trs >= 0) trace_mark(a, trs);
+  // stage by stage over blocks of up to 4 rows, so the rows' reduction chains interleave
+  constexpr int RB = T < 4 ? T : 4;
 #pragma unroll
-  for (int t = 0; t < T; t++) {
-    const float s = gsum<64>(v0[t] * v0[t] + v1[t] * v1[t]);
-    if (lane == 0) P.red[w][t] = s;
+  for (int t0 = 0; t0 < T; t0 += RB) {
+    float u0[RB], u1[RB], m0[RB], m1[RB], ss[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      const int t = t0 + r;
+      ss[r] = gsum<64>(v0[t] * v0[t] + v1[t] * v1[t]);
+      u0[r] = v0[t] * g0;
+      u1[r] = v1[t] * g1;
+      m0[r] = gmaxabs<64>(u0[r]);
+      m1[r] = gmaxabs<64>(u1[r]);
+    }
+    int q0[RB], q1[RB], s0[RB], s1[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      q0[r] = quant_code(u0[r], m0[r]);
+      q1[r] = quant_code(u1[r], m1[r]);
+      s0[r] = gsumi<64>(q0[r]);
+      s1[r] = gsumi<64>(q1[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      const int t = t0 + r;
+      quant_store<T>(q0[r], t, P.ahi + w * 4 * T, P.alo + w * 4 * T, lane);
+      if (two) quant_store<T>(q1[r], t, P.ahi + G1 * 4 * T, P.alo + G1 * 4 * T, lane);
+      if (lane == 0) {
+        P.red[w][t] = ss[r];
+        P.gm[w][t] = m0[r];
+        P.gq[w][t] = s0[r];
+        if (two) {
+          P.gm[G1][t] = m1[r];
+          P.gq[G1][t] = s1[r];
+        }
+      }
+    }
   }
   if (lane == 0) P.ok[w] = alive;
-  lds_barrier();
-  bool all = true;
-#pragma unroll
-  for (int ww = 0; ww < ILL_WAVES; ww++) all &= P.ok[ww] != 0;
-  if (!all) return false;
-  // stage by stage over all rows, so the rows' reduction chains interleave
-  float m0[T], m1[T];
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    float ss = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < ILL_WAVES; ww++) ss += P.red[ww][t];
-    const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / (float)ILL_H) + ILL_EPS);
-    v0[t] = v0[t] * scale * g0;
-    v1[t] = v1[t] * scale * g1;
-    m0[t] = gmax<64>(fabsf(v0[t]));
-    m1[t] = gmax<64>(fabsf(v1[t]));
-  }
-  int q0[T], q1[T], s0[T], s1[T];
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    const float d0 = m0[t] * (1.0f / ILL_QMAX), d1 = m1[t] * (1.0f / ILL_QMAX);
-    q0[t] = (int)rintf(v0[t] * (d0 > 0.f ? __builtin_amdgcn_rcpf(d0) : 0.f));
-    q1[t] = (int)rintf(v1[t] * (d1 > 0.f ? __builtin_amdgcn_rcpf(d1) : 0.f));
-    s0[t] = gsumi<64>(q0[t]);
-    s1[t] = gsumi<64>(q1[t]);
-  }
-  const int gi = lane >> 4, p = q4perm_inv(lane & 15);
-#pragma unroll
-  for (int t = 0; t < T; t++) {
-    quant_store<T>(q0[t], m0[t] * (1.0f / ILL_QMAX), s0[t], t, P.ahi + w * 4 * T, P.alo + w * 4 * T, P.sc + w * T, gi, p, lane);
-    if (two) quant_store<T>(q1[t], m1[t] * (1.0f / ILL_QMAX), s1[t], t, P.ahi + G1 * 4 * T, P.alo + G1 * 4 * T, P.sc + G1 * T, gi, p, lane);
-  }
   if (trs >= 0 && (trs + 1) % ILL_TRL != 0) trace_mark(a, trs + 1);
   lds_barrier();
+  const int4 ok0 = *(const int4*)&P.ok[0], ok1 = *(const int4*)&P.ok[4];
+  if ((ok0.x & ok0.y & ok0.z & ok0.w & ok1.x & ok1.y & ok1.z & ok1.w) == 0) return false;
+  // group steps (d, d * sum v) of every (group, row), written by every wave (the same values)
+  for (int i = lane; i < 14 * T; i += 64) {
+    const int G = i / T, t = i - G * T;
+    float sst = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < ILL_WAVES; ww++) sst += P.red[ww][t];
+    const float scale = __builtin_amdgcn_rsqf(sst * (1.0f / (float)ILL_H) + ILL_EPS);
+    const float d = P.gm[G][t] * scale * (1.0f / ILL_QMAX);
+    P.sc[G * T + t] = make_float2(d, d * (float)P.gq[G][t]);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's own writes, read below
   return true;
 }
-
 
 // ---- weight staging in LDS ----------------------------------------------------------------
 // Each role copies the next layer's weights HBM -> LDS (global_load_lds) as soon as it has

@@ -578,10 +578,13 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
       k1 = msel4(mc, k1, msel4(ml, l1, zz));
     }
     v4f s = {0.f, 0.f, 0.f, 0.f};
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], u4_to_v8h(k0), s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], u4_to_v8h(k0), s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], u4_to_v8h(k1), s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(k1), s, 0, 0, 0);
+    // T = 1: a key block wholly above pos is all masked; its MFMAs are skipped (wave-uniform)
+    if (!(T == 1 && part && 16 * b > pos - 64 * c)) {
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], u4_to_v8h(k0), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], u4_to_v8h(k0), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], u4_to_v8h(k1), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(k1), s, 0, 0, 0);
+    }
     const bool valid = vp < Lt;
 #pragma unroll
     for (int j = 0; j < 4; j++) sc[b][j] = valid ? s[j] : -INFINITY;
@@ -673,8 +676,12 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], acc, 0, 0, 0);
+    // T = 1: positions 32 .. 63 of the chunk all above pos hold p = 0 and v = 0 (skipped;
+    // adding them would add zeros)
+    if (!(T == 1 && part && dp < 32)) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], acc, 0, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) o[nb][j] = acc[j];
   }

@@ -38,8 +38,8 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
 # a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (165,954.4 x 2 + 16,022.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 356_281_280
+# (169,523.25 x 2 + 16,694.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 364_278_464
 
 
 def step_bytes(L: float) -> float:
@@ -164,6 +164,11 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV microbench")
     ap.add_argument("--no-config4", action="store_true", help="skip the q8 / f16 prefill and decode runs")
+    ap.add_argument("--dispatch", choices=("graph", "single"), default="graph",
+                    help="graph: the timed steps are one captured hipGraph (default); single: each "
+                         "step is its own launch, timed with HIP events around its kernel, and prompts "
+                         "are prefilled through 16-row passes (for profilers that do not follow graph "
+                         "launches)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (the reference dispatch "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -193,11 +198,28 @@ def main() -> int:
     e = Engine(path, max_context=1024, max_pass=16, max_steps=max(4096, K + W + 16))
     no_eos = (-5, -5)   # the reference's idsbench disables the stop ids (main.swift:165)
 
+    single = args.dispatch == "single"
+
+    def prefill(toks: list[int]) -> None:
+        if not single:
+            e.prefill(toks)
+            return
+        for i in range(0, len(toks), 16):   # 16-row passes of the pass kernel
+            e.prefill(toks[i:i + 16])
+
     def run(nsteps: int) -> tuple[float, float, float]:
         e.reset_out_tokens()
-        e.set_state(pos=0, n=len(prompt), maxsteps=nsteps + 1, eos=no_eos)
-        e.prefill(prompt)
+        e.set_state(pos=0, n=len(prompt), maxsteps=nsteps + 64, eos=no_eos)
+        prefill(prompt)
         e.sync()
+        if single:
+            ms_dev = 0.0
+            t0 = time.perf_counter()
+            for _ in range(nsteps):
+                e.decode_step()
+                ms_dev += e.last_pass_ms()   # HIP events around the step's kernel
+            t1 = time.perf_counter()
+            return (t1 - t0) * 1e3, ms_dev, e.get_state()["pos"]
         e.capture_steps(nsteps)
         e.sync()
         t0 = time.perf_counter()
@@ -210,7 +232,7 @@ def main() -> int:
     wall_ms, dev_ms, pos_end = run(K)
     if pos_end != len(prompt) + K:
         raise RuntimeError(f"decode did not advance: pos {pos_end}")
-    toks = e.out_tokens()[: K + 1].tolist()
+    toks = e.out_tokens()[: K + 1].tolist() if not single else []
     us_tok = dev_ms * 1e3 / K
     L_avg = len(prompt) + (K + 1) / 2.0
     achieved = step_bytes(L_avg) / (us_tok * 1e-6) / 1e9
@@ -218,11 +240,12 @@ def main() -> int:
     # 16-row tree-verify pass (config 3): prefix 512, 15 drafts + root
     vr = np.random.default_rng(3)
     vprompt = [int(t) for t in vr.integers(0, F.VOCAB, size=512)]
-    e.set_state(pos=0, n=512, maxsteps=64, eos=no_eos)
-    e.prefill(vprompt)
+    e.reset_out_tokens()
+    e.set_state(pos=0, n=512, maxsteps=128, eos=no_eos)
+    prefill(vprompt)
     st = e.get_state()
     tree = random_tree(vr, 16, F.VOCAB)
-    tree[33] = int(e.out_tokens()[0])
+    tree[33] = int(e.out_tokens()[st["step"] - 1])
     verify_us = []
     for _ in range(5):
         e.set_state(pos=st["pos"], n=16, maxsteps=64, eos=no_eos)
@@ -254,13 +277,15 @@ def main() -> int:
         "dtype": "int8 MFMA (q4 weights, 16-bit fixed-point activations) + f32",
         "data": "synthetic (seeded random weights and token ids)",
         "config": {"workload": "config 2: q4 1-row greedy decode, Qwen2.5-0.5B shape (24L, d896, 14/2 heads, "
-                               "FFN 4864, vocab 151936), prefix KV 256, each step one persistent kernel in a hipGraph",
+                               "FFN 4864, vocab 151936), prefix KV 256, each step one persistent kernel "
+                               + ("in a hipGraph" if not single else "launched on its own (--dispatch single)"),
                    "prefix": len(prompt), "model_seed": 2, "first_tokens": toks[:8]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES_PER_STEP,
                      "note": f"bytes(L)={step_bytes(L_avg):.0f} at mean L={L_avg:.1f}; dominant kernel "
-                             "ill_pass_kernel<1> (the whole step), duration from HIP events over the timed graph; "
-                             "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE "
+                             "ill_pass_kernel<1> (the whole step), duration from HIP events "
+                             + ("over the timed graph; " if not single else "around each step's kernel; ")
+                             + "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE "
                              "(profiles/pass_kernel_q4_decode_config2.md)"},
     }
     if not args.no_gemv:

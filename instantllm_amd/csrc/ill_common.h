@@ -27,7 +27,9 @@
 #ifndef ILL_XA_COPIES
 #define ILL_XA_COPIES 2
 #endif
-#define ILL_XB_COPIES 4
+#ifndef ILL_XB_COPIES
+#define ILL_XB_COPIES 2
+#endif
 #define ILL_NKIND (ILL_XA_COPIES + ILL_XB_COPIES)   // accumulator kinds per layer: XA, XB copies
 #define ILL_NOT 56           // 896 / 16 row tiles of O and down
 #define ILL_NQB 36           // 1152 / 32 rotary blocks of QKV

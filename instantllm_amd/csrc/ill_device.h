@@ -275,11 +275,9 @@ template <int T>
 struct PrepLds {
   uint4 ahi[14 * 4 * T];
   uint4 alo[14 * 4 * T];
-  float2 sc[14 * T];
-  float red[ILL_WAVES][T];   // per-wave partial sums of squares
-  float gm[14][T];           // per-group max |x * gamma|
-  int gq[14][T];             // per-group sum of the codes
-  alignas(16) int ok[ILL_WAVES];   // per-wave "input complete" votes
+  float2 sc[14 * T];          // per (group, row): step d and d * sum of the codes
+  alignas(16) float red[ILL_WAVES][T];   // per-wave partial sums of squares
+  alignas(16) int ok[ILL_WAVES];         // per-wave "input complete" votes
 };
 
 // MFMA A-operand row read by lane row m: at T = 1 every lane row aliases row 0, so the

@@ -261,15 +261,16 @@ __device__ __forceinline__ void quant_row64(float h, int t, uint4* ahi, uint4* a
 // operands, spread over the whole workgroup: wave w owns column groups w and w + 8 (< 14)
 // of every row, one column per lane. Every wave polls its own columns until they are
 // complete, so the input is taken one memory round trip after its last contribution
-// lands. Rows >= nrows are coded as zeros. The norm scale of a row is one positive factor,
-// so it only scales each group's step: per row, u = x * gamma is coded per group as
-// v = rint(u * 32639 / max|u|) before the workgroup barrier, together with the wave's sum
-// of squares of x; after it every wave forms the group steps
-// d = max|u| * rsqrt(ss / 896 + eps) / 32639 itself (ss = sum over waves in order), so no
-// second barrier is needed. The sequence for a row does not depend on T.
+// lands. Rows >= nrows are coded as zeros. The norm scale of a row is one positive factor
+// of the whole row, so it is left out of the coding and applied to the products: per row,
+// u = x * gamma is coded per group as v = rint(u * 32639 / max|u|) with step
+// d = max|u| / 32639, all before the workgroup's one barrier, and the row's scale
+// rsqrt(ss / 896 + eps) (ss = the waves' sums of squares of x, in order) is returned in
+// rs[j] for rows 4 kg + j of this lane: callers multiply each product of the row by it.
+// The sequence for a row does not depend on T.
 template <int T, class Src>
 __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int nrows, PrepLds<T>& P,
-                                        IllCtl* ctl, int code, const IllPassArgs& a, int trs = -1) {
+                                        IllCtl* ctl, int code, const IllPassArgs& a, float rs[4], int trs = -1) {
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int G1 = w + ILL_WAVES;
   const bool two = G1 < 14;   // wave-uniform
@@ -319,11 +320,11 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
       if (two) quant_store<T>(q1[r], t, P.ahi + G1 * 4 * T, P.alo + G1 * 4 * T, lane);
       if (lane == 0) {
         P.red[w][t] = ss[r];
-        P.gm[w][t] = m0[r];
-        P.gq[w][t] = s0[r];
+        const float d0 = m0[r] * (1.0f / ILL_QMAX);
+        P.sc[w * T + t] = make_float2(d0, d0 * (float)s0[r]);
         if (two) {
-          P.gm[G1][t] = m1[r];
-          P.gq[G1][t] = s1[r];
+          const float d1 = m1[r] * (1.0f / ILL_QMAX);
+          P.sc[G1 * T + t] = make_float2(d1, d1 * (float)s1[r]);
         }
       }
     }
@@ -332,19 +333,20 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   if (trs >= 0 && (trs + 1) % ILL_TRL != 0) trace_mark(a, trs + 1);
   lds_barrier();
   const int4 ok0 = *(const int4*)&P.ok[0], ok1 = *(const int4*)&P.ok[4];
-  if ((ok0.x & ok0.y & ok0.z & ok0.w & ok1.x & ok1.y & ok1.z & ok1.w) == 0) return false;
-  // group steps (d, d * sum v) of every (group, row), written by every wave (the same values)
-  for (int i = lane; i < 14 * T; i += 64) {
-    const int G = i / T, t = i - G * T;
+  // the row scales of this lane's rows 4 kg + j (at T = 1 every lane's row 0)
+  const int kg = lane >> 4;
+  constexpr int RPL = T >= 4 ? 4 : T;
+#pragma unroll
+  for (int j = 0; j < 4; j++) rs[j] = 1.f;
+#pragma unroll
+  for (int j = 0; j < RPL; j++) {
+    const int t = arow<T>(4 * kg + j);
     float sst = 0.f;
 #pragma unroll
     for (int ww = 0; ww < ILL_WAVES; ww++) sst += P.red[ww][t];
-    const float scale = __builtin_amdgcn_rsqf(sst * (1.0f / (float)ILL_H) + ILL_EPS);
-    const float d = P.gm[G][t] * scale * (1.0f / ILL_QMAX);
-    P.sc[G * T + t] = make_float2(d, d * (float)P.gq[G][t]);
+    rs[j] = __builtin_amdgcn_rsqf(sst * (1.0f / (float)ILL_H) + ILL_EPS);
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's own writes, read below
-  return true;
+  return (ok0.x & ok0.y & ok0.z & ok0.w & ok1.x & ok1.y & ok1.z & ok1.w) != 0;
 }
 
 // ---- weight staging in LDS ----------------------------------------------------------------
@@ -847,8 +849,9 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   }
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
-  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a);
-  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, ILL_TRL * l + 15);
+  float rs[4];   // RMSNorm scale of this lane's rows
+  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs);
+  else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
   // ---- q_h, k_g, v_g rows (the wave's row tiles, see qkv_nt)
@@ -877,7 +880,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     const int dim = d + 32 * hf1;
     const bool writer = (h % 7) == 0;
     if (kg == 0) {
-      const uint32_t h0 = f2h(acc0[0] + bias0);
+      const uint32_t h0 = f2h(acc0[0] * rs[0] + bias0);
       A.v[0][dim] = (uint16_t)h0;
       if (writer) {
         uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + pos / 64) * 64 * 64;
@@ -892,7 +895,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
       if (t >= nrows) continue;
-      float x0 = acc0[j] + bias0, x1 = acc1[j] + bias1;
+      float x0 = acc0[j] * rs[j] + bias0, x1 = acc1[j] * rs[j] + bias1;
       if (head < ILL_NH + ILL_NKV) {
         const float2 cs = rope[j];
         const float r0 = x0 * cs.x - x1 * cs.y;
@@ -1110,7 +1113,8 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   const IllLayerW& L = a.L[l];
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
-  if (!prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, ILL_TRL * l + 6)) return false;
+  float rs[4];   // RMSNorm scale of this lane's rows
+  if (!prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6)) return false;
   trace_mark(a, ILL_TRL * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1122,7 +1126,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
-      if (t < T) G.gu[w][t][n] = acc[j];
+      if (t < T) G.gu[w][t][n] = acc[j] * rs[j];
     }
   }
   lds_barrier();
@@ -1232,7 +1236,8 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     int tile = wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
-    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a)) return false;
+    float rs[4];   // final-norm scale of this lane's rows
+    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a, rs)) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {
@@ -1242,6 +1247,8 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
       q4_tile896<T>(cur, Lm.prep, lane, acc);
       const int idx = 16 * tile + n;
+#pragma unroll
+      for (int j = 0; j < RPL; j++) acc[j] *= rs[j];
 #pragma unroll
       for (int j = 0; j < RPL; j++) {
         const int t = 4 * kg + j;

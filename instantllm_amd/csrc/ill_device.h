@@ -183,7 +183,7 @@ template <int N> __device__ __forceinline__ float gmaxabs(float v) {
 
 // Order-preserving 64-bit key of (value, index): larger value first, then lower index.
 __device__ __forceinline__ uint64_t amax_key(float v, int idx) {
-  const uint32_t b = __float_as_uint(v);
+  const uint32_t b = __float_as_uint(v + 0.0f);   // -0 orders as +0
   const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)ord << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
 }

@@ -67,6 +67,7 @@ __device__ __forceinline__ void trace_mark(const IllPassArgs& a, int slot) {
 struct PassHdr {
   uint32_t epoch;
   int mode, nrows, pos, lmh0, lmhn, wlog, commit, done, bank, zrows;
+  int step, maxsteps, eos0, eos1, passes, accepted;   // State as the pass found it
   int tok[16], depth[16], parent[16];
   int prow[16][16];        // prow[t][d]: pass row on row t's path at depth d
 };
@@ -89,6 +90,12 @@ __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
   const IllState* st = a.st;
   const IllCtl* c = a.ctl;
   H.done = st->done;
+  H.step = st->step;
+  H.maxsteps = st->maxsteps;
+  H.eos0 = st->eos0;
+  H.eos1 = st->eos1;
+  H.passes = st->passes;
+  H.accepted = st->accepted;
   H.epoch = c->epoch;
   H.bank = c->epoch & 1;
   H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
@@ -416,8 +423,7 @@ struct LmhLds {
 };
 
 struct CommitLds {
-  float v[256];
-  int i[256];
+  uint64_t key[ILL_WG / 64];
   int g[16];
   int path[16];
   int npath, pos0;
@@ -1326,23 +1332,23 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
   }, a.ctl, 700);
   if (!ok) return;
   trace_mark(a, ILL_TR_TAIL + 4);
+  // global argmax per row: order-preserving keys (value, lowest index), reduced in each of
+  // the 4 waves that hold a partial, then across them
+  const int lane = i & 63, wv = i >> 6;
   for (int t = H.lmh0; t < H.lmh0 + H.lmhn; t++) {
-    if (i < ILL_WG) {
-      C.v[i] = wval(aload64(a.lmp + (i * 16 + t) * 2));
-      C.i[i] = (int)(uint32_t)aload64(a.lmp + (i * 16 + t) * 2 + 1);
+    uint64_t k = 0;
+    if (i < ILL_WG) k = amax_key(wval(aload64(a.lmp + (i * 16 + t) * 2)), (int)(uint32_t)aload64(a.lmp + (i * 16 + t) * 2 + 1));
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t ok = __shfl_xor(k, o, 64);
+      k = ok > k ? ok : k;
     }
+    if (lane == 0 && wv < ILL_WG / 64) C.key[wv] = k;
     __syncthreads();
-    for (int s = ILL_WG / 2; s >= 1; s >>= 1) {
-      if (i < s) {
-        float v = C.v[i];
-        int id = C.i[i];
-        amax_merge(v, id, C.v[i + s], C.i[i + s]);
-        C.v[i] = v;
-        C.i[i] = id;
-      }
-      __syncthreads();
+    if (i == 0) {
+      uint64_t m = C.key[0];
+      for (int ww = 1; ww < ILL_WG / 64; ww++) m = C.key[ww] > m ? C.key[ww] : m;
+      C.g[t] = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFu));
     }
-    if (i == 0) C.g[t] = C.i[0];
     __syncthreads();
   }
   commit_apply(a, H, C, true);
@@ -1350,24 +1356,26 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
 
 // Commit of the pass's argmaxes C.g[t] (rows lmh0 ..): token record, State advance, stop
 // test, chain / tree accept walk and KV compaction (Shaders.swift:192-244, :246-418). The
-// pass kernel also advances the epoch and its accumulator-bank bookkeeping.
+// pass kernel also advances the epoch and its accumulator-bank bookkeeping. The State is
+// read from the header (the snapshot taken at the start of the pass: only the commit
+// writes it during a pass), so the commit issues stores only.
 __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel) {
   const int i = tid_opaque();
   IllState* st = a.st;
   if (i == 0) {
     C.npath = 0;
-    C.pos0 = st->pos;
+    C.pos0 = H.pos;
     if (H.commit == 0) {
-      st->pos += H.nrows;
+      st->pos = H.pos + H.nrows;
     } else if (H.commit == 1) {
       const int tok = C.g[H.lmh0];
-      const int step = st->step;
+      const int step = H.step;
       a.out_dev[step] = tok;
       __hip_atomic_store(a.out_host + step, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       st->step = step + 1;
-      st->pos += H.nrows;
+      st->pos = H.pos + H.nrows;
       st->n = 1;
-      if (tok == st->eos0 || tok == st->eos1 || step + 1 >= st->maxsteps) st->done = 1;
+      if (tok == H.eos0 || tok == H.eos1 || step + 1 >= H.maxsteps) st->done = 1;
       a.ptoks[0] = tok;
       a.ctl->last_tok = tok;
     } else {
@@ -1389,20 +1397,21 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
         while (m < nv - 1 && H.tok[m + 1] == C.g[m]) m++;
         for (int k = 0; k < m; k++) C.path[k] = k + 1;
       }
-      st->passes += 1;
-      st->accepted += m;
+      st->passes = H.passes + 1;
+      st->accepted = H.accepted + m;
       bool stop = false;
       int last = C.g[0];
+      int step = H.step;
       for (int k = 0; k <= m && !stop; k++) {
         const int tok = C.g[k == 0 ? 0 : C.path[k - 1]];
-        const int step = st->step;
         a.out_dev[step] = tok;
         __hip_atomic_store(a.out_host + step, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        st->step = step + 1;
         last = tok;
-        if (tok == st->eos0 || tok == st->eos1 || step + 1 >= st->maxsteps) stop = true;
+        if (tok == H.eos0 || tok == H.eos1 || step + 1 >= H.maxsteps) stop = true;
+        step++;
       }
-      st->pos += m + 1;
+      st->step = step;
+      st->pos = H.pos + m + 1;
       st->n = 1;
       st->nver = 1;
       st->tree = 0;

@@ -192,6 +192,10 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 __device__ __forceinline__ uint32_t f2h(float v) { return (uint32_t)__half_as_ushort(__float2half_rn(v)); }
+// f16 with saturation to the finite range (NaN to the largest finite value): what the V
+// cache stores, so that every V slot holds a finite value and a zero probability times an
+// unused slot is zero
+__device__ __forceinline__ uint32_t f2h_sat(float v) { return f2h(__builtin_amdgcn_fmed3f(v, -65504.0f, 65504.0f)); }
 
 // ---- activation quantization ------------------------------------------------------------
 // A row of activations is coded per 64-column group as 16-bit fixed point

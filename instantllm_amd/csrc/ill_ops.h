@@ -236,8 +236,8 @@ __device__ __forceinline__ void epi_qkv(const OpCtx& c, int layer, int m, int b,
     kr[d + 32] = (uint16_t)f2h(x1);
   } else {
     uint16_t* vb = c.vt + (((size_t)layer * ILL_NKV + (head - ILL_NH - ILL_NKV)) * (c.maxctx / 64) + slot / 64) * 4096;
-    vb[d * 64 + (slot & 63)] = (uint16_t)f2h(x0);
-    vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)f2h(x1);
+    vb[d * 64 + (slot & 63)] = (uint16_t)f2h_sat(x0);
+    vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)f2h_sat(x1);
   }
 }
 // gate/up rows in groups of 4: g[2q], g[2q+1], u[2q], u[2q+1] (Convert.swift:134-136)

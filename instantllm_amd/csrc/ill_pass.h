@@ -562,8 +562,9 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
 #pragma unroll
     for (int b = 0; b < 4; b++) rk[b] = min(H.prow[t1][min(max(64 * c + 16 * b + n - pos, 0), 15)], T - 1);
   }
-  // T = 1: the key at pos is the pass row's (from LDS); keys above pos are masked through
-  // their scores, so their cache contents are never used
+  // T = 1: the key at pos is the pass row's (from LDS; only block (pos - 64 c) / 16 holds
+  // it); keys above pos are masked through their scores, so their cache contents are never
+  // used
   uint4 kp0 = zz, kp1 = zz;
   if (T == 1 && part) {
     kp0 = *(const uint4*)&A.k[0][8 * kg];
@@ -575,9 +576,11 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
     const int vp = 64 * c + 16 * b + n;
     uint4 k0 = f.k[b][0], k1 = f.k[b][1];
     if (T == 1 && part) {
-      const uint32_t mp = mask_of(vp == pos);
-      k0 = msel4(mp, kp0, k0);
-      k1 = msel4(mp, kp1, k1);
+      if (b == ((pos - 64 * c) >> 4)) {   // wave-uniform
+        const uint32_t mp = mask_of(vp == pos);
+        k0 = msel4(mp, kp0, k0);
+        k1 = msel4(mp, kp1, k1);
+      }
     } else if (part) {
       const uint4 l0 = *(const uint4*)&A.k[rk[b]][8 * kg];
       const uint4 l1 = *(const uint4*)&A.k[rk[b]][32 + 8 * kg];
@@ -633,19 +636,11 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
     }
   }
   wave_lds_sync();
-  // T = 1: V at positions below pos from the cache, at pos the pass row's, above pos zero.
-  // This lane's 8 positions 32 ks + 8 kg + i of the chunk keep the first nk cache values;
-  // the one 32-bit word holding pos (wave-uniform ks, word and half) takes the pass row.
+  // T = 1: V at positions below pos from the cache, at pos the pass row's; positions above
+  // pos keep their (finite: the cache stores saturated f16) cache values, which meet
+  // probabilities of exactly 0. The one 32-bit word holding pos (wave-uniform ks, word and
+  // half, lanes kg = (dp / 8) % 4) takes the pass row.
   const int dp = pos - 64 * c;
-  uint32_t km[2][4];
-  if (T == 1 && part) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const int nk = min(max(dp - 32 * ks - 8 * kg, 0), 8);
-#pragma unroll
-      for (int wi = 0; wi < 4; wi++) km[ks][wi] = nk >= 2 * wi + 2 ? 0xffffffffu : (nk == 2 * wi + 1 ? 0xffffu : 0u);
-    }
-  }
   uint32_t lv1[4] = {0u, 0u, 0u, 0u};   // T = 1: the pass row's V, read by every lane
   if (T == 1 && part) {
 #pragma unroll
@@ -655,15 +650,16 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
   for (int nb = 0; nb < 4; nb++) {
     const int dim = 16 * nb + n;
     v8h vv[2];
-    const uint32_t lvs = msel(mask_of(kg == ((dp >> 3) & 3)), lv1[nb] << (16 * (dp & 1)), 0u);
+    const uint32_t hm = mask_of(kg == ((dp >> 3) & 3)) & (0xffffu << (16 * (dp & 1)));   // bits of pos
+    const uint32_t lvs = lv1[nb] << (16 * (dp & 1));
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       uint4 u = f.v[nb][ks];
       if (T == 1 && part) {
-        uint32_t x[4] = {u.x & km[ks][0], u.y & km[ks][1], u.z & km[ks][2], u.w & km[ks][3]};
+        uint32_t x[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int wi = 0; wi < 4; wi++)
-          if (ks == (dp >> 5) && wi == ((dp >> 1) & 3)) x[wi] |= lvs;
+          if (ks == (dp >> 5) && wi == ((dp >> 1) & 3)) x[wi] = msel(hm, lvs, x[wi]);
         u = make_uint4(x[0], x[1], x[2], x[3]);
       } else if (part) {
         // positions >= pos: row t1's path table (zero beyond its depth); positions >= pos + 16 hold no key
@@ -684,8 +680,8 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], acc, 0, 0, 0);
-    // T = 1: positions 32 .. 63 of the chunk all above pos hold p = 0 and v = 0 (skipped;
-    // adding them would add zeros)
+    // T = 1: positions 32 .. 63 of the chunk all above pos hold p = 0 and finite v
+    // (skipped; adding them would add zeros)
     if (!(T == 1 && part && dp < 32)) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], acc, 0, 0, 0);
@@ -886,7 +882,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     const int dim = d + 32 * hf1;
     const bool writer = (h % 7) == 0;
     if (kg == 0) {
-      const uint32_t h0 = f2h(acc0[0] * rs[0] + bias0);
+      const uint32_t h0 = f2h_sat(acc0[0] * rs[0] + bias0);
       A.v[0][dim] = (uint16_t)h0;
       if (writer) {
         uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + pos / 64) * 64 * 64;
@@ -923,7 +919,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
           gst(kr + d + 32, (uint16_t)h1);
         }
       } else {
-        const uint32_t h0 = f2h(x0), h1 = f2h(x1);
+        const uint32_t h0 = f2h_sat(x0), h1 = f2h_sat(x1);
         A.v[t][d] = (uint16_t)h0;
         A.v[t][d + 32] = (uint16_t)h1;
         if (writer) {

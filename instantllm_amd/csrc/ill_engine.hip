@@ -111,7 +111,7 @@ struct ill_engine {
   float2* rope = nullptr;
   uint16_t* kc = nullptr;
   uint16_t* vt = nullptr;
-  uint64_t *acc = nullptr, *lmp = nullptr;
+  uint64_t *acc = nullptr, *lmp = nullptr, *pub = nullptr;
   size_t acc_bytes = 0;
   float* logits = nullptr;
   int32_t* out_dev = nullptr;
@@ -498,7 +498,8 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
             dalloc((void**)&e->ptoks, ILL_OP_MAXM * 4) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
             dalloc((void**)&e->acc, e->acc_bytes) &&
-            dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
+            dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->pub, (size_t)ILL_PUB_WORDS * 8) &&
+            dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
             dalloc((void**)&e->out_dev, (size_t)max_steps * 4);
   ok = ok && dalloc((void**)&e->dolayers, sizeof(OpLayerW) * layers) && dalloc((void**)&e->octx.x, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
        dalloc((void**)&e->octx.xn, (size_t)ILL_OP_MAXM * ILL_H * 2) && dalloc((void**)&e->octx.q, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
@@ -550,6 +551,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.vt = e->vt;
   a.acc = e->acc;
   a.lmp = e->lmp;
+  a.pub = e->pub;
   a.logits = e->logits;
   a.out_dev = e->out_dev;
   a.out_host = e->out_host;
@@ -579,7 +581,7 @@ int ill_destroy(ill_engine* e) {
   if (e->gexec) hipGraphExecDestroy(e->gexec);
   if (e->graph) hipGraphDestroy(e->graph);
   void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
-                  e->lmp, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
+                  e->lmp, e->pub, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
                   e->octx.q, e->octx.ao, e->octx.h, e->octx.amax, e->opart};
   for (void* p : bufs)
     if (p) hipFree(p);

@@ -34,6 +34,7 @@
 #define ILL_R_ATT0 0         // ATT WGs 0..13
 #define ILL_R_BASE 14        // the residual-copy workgroup
 #define ILL_R_GUD0 16        // GUD WGs 16..91
+#define ILL_R_PREP0 92       // 16-row passes: PREP WGs 92..107 (one per row)
 
 struct IllPassArgs {
   IllWeights W;
@@ -51,6 +52,7 @@ struct IllPassArgs {
   int32_t* out_dev;        // [maxsteps]
   int32_t* out_host;       // [maxsteps] pinned host memory
   uint64_t* trace;         // optional [256][ILL_TRACE_SLOTS] timestamps (nullptr = off)
+  uint64_t* pub;           // 16-row passes: published row codings [2][ILL_MAXLAYERS + 1][16][ILL_PUB_W]
   int maxctx;
   int maxsteps;
 };
@@ -356,6 +358,87 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   return (ok0.x & ok0.y & ok0.z & ok0.w & ok1.x & ok1.y & ok1.z & ok1.w) != 0;
 }
 
+// ---- published codings (16-row passes) ----------------------------------------------------
+// Every consumer of an accumulator needs all of its rows coded. In a 16-row pass that is
+// 16 x 896 fixed-point words (114 KB) per consumer workgroup, read by 14 ATT, 76 GUD and
+// 256 lm_head workgroups, each then running the same RMSNorm coding over 16 rows. Instead,
+// one PREP workgroup per row runs prep896 on its row once (the arithmetic of a 1-row pass,
+// so codes, group scales and row scale are bit-identical to it) and publishes the result
+// as ILL_PUB_PAY tagged words (payload | tag << 32, tag = epoch * 32 + slot + 1):
+//   [0, 224)    A-operand high bytes, 56 uint4 (column group g, k-group gi at 4 g + gi)
+//   [224, 448)  low bytes
+//   [448, 476)  group scales, 14 float2 (d, d * sum of the codes)
+//   476         the row scale rsqrt(ss / 896 + eps)
+// Consumers read the published rows (61 KB for 16 rows) straight into PrepLds<16>.
+// Buffers: kind 0 holds the GUD inputs (slot l: XA[l] under ln2), kind 1 the ATT inputs
+// (slot l: x_l under ln1) and the final norm (slot = layers).
+#define ILL_PUB_W 480
+#define ILL_PUB_PAY 477
+#define ILL_PUB_WORDS (2 * (ILL_MAXLAYERS + 1) * ILL_MAXT * ILL_PUB_W)
+__device__ __forceinline__ uint32_t tagof_pub(uint32_t epoch, int slot) { return epoch * 32u + (uint32_t)slot + 1u; }
+__device__ __forceinline__ uint64_t* pub_ptr(const IllPassArgs& a, int kind, int slot, int t) {
+  return a.pub + (((size_t)kind * (ILL_MAXLAYERS + 1) + slot) * ILL_MAXT + t) * ILL_PUB_W;
+}
+
+// Publish a 1-row coding (PrepLds<1> as prep896<1> left it, rs = its row scale).
+__device__ __forceinline__ void pub_write(const PrepLds<1>& P, float rs, uint64_t* dst, uint32_t tag) {
+  const int k = tid_opaque();
+  if (k < ILL_PUB_PAY) {
+    uint32_t v;
+    if (k < 224) v = ((const uint32_t*)P.ahi)[k];
+    else if (k < 448) v = ((const uint32_t*)P.alo)[k - 224];
+    else if (k < 476) v = ((const uint32_t*)P.sc)[k - 448];
+    else v = __float_as_uint(rs);
+    astore64(dst + k, mkwu(v, tag));
+  }
+}
+
+// The consumer side: rows 0 .. nrows - 1 of a published coding (src = row 0) into P, as
+// prep896<T> would have left it (rows >= nrows coded as zeros), and the row scales of this
+// lane's rows 4 kg + j in rs[j]. Every wave waits for its own words.
+template <int T>
+__device__ __forceinline__ bool pub_read(const uint64_t* src, uint32_t tag, int nrows, PrepLds<T>& P, IllCtl* ctl,
+                                         int code, const IllPassArgs& a, float rs[4], int trs = -1) {
+  static_assert(T == ILL_MAXT, "published codings are read by 16-row passes");
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  constexpr int NI = (T * ILL_PUB_W + ILL_WG_THREADS - 1) / ILL_WG_THREADS;
+  uint32_t v[NI];
+  const bool alive = wave_wait([&]() {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int f = tid + ILL_WG_THREADS * i;
+      const int t = f / ILL_PUB_W, k = f % ILL_PUB_W;
+      v[i] = 0u;
+      if (t < nrows && k < ILL_PUB_PAY) {
+        const uint64_t x = aload64(src + f);
+        ok &= (uint32_t)(x >> 32) == tag;
+        v[i] = (uint32_t)x;
+      }
+    }
+    return ok;
+  }, ctl, code);
+  if (trs >= 0) trace_mark(a, trs);
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int f = tid + ILL_WG_THREADS * i;
+    const int t = f / ILL_PUB_W, k = f % ILL_PUB_W;
+    if (t < T && k < ILL_PUB_PAY) {
+      if (k < 224) ((uint32_t*)P.ahi)[((k >> 2) * T + t) * 4 + (k & 3)] = v[i];
+      else if (k < 448) ((uint32_t*)P.alo)[(((k - 224) >> 2) * T + t) * 4 + (k & 3)] = v[i];
+      else if (k < 476) ((uint32_t*)P.sc)[(((k - 448) >> 1) * T + t) * 2 + (k & 1)] = v[i];
+      else P.red[0][t] = t < nrows ? __uint_as_float(v[i]) : 1.f;
+    }
+  }
+  if (lane == 0) P.ok[w] = alive;
+  lds_barrier();
+  const int4 ok0 = *(const int4*)&P.ok[0], ok1 = *(const int4*)&P.ok[4];
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; j++) rs[j] = P.red[0][arow<T>(4 * kg + j)];
+  return (ok0.x & ok0.y & ok0.z & ok0.w & ok1.x & ok1.y & ok1.z & ok1.w) != 0;
+}
+
 // ---- weight staging in LDS ----------------------------------------------------------------
 // Each role copies the next layer's weights HBM -> LDS (global_load_lds) as soon as it has
 // finished the current layer, per wave, into a dynamic-LDS stage of ILL_STAGE_BYTES:
@@ -434,6 +517,7 @@ union PassLds {
   AttLds<T> att;
   GudLds<T> gud;
   LmhLds<T> lmh;
+  PrepLds<1> prep1;
   CommitLds cm;
 };
 
@@ -852,7 +936,8 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   float rs[4];   // RMSNorm scale of this lane's rows
-  if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs);
+  if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 1, l, 0), tagof_pub(H.epoch, l), nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
+  else if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs);
   else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
@@ -1116,7 +1201,10 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
   float rs[4];   // RMSNorm scale of this lane's rows
-  if (!prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6)) return false;
+  bool ok;
+  if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 0, l, 0), tagof_pub(H.epoch, l), nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6);
+  else ok = prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6);
+  if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
   {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1218,6 +1306,31 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
 }
 
 // ---------------------------------------------------------------------------------------
+// PREP (16-row passes, one workgroup per row t < nrows): the published codings of row t,
+// layer by layer, in the order the pass needs them: the ATT input x_l (the embedding at
+// layer 0, else the completed XB[l-1]) under ln1, then the GUD input XA[l] under ln2, and
+// after the last layer the final-norm input of the lm_head.
+template <int T>
+__device__ __forceinline__ bool role_prep(const IllPassArgs& a, const PassHdr& H, PrepLds<1>& P, int t) {
+  const int NL = a.W.layers;
+  float rs[4];
+  for (int l = 0; l <= NL; l++) {
+    const float* gam = l < NL ? a.L[l].ln1 : a.W.fnorm;
+    bool ok;
+    if (l == 0) ok = prep896<1>(SrcEmbed{a.W, H.tok + t}, gam, 1, P, a.ctl, 700, a, rs);
+    else ok = prep896<1>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, t)}, gam, 1, P, a.ctl, 700 + l, a, rs);
+    if (!ok) return false;
+    pub_write(P, rs[0], pub_ptr(a, 1, l, t), tagof_pub(H.epoch, l));
+    lds_barrier();   // the coding is read out before the next one is written
+    if (l == NL) break;
+    if (!prep896<1>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, t)}, a.L[l].ln2, 1, P, a.ctl, 750 + l, a, rs)) return false;
+    pub_write(P, rs[0], pub_ptr(a, 0, l, t), tagof_pub(H.epoch, l));
+    lds_barrier();
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void amax_merge(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
@@ -1239,7 +1352,10 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
     float rs[4];   // final-norm scale of this lane's rows
-    if (!prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a, rs)) return false;
+    bool ok;
+    if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 1, NL, 0), tagof_pub(H.epoch, NL), H.nrows, Lm.prep, a.ctl, 600, a, rs);
+    else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a, rs);
+    if (!ok) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
     while (tile < ntiles) {
@@ -1485,6 +1601,12 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       trace_mark(a, ILL_TRL * l);
       if (!role_base<T>(a, H, l)) return;
       trace_mark(a, ILL_TRL * l + 11);
+    }
+  } else if (T > 1 && wg >= ILL_R_PREP0 && wg < ILL_R_PREP0 + ILL_MAXT) {
+    const int t = wg - ILL_R_PREP0;
+    if (t < H.nrows) {
+      if (!role_prep<T>(a, H, S.prep1, t)) return;
+      lds_barrier();
     }
   }
   trace_mark(a, ILL_TR_TAIL);

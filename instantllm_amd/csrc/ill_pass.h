@@ -627,10 +627,11 @@ __device__ __forceinline__ void kv_fetch(const uint16_t* kbase, const uint16_t* 
   }
 }
 
-// Chunk-local attention over positions 64c .. 64c+63. With `part`, keys at positions
-// >= pos come from the pass rows on row t1's path and keys at positions >= L(t1) are
+// Chunk-local attention over positions 64c .. 64c+63. With `part` (1-row passes: the chunk
+// holding pos), the key and value at pos are the pass row's and keys above pos are
 // masked; without it every key is a valid cache key. Results for rows 4 kg + j of this
 // lane: mx = max score, ls = sum exp(s - mx), o[nb] = sum exp(s - mx) v (dims 16 nb + n).
+// (16-row passes evaluate their partial chunks with part_eval16.)
 template <int T>
 __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const uint8_t* stage, const KVFrag& f, int c, bool part,
                                            int t1, const v8h qa[2][2], float mx[4], float ls[4], float o[4][4]) {
@@ -640,12 +641,6 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
   const int Lt = part ? pos + H.depth[t1] + 1 : 0x7fffffff;
   const uint4 zz = make_uint4(0, 0, 0, 0);
   float* pb = att_pbuf<T>(A, w);
-  // pass rows on row t1's path for this lane's key positions
-  int rk[4] = {0, 0, 0, 0};   // at T = 1 the only pass row is row 0 at position pos
-  if (T > 1 && part) {
-#pragma unroll
-    for (int b = 0; b < 4; b++) rk[b] = min(H.prow[t1][min(max(64 * c + 16 * b + n - pos, 0), 15)], T - 1);
-  }
   // T = 1: the key at pos is the pass row's (from LDS; only block (pos - 64 c) / 16 holds
   // it); keys above pos are masked through their scores, so their cache contents are never
   // used
@@ -665,12 +660,6 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
         k0 = msel4(mp, kp0, k0);
         k1 = msel4(mp, kp1, k1);
       }
-    } else if (part) {
-      const uint4 l0 = *(const uint4*)&A.k[rk[b]][8 * kg];
-      const uint4 l1 = *(const uint4*)&A.k[rk[b]][32 + 8 * kg];
-      const uint32_t mc = mask_of(vp < pos), ml = mask_of(vp >= pos && vp < Lt);
-      k0 = msel4(mc, k0, msel4(ml, l0, zz));
-      k1 = msel4(mc, k1, msel4(ml, l1, zz));
     }
     v4f s = {0.f, 0.f, 0.f, 0.f};
     // T = 1: a key block wholly above pos is all masked; its MFMAs are skipped (wave-uniform)
@@ -745,19 +734,6 @@ __device__ __forceinline__ void chunk_eval(const PassHdr& H, AttLds<T>& A, const
         for (int wi = 0; wi < 4; wi++)
           if (ks == (dp >> 5) && wi == ((dp >> 1) & 3)) x[wi] = msel(hm, lvs, x[wi]);
         u = make_uint4(x[0], x[1], x[2], x[3]);
-      } else if (part) {
-        // positions >= pos: row t1's path table (zero beyond its depth); positions >= pos + 16 hold no key
-        const uint16_t* vpt = (const uint16_t*)(stage + ILL_ST_VPT) + ((size_t)t1 * 64 + dim) * 16;
-        uint32_t e[8];
-        const uint32_t x[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const int d = 64 * c + 32 * ks + 8 * kg + i - pos;
-          const uint32_t lv = vpt[min(max(d, 0), 15)];
-          const uint32_t cv = (x[i >> 1] >> (16 * (i & 1))) & 0xffff;
-          e[i] = msel(mask_of(d < 0), cv, lv & mask_of(d < 16));
-        }
-        u = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
       }
       vv[ks] = u4_to_v8h(u);
     }
@@ -875,8 +851,143 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
   }
 }
 
+// 16-row passes: the partial chunk c (the chunk holding pos, or the one after it) for
+// every row at once. Keys and values at positions >= pos are the pass rows on each row's
+// path. Scores: the blocks holding cached keys from the cache (all rows), the pass
+// positions from one 16 x 16 block SP[t][j] = q_t . k_j over the pass rows j, gathered along
+// each row's path. Every score is the MFMA product of the same operands as in a 1-row pass
+// at that row's position, and the softmax runs in the same lane layout, so a row's maximum
+// and sum match that pass bit for bit. The value operand differs per row, so each row's
+// P x V runs on its own operand (the cached values below pos, the table of path values vq
+// above it), with the 1-row pass's instruction sequence. Wave w finishes rows w and w + 8:
+// their statistics and outputs go to A.pm / A.pl / A.po[c - ns].
+// vq (stage + ILL_ST_VPT): [row t][dim][24] f16, the values at positions 8 (pos / 8) + q,
+// q < 24 (a range holding pos .. pos + 15): path row values at depths 0 .. depth(t), else 0.
+template <int T>
+__device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, const uint8_t* stage, const KVFrag& f, int c,
+                                            bool cache, const v8h qa[2][2]) {
+  const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int pos = H.pos, nrows = H.nrows, ns = pos >> 6;
+  const uint4 zz = make_uint4(0, 0, 0, 0);
+  float* pb = att_pbuf<T>(A, w);
+  // SP: lane (kg, n) holds q_t . k_n for rows t = 4 kg + j
+  v4f sp = {0.f, 0.f, 0.f, 0.f};
+  {
+    const v8h k0 = u4_to_v8h(*(const uint4*)&A.k[n][8 * kg]), k1 = u4_to_v8h(*(const uint4*)&A.k[n][32 + 8 * kg]);
+    sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], k0, sp, 0, 0, 0);
+    sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], k0, sp, 0, 0, 0);
+    sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], k1, sp, 0, 0, 0);
+    sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], k1, sp, 0, 0, 0);
+  }
+  int Lr[4];   // L(t) of this lane's rows (0: no row)
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int t = 4 * kg + j;
+    Lr[j] = t < nrows ? pos + H.depth[t] + 1 : 0;
+  }
+  float sc[4][4];
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const int vp = 64 * c + 16 * b + n;
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+    if (cache && 64 * c + 16 * b < pos) {   // wave-uniform: the block holds cached keys
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], u4_to_v8h(f.k[b][0]), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], u4_to_v8h(f.k[b][0]), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], u4_to_v8h(f.k[b][1]), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(f.k[b][1]), s, 0, 0, 0);
+    }
+    const int dd = min(max(vp - pos, 0), 15);   // depth of a pass position
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int src = (lane & 48) | H.prow[4 * kg + j][dd];
+      const float g = __shfl(sp[j], src, 64);
+      sc[b][j] = vp < pos ? s[j] : (vp < Lr[j] ? g : -INFINITY);
+    }
+  }
+  float mx[4], ls[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float m = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
+    mx[j] = gmax<16>(m);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      sc[b][j] = att_exp(sc[b][j] - mx[j]);
+      sum += sc[b][j];
+    }
+    ls[j] = gsum<16>(sum);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+#pragma unroll
+    for (int b = 0; b < 4; b++) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
+  }
+  wave_lds_sync();
+  v8h ph[2], pl[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float p = pb[n * 64 + 32 * ks + 8 * kg + i];
+      const _Float16 hi = (_Float16)p;
+      ph[ks][i] = hi;
+      pl[ks][i] = (_Float16)(p - (float)hi);
+    }
+  }
+  wave_lds_sync();
+  const uint4* vq = (const uint4*)(stage + ILL_ST_VPT);
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int t = w + ILL_WAVES * r;
+    if (t >= nrows) continue;
+    const int Lt = pos + H.depth[t] + 1;
+    if (Lt <= 64 * c) continue;   // wave-uniform: no position of the chunk is on the row's path
+    const int j = t & 3;
+    if (kg == (t >> 2) && n == 0) {
+      A.pm[c - ns][t] = j == 0 ? mx[0] : j == 1 ? mx[1] : j == 2 ? mx[2] : mx[3];
+      A.pl[c - ns][t] = j == 0 ? ls[0] : j == 1 ? ls[1] : j == 2 ? ls[2] : ls[3];
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+      const int dim = 16 * nb + n;
+      v8h vv[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        const int p0 = 64 * c + 32 * ks + 8 * kg;   // this lane's first position
+        const int sl = (p0 >> 3) - (pos >> 3);      // its 8-group in vq
+        uint4 u = cache ? f.v[nb][ks] : zz;
+        if (sl >= 0 && sl < 3) {
+          // halves below pos (the first pos - p0 < 8) from the cache, the rest from vq
+          const uint4 x = vq[((size_t)t * 64 + dim) * 3 + sl];
+          const int nc = pos - p0;
+          auto mg = [&](uint32_t uc, uint32_t xt, int k) {
+            return 2 * k + 1 < nc ? uc : (2 * k >= nc ? xt : ((uc & 0xffffu) | (xt & 0xffff0000u)));
+          };
+          u = make_uint4(mg(u.x, x.x, 0), mg(u.y, x.y, 1), mg(u.z, x.z, 2), mg(u.w, x.w, 3));
+        }
+        vv[ks] = u4_to_v8h(u);
+      }
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], vv[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], vv[0], acc, 0, 0, 0);
+      // positions 32 .. 63 all beyond the row's path hold p = 0: skipped, as the 1-row pass does
+      if (64 * c + 32 < Lt) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], vv[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], vv[1], acc, 0, 0, 0);
+      }
+      if (kg == (t >> 2)) A.po[c - ns][t][dim] = j == 0 ? acc[0] : j == 1 ? acc[1] : j == 2 ? acc[2] : acc[3];
+    }
+  }
+}
+
 // Chunk of the partial (chunk, row) pair number `idx` (pairs run over chunks c >= ns, then
-// rows t with L(t) > 64 c), or -1.
+// rows t with L(t) > 64 c), or -1. (At T = 1 there is one pair: chunk ns, row 0. This form,
+// rather than the equivalent sj == ns test, measured 1.5% faster per step: it changes how
+// the compiler schedules the first fetch.)
 __device__ __forceinline__ int att_pair_chunk(const PassHdr& H, int ns, int cmax, int idx) {
   int k = 0;
   for (int c = ns; c <= cmax; c++)
@@ -919,10 +1030,12 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   int maxL = 0;
   for (int t = 0; t < nrows; t++) maxL = max(maxL, pos + H.depth[t] + 1);
   const int ns = pos >> 6, cmax = (maxL - 1) >> 6;
-  const int pidx0 = (sj - ns) & 7;
   const uint16_t* kbase = a.kc + ((size_t)l * ILL_NKV + g) * a.maxctx * 64;
   const uint16_t* vbase = a.vt + ((size_t)l * ILL_NKV + g) * (a.maxctx / 64) * 64 * 64;
-  const int cfirst = sj < ns ? sj : att_pair_chunk(H, ns, cmax, pidx0);
+  // Waves without a shared chunk: at T = 1 the wave of the partial pair fetches chunk ns; in
+  // 16-row passes every wave evaluates chunk ns, which needs the cache if it holds positions
+  // below pos.
+  const int cfirst = sj < ns ? sj : (T == 1 ? att_pair_chunk(H, ns, cmax, (sj - ns) & 7) : (64 * ns < pos ? ns : -1));
   KVFrag f;
   int fc = -1;   // cache chunk held in f
   // The slot's first chunk streams in while the input is awaited: cache positions below pos
@@ -1018,16 +1131,22 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 4);
   if (T != 1) att_stage_o<T>(L, h, w, lane, stage);   // O weights stream in while attention runs
-  if (T > 1 && cmax >= ns) {   // partial chunks exist: path table of the pass rows' V
-    uint4* vpt = (uint4*)(stage + ILL_ST_VPT);
-    for (int i = tid; i < T * 64; i += ILL_WG_THREADS) {   // (row t1, dim): 16 depths
+  if (T > 1) {   // path values of the pass rows at positions 8 (pos / 8) + q, q < 24 (part_eval16)
+    uint4* vq = (uint4*)(stage + ILL_ST_VPT);
+    const int d0 = 8 * (pos >> 3) - pos;   // depth of q = 0 (-7 .. 0)
+    for (int i = tid; i < T * 64; i += ILL_WG_THREADS) {   // (row t1, dim)
       const int t1 = i >> 6, dim = i & 63;
       const int dep = t1 < nrows ? H.depth[t1] : -1;
-      uint32_t e[16];
+      uint32_t e[24];
 #pragma unroll
-      for (int dd = 0; dd < 16; dd++) e[dd] = dd <= dep ? (uint32_t)A.v[min(H.prow[t1][dd], T - 1)][dim] : 0u;
-      vpt[2 * i] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
-      vpt[2 * i + 1] = make_uint4(e[8] | (e[9] << 16), e[10] | (e[11] << 16), e[12] | (e[13] << 16), e[14] | (e[15] << 16));
+      for (int q = 0; q < 24; q++) {
+        const int dd = d0 + q;
+        e[q] = dd >= 0 && dd <= dep ? (uint32_t)A.v[min(H.prow[t1][min(dd, 15)], T - 1)][dim] : 0u;
+      }
+#pragma unroll
+      for (int s3 = 0; s3 < 3; s3++)
+        vq[i * 3 + s3] = make_uint4(e[8 * s3] | (e[8 * s3 + 1] << 16), e[8 * s3 + 2] | (e[8 * s3 + 3] << 16),
+                                    e[8 * s3 + 4] | (e[8 * s3 + 5] << 16), e[8 * s3 + 6] | (e[8 * s3 + 7] << 16));
     }
     lds_barrier();
   }
@@ -1084,30 +1203,13 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       fold(mx, ls, o);
     }
   } else {
-    int idx = 0;
     for (int c = ns; c <= cmax; c++) {
-      for (int t1 = 0; t1 < nrows; t1++) {
-        if (pos + H.depth[t1] + 1 <= 64 * c) continue;
-        if (((idx++) & 7) != pidx0) continue;
-        if (c != fc) {
-          kv_fetch(kbase, vbase, c, lane, f);
-          fc = c;
-        }
-        float mx[4], ls[4], o[4][4];
-        chunk_eval<T>(H, A, stage, f, c, true, t1, qa, mx, ls, o);
-        if (kg == (t1 >> 2)) {
-          const int j = t1 & 3;
-#pragma unroll
-          for (int nb = 0; nb < 4; nb++) {
-            const float ov = j == 0 ? o[nb][0] : j == 1 ? o[nb][1] : j == 2 ? o[nb][2] : o[nb][3];
-            A.po[c - ns][t1][16 * nb + n] = ov;
-          }
-          if (n == 0) {
-            A.pm[c - ns][t1] = j == 0 ? mx[0] : j == 1 ? mx[1] : j == 2 ? mx[2] : mx[3];
-            A.pl[c - ns][t1] = j == 0 ? ls[0] : j == 1 ? ls[1] : j == 2 ? ls[2] : ls[3];
-          }
-        }
+      const bool cache = 64 * c < pos;
+      if (cache && c != fc) {
+        kv_fetch(kbase, vbase, c, lane, f);
+        fc = c;
       }
+      part_eval16<T>(H, A, stage, f, c, cache, qa);
     }
   }
   trace_mark(a, ILL_TRL * l + 6);

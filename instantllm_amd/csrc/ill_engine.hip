@@ -203,7 +203,7 @@ void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   if constexpr (EPI != OP_LMH) {
     if (M > 16) {   // prefill chunk: 64-row tiles, K split only where the tiles are few
       const int mt = (M + 63) / 64;
-      int S = std::max(1, std::min(256 / (ntn * mt), nsteps / 4));
+      int S = std::max(1, std::min(std::min(256 / (ntn * mt), nsteps / 4), OP_MAXS));
       g.ksteps = (nsteps + S - 1) / S;
       S = (nsteps + g.ksteps - 1) / g.ksteps;
       hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
@@ -218,7 +218,7 @@ void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   // k-steps per slice (the split depends on the matrix only, so 1-row and 16-row passes
   // sum the same partials in the same order)
   int S = 1;
-  if (EPI != OP_LMH) S = std::max(1, std::min((256 + ntn - 1) / ntn, nsteps / 4));
+  if (EPI != OP_LMH) S = std::max(1, std::min(std::min((256 + ntn - 1) / ntn, nsteps / 4), OP_MAXS));
   g.ksteps = (nsteps + S - 1) / S;
   S = (nsteps + g.ksteps - 1) / g.ksteps;
   hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), dim3(ntn, (M + 15) / 16, S), dim3(256), 0, e->stream, g);

@@ -61,9 +61,24 @@ struct OpCtx {
   int maxctx, layers, vocab;
 };
 
+// What the kernels need from the State and the control block, read once at kernel entry
+// together with their first operands (a load that gates the others would add a memory round
+// trip to every kernel); `done` is checked before the first store.
+struct OpHdr {
+  int done, pos, mode, wlog;
+};
+__device__ __forceinline__ OpHdr op_hdr(const OpCtx& c) {
+  OpHdr h;
+  h.done = gld(&c.st->done);
+  h.pos = gld(&c.st->pos);
+  h.mode = gld(&c.ctl->mode);
+  h.wlog = gld(&c.ctl->write_logits);
+  return h;
+}
+
 // Row t's position offset from pos (its depth): tree passes read the tree, others are chains.
-__device__ __forceinline__ int op_depth(const OpCtx& c, int t) {
-  return c.ctl->mode == ILL_MODE_TREE ? c.tree[ILL_TR_DEPTH + t] : (c.ctl->mode == ILL_MODE_DECODE ? 0 : t);
+__device__ __forceinline__ int op_depth(const OpCtx& c, int mode, int t) {
+  return mode == ILL_MODE_TREE ? gld(c.tree + ILL_TR_DEPTH + t) : (mode == ILL_MODE_DECODE ? 0 : t);
 }
 
 // ---- embedding and RMSNorm -----------------------------------------------------------
@@ -85,32 +100,37 @@ __device__ __forceinline__ float op_dequant1(const OpMat& m, int r, int k) {
 // x[t][:] = embedding row of ptoks[t] (Shaders.swift:118-126, :179-190)
 template <int FMT>
 __global__ __launch_bounds__(256) void op_embed_kernel(OpCtx c, int M) {
-  if (c.st->done) return;
+  const int done = gld(&c.st->done);
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= M * ILL_H) return;
   const int t = i / ILL_H, k = i % ILL_H;
-  c.x[i] = op_dequant1<FMT>(c.emb, c.ptoks[t], k);
+  const float v = op_dequant1<FMT>(c.emb, gld(c.ptoks + t), k);
+  if (!done) gst(c.x + i, v);
 }
 
 // xn[t] = f16(x[t] * rsqrt(mean(x^2) + eps) * gamma) for rows row0 .. row0 + M - 1 (one wave
 // per row; sum of squares in a fixed order). Output row index t - row0.
 __global__ __launch_bounds__(256) void op_norm_kernel(OpCtx c, const float* gamma, int row0, int M) {
-  if (c.st->done) return;
+  const int done = gld(&c.st->done);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + w;
   if (t >= M) return;
   const float* xr = c.x + (size_t)(row0 + t) * ILL_H;
-  float v[14];
-  float ss = 0.f;
+  float v[14], g[14];
 #pragma unroll
   for (int i = 0; i < 14; i++) {
-    v[i] = xr[64 * i + lane];
-    ss += v[i] * v[i];
+    v[i] = gld(xr + 64 * i + lane);
+    g[i] = gld(gamma + 64 * i + lane);
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 14; i++) ss += v[i] * v[i];
   ss = gsum<64>(ss);
   const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / (float)ILL_H) + ILL_EPS);
+  if (done) return;
 #pragma unroll
-  for (int i = 0; i < 14; i++) c.xn[(size_t)t * ILL_H + 64 * i + lane] = __float2half(v[i] * scale * gamma[64 * i + lane]);
+  for (int i = 0; i < 14; i++)
+    gst((uint16_t*)(c.xn + (size_t)t * ILL_H + 64 * i + lane), (uint16_t)__half_as_ushort(__float2half(v[i] * scale * g[i])));
 }
 
 // ---- GEMM: Y[M][N] = A[M][K] (f16) * W[N][K]^T, fused epilogues ------------------------
@@ -129,6 +149,7 @@ struct OpGemmArgs {
 #define OP_BN 128
 #define OP_BK 64
 #define OP_LDK 72    // LDS row stride in halves (padding against bank conflicts)
+#define OP_MAXS 24   // K slices of a split GEMM at most
 
 // One k-step (64 columns) of the weight tile, rows n0 .. n0+127, as loaded from HBM, and
 // its dequantization into LDS [128][OP_LDK] f16. Thread -> (row tid / 2, half tid % 2).
@@ -215,13 +236,13 @@ __device__ __forceinline__ void op_store_a(const ARaw<BM>& r, _Float16* As, int 
 // QKV: one rotary block b = columns 32 b .. +31 holds dims d (x0, columns 32 b + i) and
 // d + 32 (x1, columns 32 b + 16 + i) of head b / 2 (Convert.swift:236-244); q heads 0-13,
 // k 14-15, v 16-17: bias, RoPE at the row's position, then q or the K / V cache slot.
-__device__ __forceinline__ void epi_qkv(const OpCtx& c, int layer, int m, int b, int i, float x0, float x1) {
+__device__ __forceinline__ void epi_qkv(const OpCtx& c, const OpHdr& hd, int layer, int m, int b, int i, float x0, float x1) {
   const int head = b >> 1, d = (b & 1) * 16 + i;
-  x0 += c.L[layer].bqkv[32 * b + i];
-  x1 += c.L[layer].bqkv[32 * b + 16 + i];
-  const int pos = c.st->pos;
+  x0 += gld(c.L[layer].bqkv + 32 * b + i);
+  x1 += gld(c.L[layer].bqkv + 32 * b + 16 + i);
+  const int pos = hd.pos;
   if (head < ILL_NH + ILL_NKV) {
-    const float2 cs = c.rope[(pos + op_depth(c, m)) * 32 + d];
+    const float2 cs = gld(c.rope + (pos + op_depth(c, hd.mode, m)) * 32 + d);
     const float r0 = x0 * cs.x - x1 * cs.y, r1 = x1 * cs.x + x0 * cs.y;
     x0 = r0;
     x1 = r1;
@@ -252,7 +273,7 @@ __device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float 
 // operands are in flight while the current one is multiplied.
 template <int FMT, int BM, int EPI>
 __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
-  if (a.c.st->done) return;
+  const OpHdr hd = op_hdr(a.c);
   __shared__ __attribute__((aligned(16))) _Float16 As[BM * OP_LDK];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[OP_BN * OP_LDK];
   __shared__ uint64_t red[4][16];
@@ -294,6 +315,7 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
     }
     __syncthreads();
   }
+  if (hd.done) return;
   const OpCtx& c = a.c;
   if (gridDim.z > 1) {   // split K: partials for op_epi_kernel
 #pragma unroll
@@ -337,10 +359,10 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + 16 * i + 4 * kg + r;
-        if (m < a.M) epi_qkv(c, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
+        if (m < a.M) epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
       }
   } else {   // OP_LMH: logits (optional) and per-tile argmax keys per row (BM == 16)
-    const int wlog = c.ctl->write_logits;
+    const int wlog = hd.wlog;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int m = 4 * kg + r;
@@ -372,25 +394,35 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
 // RESID / SILU / QKV: one thread per output column / unit / rotary pair of a row.
 template <int EPI>
 __global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
-  if (a.c.st->done) return;
+  const OpHdr hd = op_hdr(a.c);
   const int N = a.W.N;
   const int per = EPI == OP_RESID ? N : N / 2;   // SILU: units; QKV: pairs
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= a.M * per) return;
   const int m = i / per, j = i % per;
+  // every slice's partial in flight at once, then added in slice order
   auto sum = [&](int col) {
-    float v = a.part[(size_t)m * N + col];
-    for (int z = 1; z < S; z++) v += a.part[((size_t)z * a.M + m) * N + col];
+    float pz[OP_MAXS];
+#pragma unroll
+    for (int z = 0; z < OP_MAXS; z++) pz[z] = z < S ? gld(a.part + ((size_t)z * a.M + m) * N + col) : 0.f;
+    float v = pz[0];
+#pragma unroll
+    for (int z = 1; z < OP_MAXS; z++)
+      if (z < S) v += pz[z];
     return v;
   };
   if constexpr (EPI == OP_RESID) {
-    a.resid[(size_t)m * ILL_H + j] += sum(j);
+    float* r = a.resid + (size_t)m * ILL_H + j;
+    const float x = gld(r), y = sum(j);
+    if (!hd.done) gst(r, x + y);
   } else if constexpr (EPI == OP_SILU) {
     const int q = j >> 1, r = j & 1;
-    epi_silu(a.c, m, j, sum(4 * q + r), sum(4 * q + 2 + r));
+    const float g = sum(4 * q + r), u = sum(4 * q + 2 + r);
+    if (!hd.done) epi_silu(a.c, m, j, g, u);
   } else if constexpr (EPI == OP_QKV) {
     const int b = j >> 4, ii = j & 15;
-    epi_qkv(a.c, a.layer, m, b, ii, sum(32 * b + ii), sum(32 * b + 16 + ii));
+    const float x0 = sum(32 * b + ii), x1 = sum(32 * b + 16 + ii);
+    if (!hd.done) epi_qkv(a.c, hd, a.layer, m, b, ii, x0, x1);
   }
 }
 
@@ -403,50 +435,59 @@ __global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
 // own path, not on M); prefill chunks use NW = 2 (short rows, many of them).
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, int M) {
-  if (c.st->done) return;
   __shared__ float qs[64];
   __shared__ float ps[NW][64];
   __shared__ int path[16];
   __shared__ float cm[NW], cl[NW], co[NW][64];
+  const OpHdr hd = op_hdr(c);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x / ILL_NH, h = blockIdx.x % ILL_NH, g = h / 7;
-  const int pos = c.st->pos;
-  const bool tree = c.ctl->mode == ILL_MODE_TREE;
-  const int dep = op_depth(c, t);
-  const int L = pos + dep + 1;
+  const int pos = hd.pos;
+  const bool tree = hd.mode == ILL_MODE_TREE;
   if (w == 0) {
+    const float qv = gld(c.q + (size_t)t * ILL_H + h * 64 + lane);
+    const int dep0 = op_depth(c, hd.mode, t);
     if (lane < 16) {   // rows on t's path by depth (tree passes: depth <= 15)
       int pr = lane;
       if (tree) {
         int r = t;
-        for (int d = dep; d >= 0; --d) {
+        for (int d = dep0; d >= 0; --d) {
           if (d == lane) pr = r;
-          r = r > 0 ? c.tree[ILL_TR_PARENT + r] : 0;
+          r = r > 0 ? gld(c.tree + ILL_TR_PARENT + r) : 0;
         }
       }
       path[lane] = pr;
     }
-    qs[lane] = c.q[(size_t)t * ILL_H + h * 64 + lane] * 0.125f;
+    qs[lane] = qv * 0.125f;
   }
+  const int dep = op_depth(c, hd.mode, t);
   __syncthreads();
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
+  const int L = pos + dep + 1;
   float Mx = -INFINITY, Ls = 0.f, O = 0.f;
   const int nch = (L + 63) >> 6;
-  for (int ch = w; ch < nch; ch += NW) {
+  // chunk ch: the K row of position 64 ch + lane (slot remapped along the path in tree
+  // passes) and the transposed V row of dim = lane; the next chunk streams in while the
+  // current one is evaluated
+  auto fetch = [&](int ch, uint4 (&kv)[8], uint4 (&vv)[8]) {
     const int vp = 64 * ch + lane;
-    const bool valid = vp < L;
     const int slot = min(vp < pos || !tree ? vp : pos + path[min(vp - pos, 15)], c.maxctx - 1);
-    // score of position vp (lane = position)
     const uint4* kr = (const uint4*)(kb + (size_t)slot * 64);
-    uint4 kv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
-    // P.V operands for dim = lane (transposed V: 64 slots per row), issued with K
     const uint4* vr = (const uint4*)(vb + ((size_t)ch * 64 + lane) * 64);
-    uint4 vv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
+  };
+  uint4 kv[8], vv[8];
+  if (w < nch) fetch(w, kv, vv);
+  for (int ch = w; ch < nch; ch += NW) {
+    uint4 kn[8], vn[8];
+    const bool more = ch + NW < nch;
+    if (more) fetch(ch + NW, kn, vn);
+    const int vp = 64 * ch + lane;
+    const bool valid = vp < L;
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -472,7 +513,7 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
         float v = h2f(x[e >> 1] >> (16 * (e & 1)));
         if (remap && vq >= pos && vq < L) {
           const int sl = pos + path[vq - pos];
-          v = h2f(vb[((size_t)(sl >> 6) * 64 + lane) * 64 + (sl & 63)]);
+          v = h2f(gld(vb + ((size_t)(sl >> 6) * 64 + lane) * 64 + (sl & 63)));
         }
         v = vq < L ? v : 0.f;
         oc = fmaf(ps[w][pp], v, oc);
@@ -483,6 +524,13 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
     O = att_fold(O, oc, k);
     Ls = att_fold(Ls, lc, k);
     Mx = k.mn;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        kv[i] = kn[i];
+        vv[i] = vn[i];
+      }
+    }
   }
   if (lane == 0) {
     cm[w] = Mx;
@@ -490,7 +538,7 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
   }
   co[w][lane] = O;
   __syncthreads();
-  if (w == 0) {
+  if (w == 0 && !hd.done) {
     float m = cm[0];
 #pragma unroll
     for (int ww = 1; ww < NW; ww++) m = fmaxf(m, cm[ww]);
@@ -501,7 +549,7 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
       sum = sum + cl[ww] * e;
       o = o + co[ww][lane] * e;
     }
-    c.ao[(size_t)t * ILL_H + h * 64 + lane] = __float2half(o / sum);
+    gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(o / sum)));
   }
 }
 

@@ -480,11 +480,14 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
 #pragma unroll
     for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
   };
+  // (prefill chunks, NW = 2: many short rows, where the doubled registers cost more
+  // occupancy than the prefetch saves: no prefetch)
+  constexpr bool PF = NW >= 8;
   uint4 kv[8], vv[8];
   if (w < nch) fetch(w, kv, vv);
   for (int ch = w; ch < nch; ch += NW) {
     uint4 kn[8], vn[8];
-    const bool more = ch + NW < nch;
+    const bool more = PF && ch + NW < nch;
     if (more) fetch(ch + NW, kn, vn);
     const int vp = 64 * ch + lane;
     const bool valid = vp < L;
@@ -530,6 +533,8 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
         kv[i] = kn[i];
         vv[i] = vn[i];
       }
+    } else if (!PF && ch + NW < nch) {
+      fetch(ch + NW, kv, vv);
     }
   }
   if (lane == 0) {

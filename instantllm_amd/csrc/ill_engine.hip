@@ -241,7 +241,7 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     const OpLayerW& L = e->holayers[l];
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
-    if (M > 16) hipLaunchKernelGGL(op_attn_kernel<2>, dim3(M * ILL_NH), dim3(128), 0, s, c, l, M);
+    if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64), 0, s, c, l, M);
     else hipLaunchKernelGGL(op_attn_kernel<ILL_WAVES>, dim3(M * ILL_NH), dim3(64 * ILL_WAVES), 0, s, c, l, M);
     op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x);
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);

@@ -558,6 +558,131 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
   }
 }
 
+// ---- attention of prefill chunks (more than 16 rows): MFMA flash attention --------------
+// One wave per (16-row block, query head h). Row t < M sits at position pos + t and attends
+// to positions 0 .. pos + t, all in the cache (this chunk's QKV kernel has written its own
+// keys and values). Per 64-position chunk: scores (0.125 q) . k on v_mfma_f32_16x16x32_f16
+// with q split into f16 high and low parts (products as accurate as fp32 q), the causal
+// mask, the row softmax statistics (maximum, sum of exponentials) folded chunk by chunk with
+// the rule of the other attention kernels, and O += P V with P split the same way. The next
+// chunk's keys and values stream in while one is evaluated.
+__global__ __launch_bounds__(64) void op_attn_rows_kernel(OpCtx c, int layer, int M) {
+  __shared__ float pb[16 * 64];
+  const OpHdr hd = op_hdr(c);
+  const int lane = threadIdx.x, kg = lane >> 4, n = lane & 15;
+  const int t0 = 16 * blockIdx.x, h = blockIdx.y, g = h / 7;
+  const int pos = hd.pos;
+  // A operand: lane (kg, n) holds row t0 + n, dims 32 ks + 8 kg + i
+  v8h qa[2][2];
+  {
+    const float* qr = c.q + (size_t)min(t0 + n, M - 1) * ILL_H + h * 64;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const uint4 a0 = gld((const uint4*)(qr + 32 * ks + 8 * kg)), a1 = gld((const uint4*)(qr + 32 * ks + 8 * kg + 4));
+      const uint32_t x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float v = __uint_as_float(x[i]) * 0.125f;
+        const _Float16 hi = (_Float16)v;
+        qa[ks][0][i] = hi;
+        qa[ks][1][i] = (_Float16)(v - (float)hi);
+      }
+    }
+  }
+  int Lr[4];   // L of this lane's rows t0 + 4 kg + j (0: no row)
+#pragma unroll
+  for (int j = 0; j < 4; j++) Lr[j] = t0 + 4 * kg + j < M ? pos + t0 + 4 * kg + j + 1 : 0;
+  const int nch = (pos + min(t0 + 16, M) + 63) >> 6;
+  const uint16_t* kbase = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
+  const uint16_t* vbase = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 64 * 64;
+  float Mx[4], Ls[4], O[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    Mx[j] = -INFINITY;
+    Ls[j] = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
+  }
+  KVFrag f;
+  kv_fetch(kbase, vbase, 0, lane, f);
+  for (int ch = 0; ch < nch; ch++) {
+    KVFrag fn;
+    const bool more = ch + 1 < nch;
+    if (more) kv_fetch(kbase, vbase, ch + 1, lane, fn);
+    float sc[4][4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      v4f sv = {0.f, 0.f, 0.f, 0.f};
+      sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], u4_to_v8h(f.k[b][0]), sv, 0, 0, 0);
+      sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], u4_to_v8h(f.k[b][0]), sv, 0, 0, 0);
+      sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], u4_to_v8h(f.k[b][1]), sv, 0, 0, 0);
+      sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(f.k[b][1]), sv, 0, 0, 0);
+      const int vp = 64 * ch + 16 * b + n;
+#pragma unroll
+      for (int j = 0; j < 4; j++) sc[b][j] = vp < Lr[j] ? sv[j] : -INFINITY;
+    }
+    float mx[4], ls[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      mx[j] = gmax<16>(fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j])));
+      const float ms = mx[j] == -INFINITY ? 0.f : mx[j];   // a row with no position here: p = 0
+      float sum = 0.f;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        sc[b][j] = att_exp(sc[b][j] - ms);
+        sum += sc[b][j];
+      }
+      ls[j] = gsum<16>(sum);
+#pragma unroll
+      for (int b = 0; b < 4; b++) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    v8h ph[2], pl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float p = pb[n * 64 + 32 * ks + 8 * kg + i];
+        const _Float16 hi = (_Float16)p;
+        ph[ks][i] = hi;
+        pl[ks][i] = (_Float16)(p - (float)hi);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[0], u4_to_v8h(f.v[nb][0]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[0], u4_to_v8h(f.v[nb][0]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[1], u4_to_v8h(f.v[nb][1]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[1], u4_to_v8h(f.v[nb][1]), acc, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if (mx[j] == -INFINITY) continue;   // nothing of this row in the chunk
+        const AttScale k = att_scale(Mx[j], mx[j]);
+        O[nb][j] = att_fold(O[nb][j], acc[j], k);
+        if (nb == 3) {
+          Ls[j] = att_fold(Ls[j], ls[j], k);
+          Mx[j] = k.mn;
+        }
+      }
+    }
+    if (more) f = fn;
+  }
+  if (hd.done) return;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int t = t0 + 4 * kg + j;
+    if (t < M) {
+#pragma unroll
+      for (int nb = 0; nb < 4; nb++)
+        gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + 16 * nb + n), (uint16_t)__half_as_ushort(__float2half(O[nb][j] / Ls[j])));
+    }
+  }
+}
+
 // ---- commit ----------------------------------------------------------------------------
 // Global argmax of rows lmh0 .. lmh0 + lmhn - 1 over the lm_head tiles, then the same
 // commit as the pass kernel (greedy, chain or tree accept, KV compaction, State advance).

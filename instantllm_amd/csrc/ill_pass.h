@@ -395,41 +395,40 @@ __device__ __forceinline__ void pub_write(const PrepLds<1>& P, float rs, uint64_
 
 // The consumer side: rows 0 .. nrows - 1 of a published coding (src = row 0) into P, as
 // prep896<T> would have left it (rows >= nrows coded as zeros), and the row scales of this
-// lane's rows 4 kg + j in rs[j]. Every wave waits for its own words.
+// lane's rows 4 kg + j in rs[j]. Half-wave r of the workgroup reads row r, words lane + 32 j
+// (j < 15): for j < 14 the word's kind (high / low bytes) and place follow from j and the
+// lane by shifts, so placing a word costs no division.
 template <int T>
 __device__ __forceinline__ bool pub_read(const uint64_t* src, uint32_t tag, int nrows, PrepLds<T>& P, IllCtl* ctl,
                                          int code, const IllPassArgs& a, float rs[4], int trs = -1) {
-  static_assert(T == ILL_MAXT, "published codings are read by 16-row passes");
+  static_assert(T == ILL_MAXT && ILL_PUB_W == 15 * 32 && T * 32 == ILL_WG_THREADS, "one half-wave per row");
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  constexpr int NI = (T * ILL_PUB_W + ILL_WG_THREADS - 1) / ILL_WG_THREADS;
-  uint32_t v[NI];
+  const int t = tid >> 5, l32 = tid & 31;
+  const bool live = t < nrows;
+  const uint64_t* rp = src + (size_t)t * ILL_PUB_W + l32;
+  uint32_t v[15];
   const bool alive = wave_wait([&]() {
     bool ok = true;
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const int f = tid + ILL_WG_THREADS * i;
-      const int t = f / ILL_PUB_W, k = f % ILL_PUB_W;
-      v[i] = 0u;
-      if (t < nrows && k < ILL_PUB_PAY) {
-        const uint64_t x = aload64(src + f);
+    for (int j = 0; j < 15; j++) {
+      v[j] = 0u;
+      if (live && 32 * j + l32 < ILL_PUB_PAY) {
+        const uint64_t x = aload64(rp + 32 * j);
         ok &= (uint32_t)(x >> 32) == tag;
-        v[i] = (uint32_t)x;
+        v[j] = (uint32_t)x;
       }
     }
     return ok;
   }, ctl, code);
   if (trs >= 0) trace_mark(a, trs);
 #pragma unroll
-  for (int i = 0; i < NI; i++) {
-    const int f = tid + ILL_WG_THREADS * i;
-    const int t = f / ILL_PUB_W, k = f % ILL_PUB_W;
-    if (t < T && k < ILL_PUB_PAY) {
-      if (k < 224) ((uint32_t*)P.ahi)[((k >> 2) * T + t) * 4 + (k & 3)] = v[i];
-      else if (k < 448) ((uint32_t*)P.alo)[(((k - 224) >> 2) * T + t) * 4 + (k & 3)] = v[i];
-      else if (k < 476) ((uint32_t*)P.sc)[(((k - 448) >> 1) * T + t) * 2 + (k & 1)] = v[i];
-      else P.red[0][t] = t < nrows ? __uint_as_float(v[i]) : 1.f;
-    }
+  for (int j = 0; j < 14; j++) {   // codes: word k = 32 j + l32 holds uint4 k / 4 (group, k-group), dword k % 4
+    const int k = (j % 7) * 32 + l32;
+    uint32_t* dst = (uint32_t*)(j < 7 ? P.ahi : P.alo);
+    dst[((k >> 2) * T + t) * 4 + (k & 3)] = v[j];
   }
+  if (l32 < 28) ((uint32_t*)P.sc)[((l32 >> 1) * T + t) * 2 + (l32 & 1)] = v[14];
+  else if (l32 == 28) P.red[0][t] = live ? __uint_as_float(v[14]) : 1.f;
   if (lane == 0) P.ok[w] = alive;
   lds_barrier();
   const int4 ok0 = *(const int4*)&P.ok[0], ok1 = *(const int4*)&P.ok[4];

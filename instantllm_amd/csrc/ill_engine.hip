@@ -119,6 +119,7 @@ struct ill_engine {
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   int graph_steps = 0;
+  int pos_hint = 0;   // the State's pos as the host last knew it: picks the attention split
   IllCtl hctl{};
   IllPassArgs args{};
   int logits_rows_valid = 0;
@@ -237,12 +238,19 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
   const OpCtx& c = e->octx;
   hipStream_t s = e->stream;
   hipLaunchKernelGGL(op_embed_kernel<FMT>, dim3((M * ILL_H + 255) / 256), dim3(256), 0, s, c, M);
+  // passes of up to 16 rows: attention split over up to 8 workgroups per (row, head), one
+  // per 1024 positions of context (the result does not depend on the split)
+  const int nch = (e->pos_hint + M + 63) / 64;
+  const int nsplit = std::max(1, std::min(OP_NSPLIT, (nch + 15) / 16));
   for (int l = 0; l < e->layers; l++) {
     const OpLayerW& L = e->holayers[l];
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
     if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64), 0, s, c, l, M);
-    else hipLaunchKernelGGL(op_attn_kernel<ILL_WAVES>, dim3(M * ILL_NH), dim3(64 * ILL_WAVES), 0, s, c, l, M);
+    else {
+      hipLaunchKernelGGL(op_attn_kernel, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart);
+      if (nsplit > 1) hipLaunchKernelGGL(op_attn_combine_kernel, dim3(M * ILL_NH), dim3(64), 0, s, c, (const float*)e->opart);
+    }
     op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x);
     hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
     op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr);
@@ -606,6 +614,7 @@ int ill_set_state(ill_engine* e, const int32_t state[16]) {
   if (s.pos < 0 || s.pos >= e->maxctx) return fail(ILL_E_ARG, "pos %d outside the context", s.pos);
   HCK(hipMemcpyAsync(e->st, &s, sizeof s, hipMemcpyHostToDevice, e->stream));
   HCK(hipStreamSynchronize(e->stream));
+  e->pos_hint = s.pos;
   return ILL_OK;
 }
 
@@ -635,11 +644,13 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
       HCK(hipMemcpyAsync(e->ptoks, toks + c0, rows * 4, hipMemcpyHostToDevice, e->stream));
       if ((rc = write_pos_n(e, pos, rows))) return rc;
       if ((rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, last ? 1 : 0, last ? write_logits : 0, last ? 1 : 0))) return rc;
+      e->pos_hint = pos;
       if ((rc = op_launch(e, rows, last ? 1 : 0))) return rc;
       pos += rows;
       HCK(hipStreamSynchronize(e->stream));
     }
     if (write_logits) e->logits_rows_valid = 1;
+    e->pos_hint = s.pos + n;
     return check_err(e);
   }
   for (int c0 = 0; c0 < n; c0 += 16) {
@@ -656,6 +667,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
     HCK(hipStreamSynchronize(e->stream));
   }
   if (write_logits) e->logits_rows_valid = 0;
+  e->pos_hint = s.pos + n;
   if ((rc = check_err(e))) return rc;
   if (write_logits) {
     // the last row's logits sit at row (rows - 1); move them to row 0 for ill_read_logits
@@ -671,6 +683,7 @@ int ill_decode_step(ill_engine* e, int write_logits) {
   int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits, 1);
   if (rc) return rc;
   if ((rc = e->fmt == 2 ? launch(e, 1) : op_launch(e, 1, 1))) return rc;
+  e->pos_hint++;
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = 1;
   return ILL_OK;
@@ -703,7 +716,9 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
   if (tree) HCK(hipMemcpyAsync(e->tree, tree, ILL_TR_INTS * 4, hipMemcpyHostToDevice, e->stream));
   if ((rc = write_pos_n(e, s.pos, rows))) return rc;
   if ((rc = set_ctl(e, tree ? ILL_MODE_TREE : ILL_MODE_ROWS, rows, 0, rows, write_logits, 2))) return rc;
+  e->pos_hint = s.pos;
   if ((rc = e->fmt == 2 ? launch(e, rows == 1 ? 1 : 16) : op_launch(e, rows, rows))) return rc;
+  e->pos_hint = s.pos + 1;   // at least the root is accepted
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = rows;
   return ILL_OK;
@@ -721,10 +736,13 @@ int ill_capture_steps(ill_engine* e, int nsteps) {
   }
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  const int base = e->pos_hint;
   for (int i = 0; i < nsteps; i++) {
+    e->pos_hint = base + i;
     if (e->fmt == 2) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
     else op_seq_fmt(e, 1, 1);
   }
+  e->pos_hint = base;
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = nsteps;
@@ -736,6 +754,7 @@ int ill_launch_graph(ill_engine* e) {
   int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
   if (rc) return rc;
   HCK(hipGraphLaunch(e->gexec, e->stream));
+  e->pos_hint += e->graph_steps;
   return ILL_OK;
 }
 

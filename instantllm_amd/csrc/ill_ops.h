@@ -426,22 +426,56 @@ __global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
   }
 }
 
-// ---- attention: one workgroup of NW waves per (row, query head) ---------------------
-// Row t attends to virtual positions 0 .. L-1, L = pos + depth(t) + 1; position p lives
-// in cache slot p below pos and in slot pos + (the row on t's path at depth p - pos) above
-// (tree passes; chains use slot p). 64-position chunk c goes to wave c % NW, which folds its
-// chunks in order with the pass kernel's rule; the waves are then combined against the
-// global maximum. Passes of up to 16 rows use NW = 8 (the split depends only on the row's
-// own path, not on M); prefill chunks use NW = 2 (short rows, many of them).
-template <int NW>
-__global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, int M) {
-  __shared__ float qs[64];
-  __shared__ float ps[NW][64];
+// ---- attention of passes of up to 16 rows -------------------------------------------------
+// Row t attends to virtual positions 0 .. L-1, L = pos + depth(t) + 1; position p lives in
+// cache slot p below pos and in slot pos + (the row on t's path at depth p - pos) above
+// (tree passes; chains use slot p). The row's 64-position chunks are dealt to 64 slots:
+// chunk c to slot (split s = (c / 16) % 8, wave w = c % 8), so a context of up to 1024
+// positions is all split 0. Slot (s, w) folds its chunks in increasing order with the pass
+// kernel's rule, the eight slots of split s are combined against their maximum (in w
+// order), then the eight splits against theirs (in s order).
+// The grouping depends only on the row's L, not on M or on how the work is launched, so a
+// row decoded alone and the same row inside a 16-row pass give identical bits.
+// One workgroup of 8 waves per (row t, query head h, part j < nsplit) runs the splits j,
+// j + nsplit, ...: with nsplit = 1 it finishes the row; otherwise it stores its split
+// states and op_attn_combine_kernel finishes the row. (The host picks nsplit from the
+// context length it expects; any value gives the same result.)
+#define OP_NSPLIT 8
+#define OP_SPLIT_W 66   // scratch words per split state: m, l, o[64]
+#define OP_VST 72       // LDS stride (halves) of a staged V row
+
+// (m, l, o) of n states combined against their maximum, in index order; states with
+// m = -inf (no positions) add nothing, and if all are empty the result is empty too.
+template <int N>
+__device__ __forceinline__ void att_combine(const float* m, const float* l, const float* o, float& mo, float& lo, float& oo) {
+  float mm = m[0];
+#pragma unroll
+  for (int i = 1; i < N; i++) mm = fmaxf(mm, m[i]);
+  float sum = 0.f, acc = 0.f;
+  if (mm != -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      const float e = att_exp(m[i] - mm);
+      sum = sum + l[i] * e;
+      acc = acc + o[i] * e;
+    }
+  }
+  mo = mm;
+  lo = sum;
+  oo = acc;
+}
+
+__global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int layer, int M, int nsplit, float* scratch) {
+  __shared__ __attribute__((aligned(16))) float qs[64];
+  __shared__ __attribute__((aligned(16))) float ps[ILL_WAVES][64];
   __shared__ int path[16];
-  __shared__ float cm[NW], cl[NW], co[NW][64];
+  __shared__ float cm[OP_NSPLIT][ILL_WAVES], cl[OP_NSPLIT][ILL_WAVES], co[OP_NSPLIT][ILL_WAVES][64];
+  __shared__ float sm[OP_NSPLIT], sl[OP_NSPLIT], so[OP_NSPLIT][64];
+  __shared__ __attribute__((aligned(16))) uint16_t vstage[ILL_WAVES][64 * OP_VST];   // tree passes: V rows
   const OpHdr hd = op_hdr(c);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x / ILL_NH, h = blockIdx.x % ILL_NH, g = h / 7;
+  const int rh = blockIdx.x / nsplit, j = blockIdx.x % nsplit;
+  const int t = rh / ILL_NH, h = rh % ILL_NH, g = h / 7;
   const int pos = hd.pos;
   const bool tree = hd.mode == ILL_MODE_TREE;
   if (w == 0) {
@@ -465,11 +499,10 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
   const int L = pos + dep + 1;
-  float Mx = -INFINITY, Ls = 0.f, O = 0.f;
   const int nch = (L + 63) >> 6;
+  const int nne = min(OP_NSPLIT, (nch + 15) >> 4);   // splits 0 .. nne - 1 hold chunks
   // chunk ch: the K row of position 64 ch + lane (slot remapped along the path in tree
-  // passes) and the transposed V row of dim = lane; the next chunk streams in while the
-  // current one is evaluated
+  // passes) and the transposed V row of dim = lane
   auto fetch = [&](int ch, uint4 (&kv)[8], uint4 (&vv)[8]) {
     const int vp = 64 * ch + lane;
     const int slot = min(vp < pos || !tree ? vp : pos + path[min(vp - pos, 15)], c.maxctx - 1);
@@ -480,82 +513,169 @@ __global__ __launch_bounds__(64 * NW) void op_attn_kernel(OpCtx c, int layer, in
 #pragma unroll
     for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
   };
-  // (prefill chunks, NW = 2: many short rows, where the doubled registers cost more
-  // occupancy than the prefetch saves: no prefetch)
-  constexpr bool PF = NW >= 8;
-  uint4 kv[8], vv[8];
-  if (w < nch) fetch(w, kv, vv);
-  for (int ch = w; ch < nch; ch += NW) {
-    uint4 kn[8], vn[8];
-    const bool more = PF && ch + NW < nch;
-    if (more) fetch(ch + NW, kn, vn);
-    const int vp = 64 * ch + lane;
-    const bool valid = vp < L;
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t x[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
-#pragma unroll
-      for (int e = 0; e < 8; e++) s = fmaf(qs[8 * i + e], h2f(x[e >> 1] >> (16 * (e & 1))), s);
-    }
-    s = valid ? s : -INFINITY;
-    const float mc = gmax<64>(s);
-    const float p = valid ? att_exp(s - mc) : 0.f;
-    const float lc = gsum<64>(p);
-    ps[w][lane] = p;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    float oc = 0.f;
-    const bool remap = tree && 64 * ch + 63 >= pos;   // wave-uniform
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t x[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int pp = 8 * i + e, vq = 64 * ch + pp;
-        float v = h2f(x[e >> 1] >> (16 * (e & 1)));
-        if (remap && vq >= pos && vq < L) {
-          const int sl = pos + path[vq - pos];
-          v = h2f(gld(vb + ((size_t)(sl >> 6) * 64 + lane) * 64 + (sl & 63)));
-        }
-        v = vq < L ? v : 0.f;
-        oc = fmaf(ps[w][pp], v, oc);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    const AttScale k = att_scale(Mx, mc);
-    O = att_fold(O, oc, k);
-    Ls = att_fold(Ls, lc, k);
-    Mx = k.mn;
-    if (more) {
+#pragma unroll 1
+  for (int q = 0; q < OP_NSPLIT; q++) {
+    const int s = j + nsplit * q;
+    if (s >= nne) break;
+    float Mx = -INFINITY, Ls = 0.f, O = 0.f;
+    // this wave's chunks of split s: 128 r + 16 s + 8 b + w (r = 0, 1, ..., b = 0, 1) in
+    // order; the next one streams in while one is evaluated
+    auto chunk_of = [&](int i) { return 128 * (i >> 1) + 16 * s + 8 * (i & 1) + w; };
+    uint4 kv[8], vv[8];
+    int ch = chunk_of(0);
+    if (ch < nch) fetch(ch, kv, vv);
+    for (int ci = 0; ch < nch; ch = chunk_of(++ci)) {
+      uint4 kn[8], vn[8];
+      const int nx = chunk_of(ci + 1);
+      const bool more = nx < nch;
+      if (more) fetch(nx, kn, vn);
+      const int vp = 64 * ch + lane;
+      const bool valid = vp < L;
+      float sc = 0.f;
+      // q is re-read from LDS for every chunk (broadcast reads): held in registers it would
+      // push the two K/V buffers out of them
+      asm volatile("" ::: "memory");
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        kv[i] = kn[i];
-        vv[i] = vn[i];
+        const uint32_t x[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+        const float4 qa = *(const float4*)&qs[8 * i], qb = *(const float4*)&qs[8 * i + 4];
+        const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) sc = fmaf(qv[e], h2f(x[e >> 1] >> (16 * (e & 1))), sc);
       }
-    } else if (!PF && ch + NW < nch) {
-      fetch(ch + NW, kv, vv);
+      sc = valid ? sc : -INFINITY;
+      const float mc = gmax<64>(sc);
+      const float p = valid ? att_exp(sc - mc) : 0.f;
+      const float lc = gsum<64>(p);
+      ps[w][lane] = p;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      float oc = 0.f;
+      if (tree && 64 * ch + 63 >= pos) {   // wave-uniform: positions pos .. L-1 of the chunk
+        // take the V of the path rows' slots: this lane's V row goes through LDS, where
+        // those (at most 16) positions are replaced
+        uint16_t* vr = &vstage[w][lane * OP_VST];
+#pragma unroll
+        for (int i = 0; i < 8; i++) *(uint4*)(vr + 8 * i) = vv[i];
+        const int p0 = max(pos - 64 * ch, 0), p1 = min(L - 64 * ch, 64);
+        uint16_t pv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+          const int pp = p0 + k;
+          if (pp < p1) {
+            const int sl2 = pos + path[64 * ch + pp - pos];
+            pv[k] = gld(vb + ((size_t)(sl2 >> 6) * 64 + lane) * 64 + (sl2 & 63));
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          if (p0 + k < p1) vr[p0 + k] = pv[k];
+#pragma unroll
+        for (int i = 0; i < 8; i++) vv[i] = *(const uint4*)(vr + 8 * i);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t x[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int pp = 8 * i + e, vq = 64 * ch + pp;
+          float v = h2f(x[e >> 1] >> (16 * (e & 1)));
+          v = vq < L ? v : 0.f;
+          oc = fmaf(ps[w][pp], v, oc);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      const AttScale k = att_scale(Mx, mc);
+      O = att_fold(O, oc, k);
+      Ls = att_fold(Ls, lc, k);
+      Mx = k.mn;
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          kv[i] = kn[i];
+          vv[i] = vn[i];
+        }
+      }
+    }
+    if (lane == 0) {
+      cm[q][w] = Mx;
+      cl[q][w] = Ls;
+    }
+    co[q][w][lane] = O;
+  }
+  __syncthreads();
+  if (nsplit == 1 && nne == 1) {   // one split: its state is the row's (the general path
+    if (w == 0 && !hd.done) {      // below gives the same bits: scale 1, nothing added)
+      float o[ILL_WAVES];
+#pragma unroll
+      for (int ww = 0; ww < ILL_WAVES; ww++) o[ww] = co[0][ww][lane];
+      float mo, lo, oo;
+      att_combine<ILL_WAVES>(cm[0], cl[0], o, mo, lo, oo);
+      gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
+    }
+    return;
+  }
+  // split states: wave q combines the slots of split j + nsplit q (empty splits: m = -inf)
+  const int nq = (OP_NSPLIT - j + nsplit - 1) / nsplit;
+  if (w < nq) {
+    if (j + nsplit * w >= nne) {   // no chunks: nothing was stored for it
+      if (lane == 0) {
+        cm[w][0] = -INFINITY;
+        cl[w][0] = 0.f;
+      }
+#pragma unroll
+      for (int ww = 1; ww < ILL_WAVES; ww++)
+        if (lane == 0) cm[w][ww] = -INFINITY;
+    }
+    float o[ILL_WAVES];
+#pragma unroll
+    for (int ww = 0; ww < ILL_WAVES; ww++) o[ww] = co[w][ww][lane];
+    float mo, lo, oo;
+    att_combine<ILL_WAVES>(cm[w], cl[w], o, mo, lo, oo);
+    if (nsplit == 1) {
+      if (lane == 0) {
+        sm[w] = mo;
+        sl[w] = lo;
+      }
+      so[w][lane] = oo;
+    } else {
+      float* dst = scratch + ((size_t)rh * OP_NSPLIT + j + nsplit * w) * OP_SPLIT_W;
+      if (lane == 0) {
+        dst[0] = mo;
+        dst[1] = lo;
+      }
+      dst[2 + lane] = oo;
     }
   }
-  if (lane == 0) {
-    cm[w] = Mx;
-    cl[w] = Ls;
-  }
-  co[w][lane] = O;
+  if (nsplit > 1) return;
   __syncthreads();
   if (w == 0 && !hd.done) {
-    float m = cm[0];
+    float o[OP_NSPLIT];
 #pragma unroll
-    for (int ww = 1; ww < NW; ww++) m = fmaxf(m, cm[ww]);
-    float sum = 0.f, o = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ww++) {
-      const float e = att_exp(cm[ww] - m);
-      sum = sum + cl[ww] * e;
-      o = o + co[ww][lane] * e;
-    }
-    gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(o / sum)));
+    for (int q = 0; q < OP_NSPLIT; q++) o[q] = so[q][lane];
+    float mo, lo, oo;
+    att_combine<OP_NSPLIT>(sm, sl, o, mo, lo, oo);
+    gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
   }
+}
+
+// The rows of op_attn_kernel launched with nsplit > 1: the eight split states of (row, head)
+// combined in split order.
+__global__ __launch_bounds__(64) void op_attn_combine_kernel(OpCtx c, const float* scratch) {
+  const int done = gld(&c.st->done);
+  const int rh = blockIdx.x, lane = threadIdx.x;
+  const int t = rh / ILL_NH, h = rh % ILL_NH;
+  float m[OP_NSPLIT], l[OP_NSPLIT], o[OP_NSPLIT];
+#pragma unroll
+  for (int s = 0; s < OP_NSPLIT; s++) {
+    const float* src = scratch + ((size_t)rh * OP_NSPLIT + s) * OP_SPLIT_W;
+    m[s] = gld(src);
+    l[s] = gld(src + 1);
+    o[s] = gld(src + 2 + lane);
+  }
+  float mo, lo, oo;
+  att_combine<OP_NSPLIT>(m, l, o, mo, lo, oo);
+  if (!done) gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
 }
 
 // ---- attention of prefill chunks (more than 16 rows): MFMA flash attention --------------

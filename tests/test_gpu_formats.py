@@ -122,3 +122,41 @@ def test_long_prefill_chunks(model):
     tok = int(e.out_tokens()[0])
     e.decode_step(write_logits=True)
     assert metrics.rel_l2(e.read_logits(0), m.forward([tok], cache)) <= REL_L2_TOL
+
+
+def test_split_attention_rows_bit_identical_long_context(tmp_path):
+    """Past 1024 positions the 1-row and 16-row attention of the layer-by-layer path is split
+    over several workgroups per (row, head). The split follows the launch (1-row steps here
+    run both split and unsplit) but the grouping of the arithmetic follows the row alone, so
+    tree rows must still equal sequential 1-row steps bit for bit, and match the oracle."""
+    from instantllm_amd.engine import Engine
+    path = str(tmp_path / "m.ill")
+    synth.build_model(path, F.FMT_Q8, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB))
+    m = qwen.Model(illread.load(path))
+    e = Engine(path, max_context=2048, max_pass=16, max_steps=256)
+    try:
+        rng = np.random.default_rng(91)
+        ctx = [int(t) for t in rng.integers(0, VOCAB, size=1015)]
+        e.reset_out_tokens()
+        e.set_state(pos=0, n=len(ctx), maxsteps=200, eos=NO_EOS)
+        log("q8: prefill 1015, 16-row tree pass, sequential steps along its paths")
+        e.prefill(ctx)
+        st = e.get_state()
+        tr = synth.random_tree(rng, 16, VOCAB)
+        e.set_state(pos=st["pos"], n=16, maxsteps=200, eos=NO_EOS)
+        e.verify_pass(16, tree=tr, write_logits=True)
+        rows = np.stack([e.read_logits(r) for r in range(16)])
+        cache = m.new_cache(1100)
+        m.forward(ctx, cache)
+        ref = T.tree_logits(m, cache, tr)
+        for r in range(16):
+            assert metrics.rel_l2(rows[r], ref[r]) <= REL_L2_TOL, r
+        tok = tr[T.TR_TOK:T.TR_TOK + 16]
+        for p in T.paths(tr)[:3]:
+            for k, r in enumerate(p):
+                e.set_state(pos=st["pos"] + k, n=1, maxsteps=200, eos=NO_EOS)
+                e.prefill([int(tok[r])], write_logits=True)
+                one = e.read_logits(0)
+                assert np.array_equal(one.view(np.uint32), rows[r].view(np.uint32)), (p, k, r)
+    finally:
+        e.close()

@@ -38,8 +38,8 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
 # a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (169,523.25 x 2 + 16,694.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 364_278_464
+# (167,467.94 x 2 + 16,358.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 359_725_120
 
 
 def step_bytes(L: float) -> float:
@@ -117,10 +117,11 @@ def prefill_flops(m: int, layers: int = 24) -> float:
     return 2.0 * m * LAYER_PARAMS + 2.0 * LMH_PARAMS + attn
 
 
-def config4(steps: int = 64) -> dict:
+def config4(steps: int = 64, single: bool = False) -> dict:
     """Config 4: q8 (symmetric group-64) and f16 models (seed 4): a 512-token prefill on the
     MFMA GEMMs, then `steps` graph-captured greedy decode steps; then the same after a
-    4032-token prompt, so the last step attends 4096 positions."""
+    4032-token prompt, so the last step attends 4096 positions. With `single` the decode
+    steps are launched one by one (for profilers) and timed by HIP events around each."""
     from instantllm_amd import synth, illfile as F
     from instantllm_amd.engine import Engine
     no_eos = (-5, -5)
@@ -135,14 +136,22 @@ def config4(steps: int = 64) -> dict:
             e.set_state(pos=0, n=512, maxsteps=steps + 1, eos=no_eos)
             e.prefill(prompt)
             pre_ms.append(e.last_pass_ms())
-        e.capture_steps(steps)
-        dec_ms = e.time_graph(1)
+        def decode() -> float:
+            if single:
+                ms = 0.0
+                for _ in range(steps):
+                    e.decode_step()
+                    ms += e.last_pass_ms()
+                return ms
+            e.capture_steps(steps)
+            return e.time_graph(1)
+
+        dec_ms = decode()
         longp = [int(t) for t in rng.integers(0, F.VOCAB, size=4032)]
         e.reset_out_tokens()
         e.set_state(pos=0, n=len(longp), maxsteps=steps + 1, eos=no_eos)
         e.prefill(longp)
-        e.capture_steps(steps)
-        long_ms = e.time_graph(1)
+        long_ms = decode()
         pos_end = e.get_state()["pos"]
         e.close()
         pm = float(np.median(pre_ms))
@@ -291,7 +300,7 @@ def main() -> int:
     if not args.no_gemv:
         line["gemv_config1"] = gemv_config1()
     if not args.no_config4:
-        line["config4"] = config4()
+        line["config4"] = config4(single=single)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(path, prompt[:48], args.cpu_steps)
     print(json.dumps(line), flush=True)

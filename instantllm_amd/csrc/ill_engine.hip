@@ -978,7 +978,7 @@ int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* sb, i
   }
   if (hipMalloc(&g->x, (size_t)K * 4) != hipSuccess || hipMalloc(&g->gamma, (size_t)K * 4) != hipSuccess ||
       hipMalloc(&g->part, (size_t)g->ks * rows * 4) != hipSuccess || hipMalloc(&g->y, (size_t)rows * 4) != hipSuccess ||
-      hipMalloc(&g->key, 8) != hipSuccess)
+      hipMalloc(&g->key, 16) != hipSuccess)
     return bad(fail(ILL_E_HIP, "gemv buffer allocation failed"));
   if (hipStreamCreate(&g->stream) != hipSuccess || hipEventCreate(&g->e0) != hipSuccess || hipEventCreate(&g->e1) != hipSuccess)
     return bad(fail(ILL_E_HIP, "stream / event creation failed"));
@@ -1000,13 +1000,26 @@ int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, flo
   a.bps = g->bps;
   a.ks = g->ks;
   const int fin_blocks = (g->rows + 255) / 256;
+  // one slice: the gemv kernel writes y and the argmax itself (keys alternate between two
+  // words, each launch clearing the other one)
+  const bool direct = g->ks == 1;
+  if (direct && amax) HCK(hipMemsetAsync(g->key, 0, 16, g->stream));
+  int par = 0;
   auto one = [&](int c) -> int {
     a.w = g->w[c];
     a.s = g->s[c];
-    if (amax) HCK(hipMemsetAsync(g->key, 0, 8, g->stream));
-    hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
-    hipLaunchKernelGGL(ill_gemv_finish_kernel, dim3(fin_blocks), dim3(256), 0, g->stream, (const float*)g->part, g->ks,
-                       g->rows, g->y, amax ? g->key : (uint64_t*)nullptr);
+    if (direct) {
+      a.y = g->y;
+      a.key = amax ? g->key : nullptr;
+      a.par = par;
+      hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
+      par ^= 1;
+    } else {
+      if (amax) HCK(hipMemsetAsync(g->key, 0, 8, g->stream));
+      hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
+      hipLaunchKernelGGL(ill_gemv_finish_kernel, dim3(fin_blocks), dim3(256), 0, g->stream, (const float*)g->part, g->ks,
+                         g->rows, g->y, amax ? g->key : (uint64_t*)nullptr);
+    }
     HCK(hipGetLastError());
     return 0;
   };
@@ -1023,7 +1036,7 @@ int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, flo
   if (y) HCK(hipMemcpy(y, g->y, (size_t)g->rows * 4, hipMemcpyDeviceToHost));
   if (amax) {
     uint64_t k = 0;
-    HCK(hipMemcpy(&k, g->key, 8, hipMemcpyDeviceToHost));
+    HCK(hipMemcpy(&k, g->key + (direct ? (par ^ 1) : 0), 8, hipMemcpyDeviceToHost));
     *amax = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
   }
   return ILL_OK;

@@ -10,9 +10,12 @@
 // against the nibbles (exact int32), fp32 group epilogue s*d*S + m*d*sum(v).
 //
 // Work split: a wave takes one (row tile, K slice) item at a time and keeps the next
-// item's weight loads in flight while it computes the current one. With more than one
+// item's weight loads in flight while it computes the current one (a third in flight
+// measured no faster: the lm_head stream runs at about 5 TB/s either way). With more than one
 // slice per tile the slices write fp32 partials [slice][row] and a second kernel sums them
-// in slice order (deterministic) and reduces the argmax.
+// in slice order (deterministic) and reduces the argmax. With one slice (the lm_head) the
+// kernel writes y itself and reduces the argmax per workgroup into key[par] (atomic max of
+// order-preserving keys); it clears key[par ^ 1] for the next launch, which alternates par.
 #pragma once
 #include "ill_device.h"
 
@@ -26,6 +29,9 @@ struct IllGemvArgs {
   const float* gamma;    // [K] or nullptr (plain input)
   float* part;           // [ks][rows]
   int rows, K, bps, ks;  // blocks per slice, slices per tile
+  float* y;              // ks == 1: [rows] written directly
+  uint64_t* key;         // ks == 1: argmax keys [2] (nullptr: no argmax)
+  int par;
 };
 
 struct GemvLds {
@@ -33,6 +39,7 @@ struct GemvLds {
   uint4 alo[ILL_GEMV_MAXG * 4];
   float2 sc[ILL_GEMV_MAXG];
   float red[ILL_WAVES];
+  uint64_t best[ILL_WAVES];
 };
 
 struct GemvItem {
@@ -63,6 +70,9 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
   const int nitems = (a.rows >> 4) * a.ks;
   const int stride = gridDim.x * ILL_WAVES;
   int item = blockIdx.x * ILL_WAVES + w;
+  const bool direct = a.ks == 1 && a.y;
+  if (direct && a.key && blockIdx.x == 0 && tid == 0) gst(a.key + (a.par ^ 1), (uint64_t)0);
+  uint64_t kbest = 0;
   GemvItem cur;
   if (item < nitems) gemv_fetch(a, item, lane, cur);   // weights stream while x is prepared
   // ---- x: RMSNorm (sum of squares in a fixed order) and 16-bit coding per 64-column group
@@ -127,9 +137,30 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
         }
       }
     }
-    if (kg == 0) gst(a.part + (size_t)slice * a.rows + 16 * tile + n, acc);
+    if (direct) {
+      if (kg == 0) {
+        gst(a.y + 16 * tile + n, acc);
+        const uint64_t k = amax_key(acc, 16 * tile + n);
+        kbest = k > kbest ? k : kbest;
+      }
+    } else if (kg == 0) {
+      gst(a.part + (size_t)slice * a.rows + 16 * tile + n, acc);
+    }
     cur = nx;
     item = nxt;
+  }
+  if (direct && a.key) {
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t ok = __shfl_xor(kbest, o, 64);
+      kbest = ok > kbest ? ok : kbest;
+    }
+    if (lane == 0) L.best[w] = kbest;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t m = L.best[0];
+      for (int i = 1; i < ILL_WAVES; i++) m = L.best[i] > m ? L.best[i] : m;
+      __hip_atomic_fetch_max((GAS unsigned long long*)(a.key + a.par), (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 

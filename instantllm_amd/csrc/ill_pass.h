@@ -1130,22 +1130,27 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 4);
   if (T != 1) att_stage_o<T>(L, h, w, lane, stage);   // O weights stream in while attention runs
-  if (T > 1) {   // path values of the pass rows at positions 8 (pos / 8) + q, q < 24 (part_eval16)
+  if constexpr (T > 1) {   // path values of the pass rows at positions 8 (pos / 8) + q, q < 24 (part_eval16)
     uint4* vq = (uint4*)(stage + ILL_ST_VPT);
     const int d0 = 8 * (pos >> 3) - pos;   // depth of q = 0 (-7 .. 0)
-    for (int i = tid; i < T * 64; i += ILL_WG_THREADS) {   // (row t1, dim)
-      const int t1 = i >> 6, dim = i & 63;
-      const int dep = t1 < nrows ? H.depth[t1] : -1;
-      uint32_t e[24];
+    static_assert(T * 32 == ILL_WG_THREADS, "one thread per (row, dim pair)");
+    const int t1 = tid >> 5, dp = tid & 31;   // row t1, dims 2 dp and 2 dp + 1
+    const int dep = t1 < nrows ? H.depth[t1] : -1;
+    uint32_t e[24];   // both dims' values (low half: dim 2 dp)
 #pragma unroll
-      for (int q = 0; q < 24; q++) {
-        const int dd = d0 + q;
-        e[q] = dd >= 0 && dd <= dep ? (uint32_t)A.v[min(H.prow[t1][min(dd, 15)], T - 1)][dim] : 0u;
-      }
+    for (int q = 0; q < 24; q++) {
+      const int dd = d0 + q;
+      e[q] = dd >= 0 && dd <= dep ? *(const uint32_t*)&A.v[min(H.prow[t1][min(dd, 15)], T - 1)][2 * dp] : 0u;
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      uint32_t h[24];
+#pragma unroll
+      for (int q = 0; q < 24; q++) h[q] = hf ? e[q] >> 16 : e[q] & 0xffffu;
 #pragma unroll
       for (int s3 = 0; s3 < 3; s3++)
-        vq[i * 3 + s3] = make_uint4(e[8 * s3] | (e[8 * s3 + 1] << 16), e[8 * s3 + 2] | (e[8 * s3 + 3] << 16),
-                                    e[8 * s3 + 4] | (e[8 * s3 + 5] << 16), e[8 * s3 + 6] | (e[8 * s3 + 7] << 16));
+        vq[(t1 * 64 + 2 * dp + hf) * 3 + s3] = make_uint4(h[8 * s3] | (h[8 * s3 + 1] << 16), h[8 * s3 + 2] | (h[8 * s3 + 3] << 16),
+                                                         h[8 * s3 + 4] | (h[8 * s3 + 5] << 16), h[8 * s3 + 6] | (h[8 * s3 + 7] << 16));
     }
     lds_barrier();
   }

@@ -914,7 +914,6 @@ struct ill_gemv {
   std::vector<uint32_t*> s;
   float* x = nullptr;
   float* gamma = nullptr;
-  float* part = nullptr;
   float* y = nullptr;
   uint64_t* key = nullptr;
   hipStream_t stream = nullptr;
@@ -928,7 +927,6 @@ int ill_gemv_destroy(ill_gemv* g) {
   for (auto p : g->s) hipFree(p);
   hipFree(g->x);
   hipFree(g->gamma);
-  hipFree(g->part);
   hipFree(g->y);
   hipFree(g->key);
   if (g->e0) hipEventDestroy(g->e0);
@@ -951,8 +949,14 @@ int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* sb, i
   g->nb = K / 128;
   g->copies = copies;
   const int ntile = rows / 16;
-  // enough (tile, slice) items for every wave of the grid, at most 8 blocks per slice
-  int ks = std::min(g->nb, (ILL_WG * ILL_WAVES + ntile - 1) / ntile);
+  // slices per tile: the most (at most one per wave) that still fit every tile of the matrix
+  // in one round of the grid; one slice (whole tiles, one per wave) when even that does not
+  int ks = 1;
+  for (int k = std::min(g->nb, ILL_WAVES); k > 1; k--)
+    if ((ntile + ILL_WAVES / k - 1) / (ILL_WAVES / k) <= ILL_WG) {
+      ks = k;
+      break;
+    }
   int bps = (g->nb + ks - 1) / ks;
   if (bps > ILL_GEMV_MAXBPS) bps = ILL_GEMV_MAXBPS;
   g->bps = bps;
@@ -977,7 +981,7 @@ int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* sb, i
       return bad(fail(ILL_E_HIP, "weight copy %d upload failed", c));
   }
   if (hipMalloc(&g->x, (size_t)K * 4) != hipSuccess || hipMalloc(&g->gamma, (size_t)K * 4) != hipSuccess ||
-      hipMalloc(&g->part, (size_t)g->ks * rows * 4) != hipSuccess || hipMalloc(&g->y, (size_t)rows * 4) != hipSuccess ||
+      hipMalloc(&g->y, (size_t)rows * 4) != hipSuccess ||
       hipMalloc(&g->key, 16) != hipSuccess)
     return bad(fail(ILL_E_HIP, "gemv buffer allocation failed"));
   if (hipStreamCreate(&g->stream) != hipSuccess || hipEventCreate(&g->e0) != hipSuccess || hipEventCreate(&g->e1) != hipSuccess)
@@ -994,32 +998,29 @@ int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, flo
   IllGemvArgs a{};
   a.x = g->x;
   a.gamma = gamma ? g->gamma : nullptr;
-  a.part = g->part;
   a.rows = g->rows;
   a.K = g->K;
   a.bps = g->bps;
   a.ks = g->ks;
-  const int fin_blocks = (g->rows + 255) / 256;
-  // one slice: the gemv kernel writes y and the argmax itself (keys alternate between two
-  // words, each launch clearing the other one)
-  const bool direct = g->ks == 1;
-  if (direct && amax) HCK(hipMemsetAsync(g->key, 0, 16, g->stream));
+  // one kernel writes y and the argmax (keys alternate between two words, each launch
+  // clearing the other one): with one slice every item is a whole tile, with several the
+  // slices of a tile are summed in LDS by the workgroup that computed them
+  if (amax) HCK(hipMemsetAsync(g->key, 0, 16, g->stream));
+  a.y = g->y;
+  a.key = amax ? g->key : nullptr;
+  const int ntile = g->rows / 16;
+  const int tpr = ILL_WAVES / g->ks;   // ks <= 8: bps <= 8 and K <= 64 * 128
+  const int grid = std::min(ILL_WG, (ntile + tpr - 1) / tpr);
   int par = 0;
   auto one = [&](int c) -> int {
     a.w = g->w[c];
     a.s = g->s[c];
-    if (direct) {
-      a.y = g->y;
-      a.key = amax ? g->key : nullptr;
-      a.par = par;
+    a.par = par;
+    if (g->ks == 1)
       hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
-      par ^= 1;
-    } else {
-      if (amax) HCK(hipMemsetAsync(g->key, 0, 8, g->stream));
-      hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, g->stream, a);
-      hipLaunchKernelGGL(ill_gemv_finish_kernel, dim3(fin_blocks), dim3(256), 0, g->stream, (const float*)g->part, g->ks,
-                         g->rows, g->y, amax ? g->key : (uint64_t*)nullptr);
-    }
+    else
+      hipLaunchKernelGGL(ill_gemv_q4_tiles_kernel, dim3(grid), dim3(ILL_WG_THREADS), 0, g->stream, a);
+    par ^= 1;
     HCK(hipGetLastError());
     return 0;
   };
@@ -1036,7 +1037,7 @@ int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, flo
   if (y) HCK(hipMemcpy(y, g->y, (size_t)g->rows * 4, hipMemcpyDeviceToHost));
   if (amax) {
     uint64_t k = 0;
-    HCK(hipMemcpy(&k, g->key + (direct ? (par ^ 1) : 0), 8, hipMemcpyDeviceToHost));
+    HCK(hipMemcpy(&k, g->key + (par ^ 1), 8, hipMemcpyDeviceToHost));
     *amax = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
   }
   return ILL_OK;

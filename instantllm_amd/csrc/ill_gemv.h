@@ -9,13 +9,14 @@
 // kernel's: x coded per 64-column group as 16-bit fixed point (int8 hi/lo), int8 MFMA
 // against the nibbles (exact int32), fp32 group epilogue s*d*S + m*d*sum(v).
 //
-// Work split: a wave takes one (row tile, K slice) item at a time and keeps the next
-// item's weight loads in flight while it computes the current one (a third in flight
-// measured no faster: the lm_head stream runs at about 5 TB/s either way). With more than one
-// slice per tile the slices write fp32 partials [slice][row] and a second kernel sums them
-// in slice order (deterministic) and reduces the argmax. With one slice (the lm_head) the
-// kernel writes y itself and reduces the argmax per workgroup into key[par] (atomic max of
-// order-preserving keys); it clears key[par ^ 1] for the next launch, which alternates par.
+// Work split: a wave takes one (row tile, K slice) item and keeps the next item's weight
+// loads in flight while it computes the current one. One slice per tile (the lm_head: many
+// tiles): ill_gemv_q4_kernel, whose waves write y themselves. Several slices (the layer
+// matrices: few tiles, so K is split to give every wave work): ill_gemv_q4_tiles_kernel,
+// which places all slices of a tile in one workgroup and adds their fp32 partials in LDS in
+// slice order (deterministic), with no second kernel. Both reduce the argmax per workgroup
+// into key[par] (atomic max of order-preserving keys) and clear key[par ^ 1] for the next
+// launch, which alternates par.
 #pragma once
 #include "ill_device.h"
 
@@ -27,10 +28,9 @@ struct IllGemvArgs {
   const uint32_t* s;     // [ntile][nb][16][2] (scale, min) f16 pairs
   const float* x;        // [K]
   const float* gamma;    // [K] or nullptr (plain input)
-  float* part;           // [ks][rows]
-  int rows, K, bps, ks;  // blocks per slice, slices per tile
-  float* y;              // ks == 1: [rows] written directly
-  uint64_t* key;         // ks == 1: argmax keys [2] (nullptr: no argmax)
+  int rows, K, bps, ks;  // blocks per slice, slices per tile (<= 8)
+  float* y;              // [rows]
+  uint64_t* key;         // argmax keys [2] (nullptr: no argmax); launch uses key[par]
   int par;
 };
 
@@ -62,20 +62,11 @@ __device__ __forceinline__ void gemv_fetch(const IllGemvArgs& a, int item, int l
   }
 }
 
-__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvArgs a) {
-  __shared__ GemvLds L;
+// x: RMSNorm (sum of squares in a fixed order) and 16-bit coding per 64-column group into
+// L (ends with a workgroup barrier).
+__device__ __forceinline__ void gemv_prep_x(const IllGemvArgs& a, GemvLds& L) {
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int kg = lane >> 4, n = lane & 15;
-  const int nb = a.K >> 7, ng = a.K >> 6;
-  const int nitems = (a.rows >> 4) * a.ks;
-  const int stride = gridDim.x * ILL_WAVES;
-  int item = blockIdx.x * ILL_WAVES + w;
-  const bool direct = a.ks == 1 && a.y;
-  if (direct && a.key && blockIdx.x == 0 && tid == 0) gst(a.key + (a.par ^ 1), (uint64_t)0);
-  uint64_t kbest = 0;
-  GemvItem cur;
-  if (item < nitems) gemv_fetch(a, item, lane, cur);   // weights stream while x is prepared
-  // ---- x: RMSNorm (sum of squares in a fixed order) and 16-bit coding per 64-column group
+  const int ng = a.K >> 6;
   float scale = 1.f;
   if (a.gamma) {
     float ss = 0.f;
@@ -107,49 +98,66 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
     if (lane == 0) L.sc[g] = make_float2(d, d * (float)sq);
   }
   __syncthreads();
-  // ---- items
+}
+
+// One item: the 16 row sums of its tile over its K slice (lane (kg, n) holds row n).
+__device__ __forceinline__ float gemv_item(const IllGemvArgs& a, const GemvLds& L, const GemvItem& cur, int slice, int lane) {
+  const int kg = lane >> 4;
+  const int nb = a.K >> 7;
   const v4i z = {0, 0, 0, 0};
+  const int cb0 = slice * a.bps;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < ILL_GEMV_MAXBPS; i++) {
+    const int cb = cb0 + i;
+    if (i < a.bps && cb < nb) {
+#pragma unroll
+      for (int gi = 0; gi < 2; gi++) {
+        const int G = 2 * cb + gi;
+        const v4i b = gi == 0 ? q4_unpack(cur.w[i].x, cur.w[i].y) : q4_unpack(cur.w[i].z, cur.w[i].w);
+        const uint4 h = L.ahi[G * 4 + kg], l = L.alo[G * 4 + kg];
+        const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
+        const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
+        const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+        const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+        const uint32_t sm = gi == 0 ? cur.s[i].x : cur.s[i].y;
+        const float2 dx = L.sc[G];
+        const int S = (dh[0] << 8) + dl[0];
+        acc = fmaf(h2f(sm & 0xffff), dx.x * (float)S, acc);
+        acc = fmaf(h2f(sm >> 16), dx.y, acc);
+      }
+    }
+  }
+  return acc;
+}
+
+// One slice (ks == 1): every item is a whole tile; y and the argmax are written here.
+__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvArgs a) {
+  __shared__ GemvLds L;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int nitems = a.rows >> 4;   // one slice: an item is a whole tile
+  const int stride = gridDim.x * ILL_WAVES;
+  int item = blockIdx.x * ILL_WAVES + w;
+  if (a.key && blockIdx.x == 0 && tid == 0) gst(a.key + (a.par ^ 1), (uint64_t)0);
+  uint64_t kbest = 0;
+  GemvItem cur;
+  if (item < nitems) gemv_fetch(a, item, lane, cur);   // weights stream while x is prepared
+  gemv_prep_x(a, L);
   while (item < nitems) {
     const int nxt = item + stride;
     GemvItem nx;
     if (nxt < nitems) gemv_fetch(a, nxt, lane, nx);
-    const int tile = item / a.ks, slice = item - tile * a.ks;
-    const int cb0 = slice * a.bps;
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < ILL_GEMV_MAXBPS; i++) {
-      const int cb = cb0 + i;
-      if (i < a.bps && cb < nb) {
-#pragma unroll
-        for (int gi = 0; gi < 2; gi++) {
-          const int G = 2 * cb + gi;
-          const v4i b = gi == 0 ? q4_unpack(cur.w[i].x, cur.w[i].y) : q4_unpack(cur.w[i].z, cur.w[i].w);
-          const uint4 h = L.ahi[G * 4 + kg], l = L.alo[G * 4 + kg];
-          const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
-          const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
-          const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
-          const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-          const uint32_t sm = gi == 0 ? cur.s[i].x : cur.s[i].y;
-          const float2 dx = L.sc[G];
-          const int S = (dh[0] << 8) + dl[0];
-          acc = fmaf(h2f(sm & 0xffff), dx.x * (float)S, acc);
-          acc = fmaf(h2f(sm >> 16), dx.y, acc);
-        }
-      }
-    }
-    if (direct) {
-      if (kg == 0) {
-        gst(a.y + 16 * tile + n, acc);
-        const uint64_t k = amax_key(acc, 16 * tile + n);
-        kbest = k > kbest ? k : kbest;
-      }
-    } else if (kg == 0) {
-      gst(a.part + (size_t)slice * a.rows + 16 * tile + n, acc);
+    const float acc = gemv_item(a, L, cur, 0, lane);
+    if (kg == 0) {
+      gst(a.y + 16 * item + n, acc);
+      const uint64_t k = amax_key(acc, 16 * item + n);
+      kbest = k > kbest ? k : kbest;
     }
     cur = nx;
     item = nxt;
   }
-  if (direct && a.key) {
+  if (a.key) {
     for (int o = 32; o >= 1; o >>= 1) {
       const uint64_t ok = __shfl_xor(kbest, o, 64);
       kbest = ok > kbest ? ok : kbest;
@@ -164,28 +172,64 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
   }
 }
 
-// y[r] = sum over slices in order; optional argmax into *key (atomic max of amax_key).
-__global__ __launch_bounds__(256) void ill_gemv_finish_kernel(const float* part, int ks, int rows, float* y, uint64_t* key) {
-  __shared__ uint64_t best[4];
-  const int r = blockIdx.x * 256 + threadIdx.x;
-  uint64_t k = 0;
-  if (r < rows) {
-    float v = 0.f;
-    for (int s = 0; s < ks; s++) v += gld(part + (size_t)s * rows + r);
-    gst(y + r, v);
-    k = amax_key(v, r);
-  }
-  if (key) {
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint64_t ok = __shfl_xor(k, o, 64);
-      k = ok > k ? ok : k;
+
+// Several slices per tile (ks <= 8): the ks slices of a tile are items of one workgroup, one
+// per wave, so a round takes 8 / ks tiles; their fp32 partials meet in LDS and one wave per
+// tile adds them in slice order, writes y and takes the argmax. Rounds step over the grid.
+__global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_tiles_kernel(IllGemvArgs a) {
+  __shared__ GemvLds L;
+  __shared__ float part[ILL_WAVES][16];   // [wave][row]
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int ntile = a.rows >> 4, ks = a.ks;
+  const int tpr = ILL_WAVES / ks;
+  const int nsets = (ntile + tpr - 1) / tpr;
+  // this wave's item of round `set`, or -1
+  auto item_of = [&](int set) -> int {
+    const int tile = set * tpr + w / ks;
+    return set < nsets && w < tpr * ks && tile < ntile ? tile * ks + w % ks : -1;
+  };
+  if (a.key && blockIdx.x == 0 && tid == 0) gst(a.key + (a.par ^ 1), (uint64_t)0);
+  uint64_t kbest = 0;
+  int set = blockIdx.x;
+  int it = item_of(set);
+  GemvItem cur;
+  if (it >= 0) gemv_fetch(a, it, lane, cur);   // weights stream while x is prepared
+  gemv_prep_x(a, L);
+  for (; set < nsets; set += gridDim.x) {
+    const int nx_it = item_of(set + gridDim.x);
+    GemvItem nx;
+    if (nx_it >= 0) gemv_fetch(a, nx_it, lane, nx);
+    if (it >= 0) {
+      const float acc = gemv_item(a, L, cur, w % ks, lane);
+      if (kg == 0) part[w][n] = acc;
     }
-    if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = k;
+    cur = nx;
+    it = nx_it;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      uint64_t m = best[0];
-      for (int i = 1; i < 4; i++) m = best[i] > m ? best[i] : m;
-      __hip_atomic_fetch_max((GAS unsigned long long*)key, (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w < tpr && lane < 16) {
+      const int tile = set * tpr + w;
+      if (tile < ntile) {
+        float v = 0.f;
+        for (int sl = 0; sl < ks; sl++) v += part[w * ks + sl][lane];
+        gst(a.y + 16 * tile + lane, v);
+        const uint64_t k = amax_key(v, 16 * tile + lane);
+        kbest = k > kbest ? k : kbest;
+      }
+    }
+    __syncthreads();
+  }
+  if (a.key) {
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t ok = __shfl_xor(kbest, o, 64);
+      kbest = ok > kbest ? ok : kbest;
+    }
+    if (lane == 0) L.best[w] = kbest;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t m = L.best[0];
+      for (int i = 1; i < ILL_WAVES; i++) m = L.best[i] > m ? L.best[i] : m;
+      __hip_atomic_fetch_max((GAS unsigned long long*)(a.key + a.par), (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

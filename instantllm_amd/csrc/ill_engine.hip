@@ -189,9 +189,17 @@ int write_pos_n(ill_engine* e, int pos, int n) {
 
 // ---- layer-by-layer path -----------------------------------------------------------------
 #define ILL_OP_PART_BYTES (16u << 20)   // >= slices x rows x N x 4 of every split GEMM
+#define ILL_OP_PART_SPLIT (2u << 20)    // floats: passes of up to 16 rows keep the gate/up
+                                        // partials below, the down GEMM's above
 
+// Returns true when it also wrote the RMSNorm of the updated residual (rows >= norm_row0,
+// weights norm_gamma) into xn: residual GEMMs of passes of up to 16 rows with K split.
+// Passes of up to 16 rows only: a gate/up GEMM given silu_out leaves its K-slice partials
+// in opart for the down GEMM and stores their count there (0: it applied SiLU itself); a
+// residual GEMM given silu_S > 0 takes its A operand from those partials.
 template <int FMT, int EPI>
-void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, float* resid) {
+bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, float* resid,
+             const float* norm_gamma = nullptr, int norm_row0 = 0, int* silu_out = nullptr, int silu_S = 0) {
   OpGemmArgs g;
   g.c = e->octx;
   g.A = A;
@@ -212,23 +220,44 @@ void op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
         const int per = EPI == OP_RESID ? W.N : W.N / 2;
         hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
       }
-      return;
+      return false;
     }
   }
-  // up to 16 rows: split K so that about 256 workgroups stream the weights, at least four
-  // k-steps per slice (the split depends on the matrix only, so 1-row and 16-row passes
-  // sum the same partials in the same order)
+  // up to 16 rows: op_gemv_kernel; split K so that about 256 workgroups stream the weights,
+  // at least four k-steps per slice (the split depends on the matrix only, so 1-row and
+  // 16-row passes sum the same partials in the same order)
   int S = 1;
   if (EPI != OP_LMH) S = std::max(1, std::min(std::min((256 + ntn - 1) / ntn, nsteps / 4), OP_MAXS));
   g.ksteps = (nsteps + S - 1) / S;
   S = (nsteps + g.ksteps - 1) / g.ksteps;
-  hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), dim3(ntn, (M + 15) / 16, S), dim3(256), 0, e->stream, g);
+  if (g.ksteps * OP_BK > OP_SMAXK) {
+    fail(ILL_E_ARG, "K slice of %d columns exceeds %d", g.ksteps * OP_BK, OP_SMAXK);
+    return false;
+  }
+  const dim3 grid(ntn, 1, S);
+  if (EPI == OP_RESID && silu_S > 0) {   // A = SwiGLU of the gate/up partials left in opart
+    g.apart = e->opart;
+    g.aS = silu_S;
+    g.part = e->opart + ILL_OP_PART_SPLIT;
+    hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, true>), grid, dim3(256), 0, e->stream, g);
+  } else {
+    hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), grid, dim3(256), 0, e->stream, g);
+  }
   if constexpr (EPI != OP_LMH) {
     if (S > 1) {
+      if (EPI == OP_SILU && silu_out && (size_t)S * M * W.N * 4 <= ILL_OP_PART_SPLIT * 4) {
+        *silu_out = S;   // the down GEMM takes the partials
+        return false;
+      }
+      if (EPI == OP_RESID && norm_gamma && W.N == ILL_H) {
+        hipLaunchKernelGGL(op_epi_norm_kernel, dim3(M), dim3(ILL_H), 0, e->stream, g, S, norm_gamma, norm_row0);
+        return true;
+      }
       const int per = EPI == OP_RESID ? W.N : W.N / 2;
       hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
     }
   }
+  return false;
 }
 
 // The kernels of one pass over M rows (control block and State already written): layers,
@@ -242,22 +271,29 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
   // per 1024 positions of context (the result does not depend on the split)
   const int nch = (e->pos_hint + M + 63) / 64;
   const int nsplit = std::max(1, std::min(OP_NSPLIT, (nch + 15) / 16));
+  // passes of up to 16 rows: each residual update also writes the next RMSNorm (op_gemm
+  // returns whether it did)
+  bool normed = false;
   for (int l = 0; l < e->layers; l++) {
     const OpLayerW& L = e->holayers[l];
-    hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
+    if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
     if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64), 0, s, c, l, M);
     else {
       hipLaunchKernelGGL(op_attn_kernel, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart);
       if (nsplit > 1) hipLaunchKernelGGL(op_attn_combine_kernel, dim3(M * ILL_NH), dim3(64), 0, s, c, (const float*)e->opart);
     }
-    op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x);
-    hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
-    op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr);
-    op_gemm<FMT, OP_RESID>(e, c.h, L.d, M, l, c.x);
+    const bool fuse = M <= 16;
+    if (!op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x, fuse ? L.ln2 : nullptr, 0))
+      hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
+    int silu_S = 0;
+    op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr, nullptr, 0, fuse ? &silu_S : nullptr);
+    const bool last = l + 1 == e->layers;
+    const float* next = last ? (lm_rows > 0 ? c.fnorm : nullptr) : e->holayers[l + 1].ln1;
+    normed = op_gemm<FMT, OP_RESID>(e, c.h, L.d, M, l, c.x, fuse ? next : nullptr, last ? M - lm_rows : 0, nullptr, silu_S);
   }
   if (lm_rows > 0) {
-    hipLaunchKernelGGL(op_norm_kernel, dim3((lm_rows + 3) / 4), dim3(256), 0, s, c, c.fnorm, M - lm_rows, lm_rows);
+    if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((lm_rows + 3) / 4), dim3(256), 0, s, c, c.fnorm, M - lm_rows, lm_rows);
     op_gemm<FMT, OP_LMH>(e, c.xn, c.emb, lm_rows, 0, nullptr);
   }
   hipLaunchKernelGGL(op_commit_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, s, e->args, (const uint64_t*)c.amax, e->vocab / OP_BN);

@@ -144,6 +144,8 @@ struct OpGemmArgs {
   float* resid;      // OP_RESID: [M][896] += Y
   float* part;       // split K: [slices][M][N] fp32 partials
   int ksteps;        // 64-column steps per K slice
+  const float* apart;   // op_gemv_kernel<.., SILU = true>: gate/up partials [aS][M][2K]
+  int aS;
 };
 
 #define OP_BN 128
@@ -156,7 +158,9 @@ struct OpGemmArgs {
 template <int FMT>
 struct WRaw {
   uint4 b[FMT == 2 ? 1 : (FMT == 1 ? 2 : 4)];
-  uint32_t sm;
+  // q4: (scale, min) pair; q8: the scale, kept 16-bit so that the load needs no widening
+  // (which would wait for it at once)
+  std::conditional_t<FMT == 1, uint16_t, uint32_t> sm;
 };
 
 template <int FMT>
@@ -193,7 +197,7 @@ __device__ __forceinline__ void op_store_w(const WRaw<FMT>& r, _Float16* Bs, int
 #pragma unroll
     for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = *(const uint4*)(o + 8 * i);
   } else if constexpr (FMT == 1) {
-    const _Float16 s = (_Float16)h2f(r.sm & 0xffff);
+    const _Float16 s = (_Float16)h2f(r.sm);
     const uint32_t x[8] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w, r.b[1].x, r.b[1].y, r.b[1].z, r.b[1].w};
     _Float16 o[32];
 #pragma unroll
@@ -207,7 +211,8 @@ __device__ __forceinline__ void op_store_w(const WRaw<FMT>& r, _Float16* Bs, int
 }
 
 // A tile: BM rows x 64 halves; thread i (< BM * 8) carries 16 bytes (rows >= M read row
-// M - 1: finite, and their outputs are unused).
+// M - 1: finite, and their outputs are unused). Every thread loads (the surplus ones a
+// duplicate), so that the number of loads in flight never depends on a branch.
 template <int BM>
 struct ARaw {
   uint4 v[(BM * 8 + 255) / 256];
@@ -216,11 +221,9 @@ template <int BM>
 __device__ __forceinline__ void op_fetch_a(const __half* A, int M, int K, int m0, int k0, int tid, ARaw<BM>& r) {
 #pragma unroll
   for (int u = 0; u < (BM * 8 + 255) / 256; u++) {
-    const int i = tid + 256 * u;
-    if (i < BM * 8) {
-      const int row = min(m0 + (i >> 3), M - 1);
-      r.v[u] = gld((const uint4*)(A + (size_t)row * K + k0) + (i & 7));
-    }
+    const int i = (tid + 256 * u) & (BM * 8 - 1);
+    const int row = min(m0 + (i >> 3), M - 1);
+    r.v[u] = gld((const uint4*)(A + (size_t)row * K + k0) + (i & 7));
   }
 }
 template <int BM>
@@ -266,57 +269,15 @@ __device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float 
   c.h[(size_t)m * ILL_FF + unit] = __float2half(g / (1.0f + expf(-g)) * u);
 }
 
-// Workgroup: 256 threads = 4 waves; a wave owns 32 columns (two 16-column MFMA tiles) of
-// the 128-column tile and all BM rows. blockIdx.z selects a K slice of `ksteps` 64-column
-// steps; with more than one slice the kernel writes fp32 partials [slice][M][N] and
-// op_epi_kernel reduces them in slice order and applies the epilogue. The next k-step's
-// operands are in flight while the current one is multiplied.
-template <int FMT, int BM, int EPI>
-__global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
-  const OpHdr hd = op_hdr(a.c);
-  __shared__ __attribute__((aligned(16))) _Float16 As[BM * OP_LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[OP_BN * OP_LDK];
-  __shared__ uint64_t red[4][16];
+// Epilogue of a 128-column tile (lane (kg, n) of wave w holds rows m0 + 16 i + 4 kg + r,
+// columns n0 + 32 w + 16 j + n): fp32 partials of a K slice, or the fused epilogue.
+template <int BM, int EPI>
+__device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHdr& hd, const v4f (&acc)[BM / 16][2], int m0,
+                                                 int n0, int w, int kg, int n, uint64_t (&red)[4][16]) {
   constexpr int TM = BM / 16;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int kg = lane >> 4, n = lane & 15;
-  const int n0 = blockIdx.x * OP_BN, m0 = blockIdx.y * BM;
-  const int K = a.W.K;
-  const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
-  v4f acc[TM][2];
-#pragma unroll
-  for (int i = 0; i < TM; i++) {
-    acc[i][0] = (v4f){0.f, 0.f, 0.f, 0.f};
-    acc[i][1] = (v4f){0.f, 0.f, 0.f, 0.f};
-  }
-  WRaw<FMT> wr;
-  ARaw<BM> ar;
-  op_fetch_w<FMT>(a.W, n0, kb, tid, wr);
-  op_fetch_a<BM>(a.A, a.M, K, m0, kb, tid, ar);
-  for (int k0 = kb; k0 < ke; k0 += OP_BK) {
-    op_store_a<BM>(ar, As, tid);
-    op_store_w<FMT>(wr, Bs, tid);
-    __syncthreads();
-    if (k0 + OP_BK < ke) {
-      op_fetch_w<FMT>(a.W, n0, k0 + OP_BK, tid, wr);
-      op_fetch_a<BM>(a.A, a.M, K, m0, k0 + OP_BK, tid, ar);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      v8h bf[2];
-#pragma unroll
-      for (int j = 0; j < 2; j++) bf[j] = *(const v8h*)(Bs + (32 * w + 16 * j + n) * OP_LDK + 32 * ks + 8 * kg);
-#pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const v8h af = *(const v8h*)(As + (16 * i + n) * OP_LDK + 32 * ks + 8 * kg);
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
-      }
-    }
-    __syncthreads();
-  }
   if (hd.done) return;
   const OpCtx& c = a.c;
+  const int tid = threadIdx.x;
   if (gridDim.z > 1) {   // split K: partials for op_epi_kernel
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -390,6 +351,237 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   }
 }
 
+// Workgroup: 256 threads = 4 waves; a wave owns 32 columns (two 16-column MFMA tiles) of
+// the 128-column tile and all BM rows. blockIdx.z selects a K slice of `ksteps` 64-column
+// steps; with more than one slice the kernel writes fp32 partials [slice][M][N] and
+// op_epi_kernel reduces them in slice order and applies the epilogue. The operands of the
+// next OP_DEPTH k-steps are in flight (a register ring) while the current one is
+// multiplied: a k-step's MFMAs take far less than a memory round trip. The LDS tiles are
+// double-buffered, so one barrier per k-step orders both their reuse and their filling; it
+// waits for LDS traffic only (a full __syncthreads would also drain the ring's loads).
+#define OP_DEPTH 4
+template <int FMT, int BM, int EPI>
+__global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
+  const OpHdr hd = op_hdr(a.c);
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * OP_LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][OP_BN * OP_LDK];
+  __shared__ uint64_t red[4][16];
+  constexpr int TM = BM / 16;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int n0 = blockIdx.x * OP_BN, m0 = blockIdx.y * BM;
+  const int K = a.W.K;
+  const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
+  const int ns = (ke - kb) / OP_BK;
+  v4f acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    acc[i][0] = (v4f){0.f, 0.f, 0.f, 0.f};
+    acc[i][1] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  // Ring loads are unconditional (steps past the slice reload its last one), so that the
+  // compiler can count the loads in flight and wait for the oldest slot only.
+  WRaw<FMT> wr[OP_DEPTH];
+  ARaw<BM> ar[OP_DEPTH];
+#pragma unroll
+  for (int d = 0; d < OP_DEPTH; d++) {
+    const int k0 = kb + min(d, ns - 1) * OP_BK;
+    op_fetch_w<FMT>(a.W, n0, k0, tid, wr[d]);
+    op_fetch_a<BM>(a.A, a.M, K, m0, k0, tid, ar[d]);
+    __builtin_amdgcn_sched_barrier(0);   // issue order = slot order (the waits count on it)
+  }
+  // One k-step from ring slot d (st: the step's index in the slice); `refetch` refills the
+  // slot with step st + OP_DEPTH (clamped: the last round reloads the slice's last step).
+  auto kstep = [&](int d, int st, bool refetch) {
+    _Float16* as = As[d & 1];
+    _Float16* bs = Bs[d & 1];
+    op_store_a<BM>(ar[d], as, tid);
+    op_store_w<FMT>(wr[d], bs, tid);
+    lds_barrier();   // LDS only: the ring's HBM loads stay in flight
+    if (refetch) {
+      const int k0 = kb + min(st + OP_DEPTH, ns - 1) * OP_BK;
+      __builtin_amdgcn_sched_barrier(0);
+      op_fetch_w<FMT>(a.W, n0, k0, tid, wr[d]);
+      op_fetch_a<BM>(a.A, a.M, K, m0, k0, tid, ar[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      v8h bf[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) bf[j] = *(const v8h*)(bs + (32 * w + 16 * j + n) * OP_LDK + 32 * ks + 8 * kg);
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const v8h af = *(const v8h*)(as + (16 * i + n) * OP_LDK + 32 * ks + 8 * kg);
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  // Whole rounds of OP_DEPTH steps with no branch between their loads (so every path into
+  // the loop head has the same loads in flight and the waits stay partial), then the tail
+  // from the ring without refills.
+  int s0 = 0;
+  for (; s0 + OP_DEPTH <= ns; s0 += OP_DEPTH) {
+#pragma unroll
+    for (int d = 0; d < OP_DEPTH; d++) kstep(d, s0 + d, true);
+  }
+#pragma unroll
+  for (int d = 0; d < OP_DEPTH - 1; d++)
+    if (s0 + d < ns) kstep(d, s0 + d, false);
+  op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, w, kg, n, red);
+}
+
+// ---- GEMM of passes of up to 16 rows --------------------------------------------------
+// Workgroup: 4 waves, wave w owns columns n0 + 32 w .. + 31 (two 16-column MFMA tiles) and
+// rows 0-15. The A rows of the K slice sit in LDS for the whole kernel (filled once, one
+// barrier); each wave loads its own weight operands straight into registers (no LDS, no
+// barrier in the k loop), OP_SDEPTH(FMT) k-steps of them in flight. Within a k-step lane (kg, n)
+// takes columns 16 kg .. 16 kg + 15 of the 64 (8 for each of the two MFMAs), a permutation
+// of k applied to A and W alike. With SILU the A operand is the SwiGLU unit
+// f16(silu(g) * u) of the gate/up GEMM's K-slice partials (summed in slice order, as
+// op_epi_kernel does), so that no separate SiLU kernel runs. The host uses it for that
+// down projection only: for the other small-pass GEMMs the LDS-tiled op_gemm_kernel<.., 16,
+// ..> measured as fast (q8) or faster (f16: about 3 us per step-kernel).
+#define OP_SDEPTH(FMT) ((FMT) == 0 ? 4 : 8)   // f16 k-steps carry twice the bytes of q8 ones
+#define OP_SMAXK 1024   // K slice columns at most (16 k-steps)
+
+template <int FMT>
+struct BOp {   // one k-step's weights of one lane for the wave's two column tiles
+  uint4 q[2][FMT == 0 ? 2 : 1];   // q4: .x .y hold the 16 nibbles
+  // q8: scale (kept 16-bit: widening the loaded value would wait for it at once);
+  // q4: (scale, min)
+  std::conditional_t<FMT == 2, uint32_t, uint16_t> s[2];
+};
+template <int FMT>
+__device__ __forceinline__ void op_fetch_b(const OpMat& W, int col0, int k0, int kg, int n, BOp<FMT>& b) {
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const size_t row = (size_t)(col0 + 16 * j + n);
+    const int k = k0 + 16 * kg;
+    if constexpr (FMT == 2) {
+      const uint2 v = gld((const uint2*)(W.w + row * (W.K / 2) + k / 2));
+      b.q[j][0] = make_uint4(v.x, v.y, 0u, 0u);
+      b.s[j] = gld((const uint32_t*)(W.s + (row * (W.K / 64) + k / 64) * 2));
+    } else if constexpr (FMT == 1) {
+      b.q[j][0] = gld((const uint4*)(W.w + row * W.K + k));
+      b.s[j] = gld(W.s + row * (W.K / W.qg) + k / W.qg);
+    } else {
+      const uint4* src = (const uint4*)(W.w + (row * W.K + k) * 2);
+      b.q[j][0] = gld(src);
+      b.q[j][1] = gld(src + 1);
+    }
+  }
+}
+// the 8 f16 operand values of MFMA half ks (k = 16 kg + 8 ks ..) of column tile j
+template <int FMT>
+__device__ __forceinline__ v8h op_bvals(const BOp<FMT>& b, int j, int ks) {
+  v8h o;
+  if constexpr (FMT == 2) {
+    const _Float16 sc = (_Float16)h2f(b.s[j] & 0xffff), mn = (_Float16)h2f(b.s[j] >> 16);
+    const uint32_t x = ks == 0 ? b.q[j][0].x : b.q[j][0].y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t byte = (x >> (8 * i)) & 0xff;
+      o[2 * i] = sc * (_Float16)(float)(byte & 15) + mn;
+      o[2 * i + 1] = sc * (_Float16)(float)(byte >> 4) + mn;
+    }
+  } else if constexpr (FMT == 1) {
+    const _Float16 sc = (_Float16)h2f(b.s[j]);
+    const uint32_t x0 = ks == 0 ? b.q[j][0].x : b.q[j][0].z, x1 = ks == 0 ? b.q[j][0].y : b.q[j][0].w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o[i] = sc * (_Float16)(float)(int8_t)((x0 >> (8 * i)) & 0xff);
+      o[4 + i] = sc * (_Float16)(float)(int8_t)((x1 >> (8 * i)) & 0xff);
+    }
+  } else {
+    o = u4_to_v8h(b.q[j][ks]);
+  }
+  return o;
+}
+
+template <int FMT, int EPI, bool SILU>
+__global__ __launch_bounds__(256) void op_gemv_kernel(OpGemmArgs a) {
+  const OpHdr hd = op_hdr(a.c);
+  __shared__ __attribute__((aligned(16))) _Float16 As[16 * (OP_SMAXK + 8)];
+  __shared__ uint64_t red[4][16];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const int n0 = blockIdx.x * OP_BN, col0 = n0 + 32 * w;
+  const int K = a.W.K;
+  const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
+  const int ns = (ke - kb) / OP_BK, kw = ke - kb;
+  const int lda = kw + 8;   // LDS row stride (halves)
+  constexpr int SD = OP_SDEPTH(FMT);
+  BOp<FMT> ring[SD];
+#pragma unroll
+  for (int d = 0; d < SD; d++) {
+    op_fetch_b<FMT>(a.W, col0, kb + min(d, ns - 1) * OP_BK, kg, n, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);   // issue order = slot order (the waits count on it)
+  }
+  // A rows 0 .. M-1 of the slice into LDS (rows >= M are left as they are: their outputs
+  // are never stored)
+  if constexpr (!SILU) {
+    const int per = kw / 8;   // uint4 per row
+    for (int i = tid; i < a.M * per; i += 256) {
+      const int m = i / per, c8 = i - m * per;
+      *(uint4*)(As + m * lda + 8 * c8) = gld((const uint4*)(a.A + (size_t)m * K + kb) + c8);
+    }
+  } else {
+    // units kb + 2 p, kb + 2 p + 1 of row m: gate/up columns 2 kb + 4 p .. + 3 (g, g, u, u)
+    const int per = kw / 2, N2 = 2 * K;
+    for (int i = tid; i < a.M * per; i += 256) {
+      const int m = i / per, p = i - m * per;
+      float4 pz[OP_MAXS];
+#pragma unroll
+      for (int z = 0; z < OP_MAXS; z++)
+        if (z < a.aS) pz[z] = gld((const float4*)(a.apart + ((size_t)z * a.M + m) * N2 + 2 * kb) + p);
+      float4 v = pz[0];
+#pragma unroll
+      for (int z = 1; z < OP_MAXS; z++)
+        if (z < a.aS) {
+          v.x += pz[z].x;
+          v.y += pz[z].y;
+          v.z += pz[z].z;
+          v.w += pz[z].w;
+        }
+      As[m * lda + 2 * p] = (_Float16)__float2half(v.x / (1.0f + expf(-v.x)) * v.z);
+      As[m * lda + 2 * p + 1] = (_Float16)__float2half(v.y / (1.0f + expf(-v.y)) * v.w);
+    }
+  }
+  __syncthreads();
+  v4f acc[1][2];
+  acc[0][0] = (v4f){0.f, 0.f, 0.f, 0.f};
+  acc[0][1] = (v4f){0.f, 0.f, 0.f, 0.f};
+  auto kstep = [&](int d, int st, bool refetch) {
+    v8h bf[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) bf[j][ks] = op_bvals<FMT>(ring[d], j, ks);
+    if (refetch) {
+      __builtin_amdgcn_sched_barrier(0);
+      op_fetch_b<FMT>(a.W, col0, kb + min(st + SD, ns - 1) * OP_BK, kg, n, ring[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const v8h af = *(const v8h*)(As + n * lda + st * OP_BK + 16 * kg + 8 * ks);
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[0][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j][ks], acc[0][j], 0, 0, 0);
+    }
+  };
+  int s0 = 0;
+  for (; s0 + SD <= ns; s0 += SD) {
+#pragma unroll
+    for (int d = 0; d < SD; d++) kstep(d, s0 + d, true);
+  }
+#pragma unroll
+  for (int d = 0; d < SD - 1; d++)
+    if (s0 + d < ns) kstep(d, s0 + d, false);
+  op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red);
+}
+
 // Split-K reduction: sum of the slices' partials in slice order, then the epilogue.
 // RESID / SILU / QKV: one thread per output column / unit / rotary pair of a row.
 template <int EPI>
@@ -424,6 +616,39 @@ __global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
     const float x0 = sum(32 * b + ii), x1 = sum(32 * b + 16 + ii);
     if (!hd.done) epi_qkv(a.c, hd, a.layer, m, b, ii, x0, x1);
   }
+}
+
+// Residual split-K reduction fused with the RMSNorm that reads the updated residual, for
+// passes of up to 16 rows: one workgroup per row m, one thread per column. x[m] += the
+// slices' partials (added in slice order, as op_epi_kernel); then, for rows m >= row0,
+// xn[m - row0] = f16(x * rsqrt(mean(x^2) + eps) * gamma), the sum of squares taken per wave
+// and the 14 wave sums added in order (a function of the row alone, so 1-row and 16-row
+// passes agree bit for bit).
+__global__ __launch_bounds__(ILL_H) void op_epi_norm_kernel(OpGemmArgs a, int S, const float* gamma, int row0) {
+  __shared__ float red[ILL_H / 64];
+  const OpHdr hd = op_hdr(a.c);
+  const int m = blockIdx.x, j = threadIdx.x, w = j >> 6, lane = j & 63;
+  float pz[OP_MAXS];
+#pragma unroll
+  for (int z = 0; z < OP_MAXS; z++) pz[z] = z < S ? gld(a.part + ((size_t)z * a.M + m) * ILL_H + j) : 0.f;
+  float* r = a.resid + (size_t)m * ILL_H + j;
+  const float g = gld(gamma + j);
+  float y = pz[0];
+#pragma unroll
+  for (int z = 1; z < OP_MAXS; z++)
+    if (z < S) y += pz[z];
+  const float v = gld(r) + y;
+  if (!hd.done) gst(r, v);
+  if (m < row0) return;   // the whole workgroup
+  const float ss = gsum<64>(v * v);
+  if (lane == 0) red[w] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < ILL_H / 64; i++) tot += red[i];
+  const float scale = __builtin_amdgcn_rsqf(tot * (1.0f / (float)ILL_H) + ILL_EPS);
+  if (hd.done) return;
+  gst((uint16_t*)(a.c.xn + (size_t)(m - row0) * ILL_H + j), (uint16_t)__half_as_ushort(__float2half(v * scale * g)));
 }
 
 // ---- attention of passes of up to 16 rows -------------------------------------------------
@@ -466,7 +691,7 @@ __device__ __forceinline__ void att_combine(const float* m, const float* l, cons
 }
 
 __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int layer, int M, int nsplit, float* scratch) {
-  __shared__ __attribute__((aligned(16))) float qs[64];
+  __shared__ __attribute__((aligned(16))) float qs[ILL_WAVES][64];   // a copy per wave
   __shared__ __attribute__((aligned(16))) float ps[ILL_WAVES][64];
   __shared__ int path[16];
   __shared__ float cm[OP_NSPLIT][ILL_WAVES], cl[OP_NSPLIT][ILL_WAVES], co[OP_NSPLIT][ILL_WAVES][64];
@@ -478,24 +703,8 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   const int t = rh / ILL_NH, h = rh % ILL_NH, g = h / 7;
   const int pos = hd.pos;
   const bool tree = hd.mode == ILL_MODE_TREE;
-  if (w == 0) {
-    const float qv = gld(c.q + (size_t)t * ILL_H + h * 64 + lane);
-    const int dep0 = op_depth(c, hd.mode, t);
-    if (lane < 16) {   // rows on t's path by depth (tree passes: depth <= 15)
-      int pr = lane;
-      if (tree) {
-        int r = t;
-        for (int d = dep0; d >= 0; --d) {
-          if (d == lane) pr = r;
-          r = r > 0 ? gld(c.tree + ILL_TR_PARENT + r) : 0;
-        }
-      }
-      path[lane] = pr;
-    }
-    qs[lane] = qv * 0.125f;
-  }
+  const float qv = gld(c.q + (size_t)t * ILL_H + h * 64 + lane);   // before the K/V loads
   const int dep = op_depth(c, hd.mode, t);
-  __syncthreads();
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
   const int L = pos + dep + 1;
@@ -505,7 +714,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   // passes) and the transposed V row of dim = lane
   auto fetch = [&](int ch, uint4 (&kv)[8], uint4 (&vv)[8]) {
     const int vp = 64 * ch + lane;
-    const int slot = min(vp < pos || !tree ? vp : pos + path[min(vp - pos, 15)], c.maxctx - 1);
+    const int slot = min(vp < pos || !tree ? vp : pos + path[min(max(vp - pos, 0), 15)], c.maxctx - 1);
     const uint4* kr = (const uint4*)(kb + (size_t)slot * 64);
 #pragma unroll
     for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
@@ -513,6 +722,25 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
 #pragma unroll
     for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
   };
+  // The wave's first chunk (split j, chunk 16 j + w) is fetched before anything waits,
+  // unless it holds pass rows of a tree pass (their slots come from the path table).
+  uint4 kv[8], vv[8];
+  const int ch0 = 16 * j + w;
+  const bool early = j < nne && ch0 < nch && (!tree || 64 * ch0 + 63 < pos);
+  if (early) fetch(ch0, kv, vv);
+  qs[w][lane] = qv * 0.125f;
+  if (w == 0 && lane < 16) {   // rows on t's path by depth (tree passes: depth <= 15)
+    int pr = lane;
+    if (tree) {
+      int r = t;
+      for (int d = dep; d >= 0; --d) {
+        if (d == lane) pr = r;
+        r = r > 0 ? gld(c.tree + ILL_TR_PARENT + r) : 0;
+      }
+    }
+    path[lane] = pr;
+  }
+  lds_barrier();   // path and qs visible; the chunk loads stay in flight
 #pragma unroll 1
   for (int q = 0; q < OP_NSPLIT; q++) {
     const int s = j + nsplit * q;
@@ -521,9 +749,8 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
     // this wave's chunks of split s: 128 r + 16 s + 8 b + w (r = 0, 1, ..., b = 0, 1) in
     // order; the next one streams in while one is evaluated
     auto chunk_of = [&](int i) { return 128 * (i >> 1) + 16 * s + 8 * (i & 1) + w; };
-    uint4 kv[8], vv[8];
     int ch = chunk_of(0);
-    if (ch < nch) fetch(ch, kv, vv);
+    if (ch < nch && !(q == 0 && early)) fetch(ch, kv, vv);
     for (int ci = 0; ch < nch; ch = chunk_of(++ci)) {
       uint4 kn[8], vn[8];
       const int nx = chunk_of(ci + 1);
@@ -538,7 +765,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const uint32_t x[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
-        const float4 qa = *(const float4*)&qs[8 * i], qb = *(const float4*)&qs[8 * i + 4];
+        const float4 qa = *(const float4*)&qs[w][8 * i], qb = *(const float4*)&qs[w][8 * i + 4];
         const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) sc = fmaf(qv[e], h2f(x[e >> 1] >> (16 * (e & 1))), sc);

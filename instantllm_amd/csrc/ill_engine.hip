@@ -212,10 +212,12 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   if constexpr (EPI != OP_LMH) {
     if (M > 16) {   // prefill chunk: 64-row tiles, K split only where the tiles are few
       const int mt = (M + 63) / 64;
-      int S = std::max(1, std::min(std::min(256 / (ntn * mt), nsteps / 4), OP_MAXS));
+      const int cap = (int)(ILL_OP_PART_BYTES / ((size_t)M * W.N * 4));   // partial buffer
+      int S = std::max(1, std::min(std::min(std::min(256 / (ntn * mt), nsteps / 4), OP_MAXS), cap));
       g.ksteps = (nsteps + S - 1) / S;
       S = (nsteps + g.ksteps - 1) / g.ksteps;
-      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
+      // the many-tile gate/up GEMM streams best with the one-step kernel (more per CU)
+      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI, EPI == OP_SILU ? 1 : 4>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
       if (S > 1) {
         const int per = EPI == OP_RESID ? W.N : W.N / 2;
         hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
@@ -223,7 +225,7 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
       return false;
     }
   }
-  // up to 16 rows: op_gemv_kernel; split K so that about 256 workgroups stream the weights,
+  // up to 16 rows: split K so that about 256 workgroups stream the weights,
   // at least four k-steps per slice (the split depends on the matrix only, so 1-row and
   // 16-row passes sum the same partials in the same order)
   int S = 1;
@@ -241,7 +243,7 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
     g.part = e->opart + ILL_OP_PART_SPLIT;
     hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, true>), grid, dim3(256), 0, e->stream, g);
   } else {
-    hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI>), grid, dim3(256), 0, e->stream, g);
+    hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI, 4>), grid, dim3(256), 0, e->stream, g);
   }
   if constexpr (EPI != OP_LMH) {
     if (S > 1) {

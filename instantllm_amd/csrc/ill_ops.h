@@ -354,17 +354,20 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
 // Workgroup: 256 threads = 4 waves; a wave owns 32 columns (two 16-column MFMA tiles) of
 // the 128-column tile and all BM rows. blockIdx.z selects a K slice of `ksteps` 64-column
 // steps; with more than one slice the kernel writes fp32 partials [slice][M][N] and
-// op_epi_kernel reduces them in slice order and applies the epilogue. The operands of the
-// next OP_DEPTH k-steps are in flight (a register ring) while the current one is
-// multiplied: a k-step's MFMAs take far less than a memory round trip. The LDS tiles are
-// double-buffered, so one barrier per k-step orders both their reuse and their filling; it
-// waits for LDS traffic only (a full __syncthreads would also drain the ring's loads).
-#define OP_DEPTH 4
-template <int FMT, int BM, int EPI>
+// op_epi_kernel reduces them in slice order and applies the epilogue.
+// DEPTH > 1: the operands of the next DEPTH k-steps are in flight (a register ring) while
+// the current one is multiplied, and the LDS tiles are double-buffered, so one barrier per
+// k-step orders both their reuse and their filling; it waits for LDS traffic only (a full
+// __syncthreads would also drain the ring's loads). DEPTH 1: one k-step ahead, one LDS
+// buffer, two barriers per k-step, half the LDS and fewer registers: more workgroups per
+// CU, which is what the many-tile prefill gate/up GEMM needs (25.6 vs 40.7 us at 512 rows,
+// f16), while the ring wins where the tiles are few (O and down: 14.6 vs 17.0 us).
+template <int FMT, int BM, int EPI, int DEPTH>
 __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
+  constexpr int NB = DEPTH > 1 ? 2 : 1;
   const OpHdr hd = op_hdr(a.c);
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * OP_LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][OP_BN * OP_LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 As[NB][BM * OP_LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[NB][OP_BN * OP_LDK];
   __shared__ uint64_t red[4][16];
   constexpr int TM = BM / 16;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -379,6 +382,37 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
     acc[i][0] = (v4f){0.f, 0.f, 0.f, 0.f};
     acc[i][1] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
+  if constexpr (DEPTH == 1) {
+    WRaw<FMT> wr;
+    ARaw<BM> ar;
+    op_fetch_w<FMT>(a.W, n0, kb, tid, wr);
+    op_fetch_a<BM>(a.A, a.M, K, m0, kb, tid, ar);
+    for (int k0 = kb; k0 < ke; k0 += OP_BK) {
+      op_store_a<BM>(ar, As[0], tid);
+      op_store_w<FMT>(wr, Bs[0], tid);
+      __syncthreads();
+      if (k0 + OP_BK < ke) {
+        op_fetch_w<FMT>(a.W, n0, k0 + OP_BK, tid, wr);
+        op_fetch_a<BM>(a.A, a.M, K, m0, k0 + OP_BK, tid, ar);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        v8h bf[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) bf[j] = *(const v8h*)(Bs[0] + (32 * w + 16 * j + n) * OP_LDK + 32 * ks + 8 * kg);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const v8h af = *(const v8h*)(As[0] + (16 * i + n) * OP_LDK + 32 * ks + 8 * kg);
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+        }
+      }
+      __syncthreads();
+    }
+    op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, w, kg, n, red);
+    return;
+  }
+  constexpr int OP_DEPTH = DEPTH;
   // Ring loads are unconditional (steps past the slice reload its last one), so that the
   // compiler can count the loads in flight and wait for the oldest slot only.
   WRaw<FMT> wr[OP_DEPTH];
@@ -393,8 +427,8 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   // One k-step from ring slot d (st: the step's index in the slice); `refetch` refills the
   // slot with step st + OP_DEPTH (clamped: the last round reloads the slice's last step).
   auto kstep = [&](int d, int st, bool refetch) {
-    _Float16* as = As[d & 1];
-    _Float16* bs = Bs[d & 1];
+    _Float16* as = As[(d & 1) % NB];
+    _Float16* bs = Bs[(d & 1) % NB];
     op_store_a<BM>(ar[d], as, tid);
     op_store_w<FMT>(wr[d], bs, tid);
     lds_barrier();   // LDS only: the ring's HBM loads stay in flight

@@ -219,6 +219,10 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
       // the many-tile gate/up GEMM streams best with the one-step kernel (more per CU)
       hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI, EPI == OP_SILU ? 1 : 4>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
       if (S > 1) {
+        if (EPI == OP_RESID && norm_gamma && W.N == ILL_H) {
+          hipLaunchKernelGGL(op_epi_norm_kernel, dim3(M), dim3(ILL_H), 0, e->stream, g, S, norm_gamma, norm_row0);
+          return true;
+        }
         const int per = EPI == OP_RESID ? W.N : W.N / 2;
         hipLaunchKernelGGL((op_epi_kernel<EPI>), dim3((M * per + 255) / 256), dim3(256), 0, e->stream, g, S);
       }
@@ -273,8 +277,8 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
   // per 1024 positions of context (the result does not depend on the split)
   const int nch = (e->pos_hint + M + 63) / 64;
   const int nsplit = std::max(1, std::min(OP_NSPLIT, (nch + 15) / 16));
-  // passes of up to 16 rows: each residual update also writes the next RMSNorm (op_gemm
-  // returns whether it did)
+  // each residual update also writes the next RMSNorm where its K is split (op_gemm returns
+  // whether it did)
   bool normed = false;
   for (int l = 0; l < e->layers; l++) {
     const OpLayerW& L = e->holayers[l];
@@ -285,14 +289,14 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
       hipLaunchKernelGGL(op_attn_kernel, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart);
       if (nsplit > 1) hipLaunchKernelGGL(op_attn_combine_kernel, dim3(M * ILL_NH), dim3(64), 0, s, c, (const float*)e->opart);
     }
-    const bool fuse = M <= 16;
-    if (!op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x, fuse ? L.ln2 : nullptr, 0))
+    const bool fuse = M <= 16;   // the SwiGLU hand-over (the residual + norm fusion: any M)
+    if (!op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x, L.ln2, 0))
       hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
     int silu_S = 0;
     op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr, nullptr, 0, fuse ? &silu_S : nullptr);
     const bool last = l + 1 == e->layers;
     const float* next = last ? (lm_rows > 0 ? c.fnorm : nullptr) : e->holayers[l + 1].ln1;
-    normed = op_gemm<FMT, OP_RESID>(e, c.h, L.d, M, l, c.x, fuse ? next : nullptr, last ? M - lm_rows : 0, nullptr, silu_S);
+    normed = op_gemm<FMT, OP_RESID>(e, c.h, L.d, M, l, c.x, next, last ? M - lm_rows : 0, nullptr, silu_S);
   }
   if (lm_rows > 0) {
     if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((lm_rows + 3) / 4), dim3(256), 0, s, c, c.fnorm, M - lm_rows, lm_rows);

@@ -284,7 +284,7 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     const OpLayerW& L = e->holayers[l];
     if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
-    if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64), 0, s, c, l, M);
+    if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64 * OP_RW), 0, s, c, l, M);
     else {
       hipLaunchKernelGGL(op_attn_kernel, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart);
       if (nsplit > 1) hipLaunchKernelGGL(op_attn_combine_kernel, dim3(M * ILL_NH), dim3(64), 0, s, c, (const float*)e->opart);

@@ -940,17 +940,21 @@ __global__ __launch_bounds__(64) void op_attn_combine_kernel(OpCtx c, const floa
 }
 
 // ---- attention of prefill chunks (more than 16 rows): MFMA flash attention --------------
-// One wave per (16-row block, query head h). Row t < M sits at position pos + t and attends
-// to positions 0 .. pos + t, all in the cache (this chunk's QKV kernel has written its own
-// keys and values). Per 64-position chunk: scores (0.125 q) . k on v_mfma_f32_16x16x32_f16
+// One workgroup of OP_RW waves per (16-row block, query head h): chunk c goes to wave
+// c % OP_RW, which folds its chunks in order, and the waves' states are combined at the end
+// in wave order. Row t < M sits at position pos + t and attends to positions 0 .. pos + t,
+// all in the cache (this chunk's QKV kernel has written its own keys and values). Per 64-position chunk: scores (0.125 q) . k on v_mfma_f32_16x16x32_f16
 // with q split into f16 high and low parts (products as accurate as fp32 q), the causal
 // mask, the row softmax statistics (maximum, sum of exponentials) folded chunk by chunk with
-// the rule of the other attention kernels, and O += P V with P split the same way. The next
-// chunk's keys and values stream in while one is evaluated.
-__global__ __launch_bounds__(64) void op_attn_rows_kernel(OpCtx c, int layer, int M) {
-  __shared__ float pb[16 * 64];
+// the rule of the other attention kernels, and O += P V with P split the same way. A wave's
+// next chunk's keys and values stream in while one is evaluated.
+#define OP_RW 4
+__global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int layer, int M) {
+  __shared__ float pbw[OP_RW][16 * 64];
+  __shared__ float sm_[OP_RW][16], sl_[OP_RW][16], so_[OP_RW][16][64];
   const OpHdr hd = op_hdr(c);
-  const int lane = threadIdx.x, kg = lane >> 4, n = lane & 15;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4, n = lane & 15;
+  float* pb = pbw[w];
   const int t0 = 16 * blockIdx.x, h = blockIdx.y, g = h / 7;
   const int pos = hd.pos;
   // A operand: lane (kg, n) holds row t0 + n, dims 32 ks + 8 kg + i
@@ -985,11 +989,11 @@ __global__ __launch_bounds__(64) void op_attn_rows_kernel(OpCtx c, int layer, in
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
   KVFrag f;
-  kv_fetch(kbase, vbase, 0, lane, f);
-  for (int ch = 0; ch < nch; ch++) {
+  if (w < nch) kv_fetch(kbase, vbase, w, lane, f);
+  for (int ch = w; ch < nch; ch += OP_RW) {
     KVFrag fn;
-    const bool more = ch + 1 < nch;
-    if (more) kv_fetch(kbase, vbase, ch + 1, lane, fn);
+    const bool more = ch + OP_RW < nch;
+    if (more) kv_fetch(kbase, vbase, ch + OP_RW, lane, fn);
     float sc[4][4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
@@ -1052,15 +1056,35 @@ __global__ __launch_bounds__(64) void op_attn_rows_kernel(OpCtx c, int layer, in
     }
     if (more) f = fn;
   }
-  if (hd.done) return;
+  // the waves' states, combined in wave order against their maximum
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const int t = t0 + 4 * kg + j;
-    if (t < M) {
-#pragma unroll
-      for (int nb = 0; nb < 4; nb++)
-        gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + 16 * nb + n), (uint16_t)__half_as_ushort(__float2half(O[nb][j] / Ls[j])));
+    if (n == 0) {
+      sm_[w][4 * kg + j] = Mx[j];
+      sl_[w][4 * kg + j] = Ls[j];
     }
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) so_[w][4 * kg + j][16 * nb + n] = O[nb][j];
+  }
+  __syncthreads();
+  if (hd.done) return;
+  const int r = threadIdx.x >> 4, t = t0 + r;
+  if (t >= M) return;
+  float m[OP_RW], l[OP_RW];
+#pragma unroll
+  for (int i = 0; i < OP_RW; i++) {
+    m[i] = sm_[i][r];
+    l[i] = sl_[i][r];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int d = (threadIdx.x & 15) + 16 * q;
+    float o[OP_RW];
+#pragma unroll
+    for (int i = 0; i < OP_RW; i++) o[i] = so_[i][r][d];
+    float mo, lo, oo;
+    att_combine<OP_RW>(m, l, o, mo, lo, oo);
+    gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + d), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
   }
 }
 

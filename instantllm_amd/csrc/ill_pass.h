@@ -505,7 +505,7 @@ struct LmhLds {
 };
 
 struct CommitLds {
-  uint64_t key[ILL_WG / 64];
+  uint64_t key[16][ILL_WG / 64];   // [row - first row][wave holding the row's partials]
   int g[16];
   int path[16];
   int npath, pos0;
@@ -1423,15 +1423,18 @@ __device__ __forceinline__ bool role_prep(const IllPassArgs& a, const PassHdr& H
   for (int l = 0; l <= NL; l++) {
     const float* gam = l < NL ? a.L[l].ln1 : a.W.fnorm;
     bool ok;
-    if (l == 0) ok = prep896<1>(SrcEmbed{a.W, H.tok + t}, gam, 1, P, a.ctl, 700, a, rs);
-    else ok = prep896<1>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, t)}, gam, 1, P, a.ctl, 700 + l, a, rs);
+    const int tr = l < NL ? ILL_TRL * l : -1;   // trace: 1/2 input seen / coded, 3 published, 5-7 the same for XA
+    if (l == 0) ok = prep896<1>(SrcEmbed{a.W, H.tok + t}, gam, 1, P, a.ctl, 700, a, rs, tr < 0 ? -1 : tr + 1);
+    else ok = prep896<1>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, t)}, gam, 1, P, a.ctl, 700 + l, a, rs, tr < 0 ? -1 : tr + 1);
     if (!ok) return false;
     pub_write(P, rs[0], pub_ptr(a, 1, l, t), tagof_pub(H.epoch, l));
     lds_barrier();   // the coding is read out before the next one is written
     if (l == NL) break;
-    if (!prep896<1>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, t)}, a.L[l].ln2, 1, P, a.ctl, 750 + l, a, rs)) return false;
+    trace_mark(a, tr + 3);
+    if (!prep896<1>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, t)}, a.L[l].ln2, 1, P, a.ctl, 750 + l, a, rs, tr + 5)) return false;
     pub_write(P, rs[0], pub_ptr(a, 0, l, t), tagof_pub(H.epoch, l));
     lds_barrier();
+    trace_mark(a, tr + 7);
   }
   return true;
 }
@@ -1539,36 +1542,47 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
   // every workgroup's partials for the rows in use (row 0 when the pass has no lm_head rows):
   // this also proves that every workgroup has read the pass header
   const int r0 = H.lmhn > 0 ? H.lmh0 : 0, nr = H.lmhn > 0 ? H.lmhn : 1;
+  static_assert(ILL_WG_THREADS == 2 * ILL_WG, "thread i: workgroup i % 256, rows r0 + i / 256 + 2 m");
+  // Thread i holds workgroup (i % 256)'s partials of rows r0 + (i >> 8) + 2 m (m < 8) as
+  // order-preserving keys (value, lowest index), taken from the poll that saw them all, so
+  // every row's partials are read in one round trip.
+  uint64_t key[8];
   const bool ok = wg_wait([&]() {
     bool r = true;
-#pragma unroll 8
-    for (int k = i; k < ILL_WG * nr; k += ILL_WG_THREADS) {
-      const int wgi = k % ILL_WG, t = r0 + k / ILL_WG;
-      r &= wok(aload64(a.lmp + (wgi * 16 + t) * 2), tag) & wok(aload64(a.lmp + (wgi * 16 + t) * 2 + 1), tag);
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+      const int k = i + ILL_WG_THREADS * m;
+      key[m] = 0;
+      if (k < ILL_WG * nr) {
+        const int wgi = k % ILL_WG, t = r0 + k / ILL_WG;
+        const uint64_t v = aload64(a.lmp + (wgi * 16 + t) * 2), x = aload64(a.lmp + (wgi * 16 + t) * 2 + 1);
+        r &= wok(v, tag) & wok(x, tag);
+        key[m] = amax_key(wval(v), (int)(uint32_t)x);
+      }
     }
     return r;
   }, a.ctl, 700);
   if (!ok) return;
   trace_mark(a, ILL_TR_TAIL + 4);
-  // global argmax per row: order-preserving keys (value, lowest index), reduced in each of
-  // the 4 waves that hold a partial, then across them
+  // global argmax per row: reduced in each of the 4 waves that hold a row's partials, then
+  // across them
   const int lane = i & 63, wv = i >> 6;
-  for (int t = H.lmh0; t < H.lmh0 + H.lmhn; t++) {
-    uint64_t k = 0;
-    if (i < ILL_WG) k = amax_key(wval(aload64(a.lmp + (i * 16 + t) * 2)), (int)(uint32_t)aload64(a.lmp + (i * 16 + t) * 2 + 1));
+#pragma unroll
+  for (int m = 0; m < 8; m++) {
+    uint64_t k = key[m];
     for (int o = 32; o >= 1; o >>= 1) {
-      const uint64_t ok = __shfl_xor(k, o, 64);
-      k = ok > k ? ok : k;
+      const uint64_t ok2 = __shfl_xor(k, o, 64);
+      k = ok2 > k ? ok2 : k;
     }
-    if (lane == 0 && wv < ILL_WG / 64) C.key[wv] = k;
-    __syncthreads();
-    if (i == 0) {
-      uint64_t m = C.key[0];
-      for (int ww = 1; ww < ILL_WG / 64; ww++) m = C.key[ww] > m ? C.key[ww] : m;
-      C.g[t] = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFu));
-    }
-    __syncthreads();
+    if (lane == 0) C.key[(i >> 8) + 2 * m][wv & 3] = k;
   }
+  __syncthreads();
+  if (H.lmhn > 0 && i < H.lmhn) {
+    uint64_t m = C.key[i][0];
+    for (int ww = 1; ww < ILL_WG / 64; ww++) m = C.key[i][ww] > m ? C.key[i][ww] : m;
+    C.g[H.lmh0 + i] = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFu));
+  }
+  __syncthreads();
   commit_apply(a, H, C, true);
 }
 
@@ -1717,11 +1731,12 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   }
   trace_mark(a, ILL_TR_TAIL);
   if (!role_lmh<T>(a, H, S.lmh)) return;
-  zero_other_bank(a, H);
+  if (wg != 0) zero_other_bank(a, H);
   trace_mark(a, ILL_TR_TAIL + 2);
-  if (wg == 0) {
+  if (wg == 0) {   // the commit first: the bank is next used by the following launch
     __syncthreads();
     commit(a, H, S.cm);
     trace_mark(a, ILL_TR_TAIL + 5);
+    zero_other_bank(a, H);
   }
 }

@@ -735,12 +735,25 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rh = blockIdx.x / nsplit, j = blockIdx.x % nsplit;
   const int t = rh / ILL_NH, h = rh % ILL_NH, g = h / 7;
-  const int pos = hd.pos;
-  const bool tree = hd.mode == ILL_MODE_TREE;
   const float qv = gld(c.q + (size_t)t * ILL_H + h * 64 + lane);   // before the K/V loads
-  const int dep = op_depth(c, hd.mode, t);
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
+  // The wave's first chunk (split j, chunk 16 j + w) at its plain slots, issued before the
+  // header is waited for; it is used unless the chunk lies past the row's positions or
+  // holds pass rows of a tree pass (their slots come from the path table).
+  uint4 kv[8], vv[8];
+  const int ch0 = 16 * j + w;
+  {
+    const uint4* kr = (const uint4*)(kb + (size_t)min(64 * ch0 + lane, c.maxctx - 1) * 64);
+    const uint4* vr = (const uint4*)(vb + ((size_t)min(ch0, c.maxctx / 64 - 1) * 64 + lane) * 64);
+#pragma unroll
+    for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
+#pragma unroll
+    for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
+  }
+  const int pos = hd.pos;
+  const bool tree = hd.mode == ILL_MODE_TREE;
+  const int dep = op_depth(c, hd.mode, t);
   const int L = pos + dep + 1;
   const int nch = (L + 63) >> 6;
   const int nne = min(OP_NSPLIT, (nch + 15) >> 4);   // splits 0 .. nne - 1 hold chunks
@@ -756,12 +769,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
 #pragma unroll
     for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
   };
-  // The wave's first chunk (split j, chunk 16 j + w) is fetched before anything waits,
-  // unless it holds pass rows of a tree pass (their slots come from the path table).
-  uint4 kv[8], vv[8];
-  const int ch0 = 16 * j + w;
   const bool early = j < nne && ch0 < nch && (!tree || 64 * ch0 + 63 < pos);
-  if (early) fetch(ch0, kv, vv);
   qs[w][lane] = qv * 0.125f;
   if (w == 0 && lane < 16) {   // rows on t's path by depth (tree passes: depth <= 15)
     int pr = lane;

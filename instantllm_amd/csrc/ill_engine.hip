@@ -208,6 +208,7 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   g.layer = layer;
   g.resid = resid;
   g.part = e->opart;
+  g.pos_hint = e->pos_hint;
   const int nsteps = W.K / OP_BK, ntn = W.N / OP_BN;
   if constexpr (EPI != OP_LMH) {
     if (M > 16) {   // prefill chunk: 64-row tiles, K split only where the tiles are few

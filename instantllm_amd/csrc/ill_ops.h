@@ -146,6 +146,8 @@ struct OpGemmArgs {
   int ksteps;        // 64-column steps per K slice
   const float* apart;   // op_gemv_kernel<.., SILU = true>: gate/up partials [aS][M][2K]
   int aS;
+  int pos_hint;         // the State's pos as the host expects it (QKV epilogue: rotary rows
+                        // are loaded for pos_hint + row with the partials)
 };
 
 #define OP_BN 128
@@ -239,13 +241,17 @@ __device__ __forceinline__ void op_store_a(const ARaw<BM>& r, _Float16* As, int 
 // QKV: one rotary block b = columns 32 b .. +31 holds dims d (x0, columns 32 b + i) and
 // d + 32 (x1, columns 32 b + 16 + i) of head b / 2 (Convert.swift:236-244); q heads 0-13,
 // k 14-15, v 16-17: bias, RoPE at the row's position, then q or the K / V cache slot.
-__device__ __forceinline__ void epi_qkv(const OpCtx& c, const OpHdr& hd, int layer, int m, int b, int i, float x0, float x1) {
+// cs_at / cs: a rotary row already loaded for position cs_at (-1: none), used when it is
+// the row's position.
+__device__ __forceinline__ void epi_qkv(const OpCtx& c, const OpHdr& hd, int layer, int m, int b, int i, float x0, float x1,
+                                        int cs_at = -1, float2 cs_pre = make_float2(0.f, 0.f)) {
   const int head = b >> 1, d = (b & 1) * 16 + i;
   x0 += gld(c.L[layer].bqkv + 32 * b + i);
   x1 += gld(c.L[layer].bqkv + 32 * b + 16 + i);
   const int pos = hd.pos;
   if (head < ILL_NH + ILL_NKV) {
-    const float2 cs = gld(c.rope + (pos + op_depth(c, hd.mode, m)) * 32 + d);
+    const int p = pos + op_depth(c, hd.mode, m);
+    const float2 cs = p == cs_at ? cs_pre : gld(c.rope + p * 32 + d);
     const float r0 = x0 * cs.x - x1 * cs.y, r1 = x1 * cs.x + x0 * cs.y;
     x0 = r0;
     x1 = r1;
@@ -647,8 +653,10 @@ __global__ __launch_bounds__(256) void op_epi_kernel(OpGemmArgs a, int S) {
     if (!hd.done) epi_silu(a.c, m, j, g, u);
   } else if constexpr (EPI == OP_QKV) {
     const int b = j >> 4, ii = j & 15;
+    const int at = min(a.pos_hint + m, a.c.maxctx - 1);   // a chain row's expected position
+    const float2 cs = gld(a.c.rope + (size_t)at * 32 + (b & 1) * 16 + ii);
     const float x0 = sum(32 * b + ii), x1 = sum(32 * b + 16 + ii);
-    if (!hd.done) epi_qkv(a.c, hd, a.layer, m, b, ii, x0, x1);
+    if (!hd.done) epi_qkv(a.c, hd, a.layer, m, b, ii, x0, x1, at, cs);
   }
 }
 

@@ -278,6 +278,11 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
   // per 1024 positions of context (the result does not depend on the split)
   const int nch = (e->pos_hint + M + 63) / 64;
   const int nsplit = std::max(1, std::min(OP_NSPLIT, (nch + 15) / 16));
+  // passes of up to 16 rows (q8 / f16; q4 ones run on the pass kernel): the O projection
+  // runs per head inside the attention kernel (one split) or the split combine, always with
+  // the same arithmetic, so the split does not change the result
+  const bool ofuse = FMT != 2 && M <= 16;
+  float* opart_o = e->opart + ILL_OP_PART_SPLIT;   // [head][row][896] O partials
   // each residual update also writes the next RMSNorm where its K is split (op_gemm returns
   // whether it did)
   bool normed = false;
@@ -287,11 +292,25 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
     if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64 * OP_RW), 0, s, c, l, M);
     else {
-      hipLaunchKernelGGL(op_attn_kernel, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart);
-      if (nsplit > 1) hipLaunchKernelGGL(op_attn_combine_kernel, dim3(M * ILL_NH), dim3(64), 0, s, c, (const float*)e->opart);
+      float* op1 = ofuse && nsplit == 1 ? opart_o : nullptr;
+      hipLaunchKernelGGL(op_attn_kernel<FMT>, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart,
+                         L.o, op1);
+      if (nsplit > 1)
+        hipLaunchKernelGGL(op_attn_combine_kernel<FMT>, dim3(M * ILL_NH), dim3(64 * ILL_WAVES), 0, s, c, (const float*)e->opart,
+                           L.o, ofuse ? opart_o : (float*)nullptr, M);
+      if (ofuse) {   // the residual + norm over the 14 per-head O partials (head order)
+        OpGemmArgs g{};
+        g.c = c;
+        g.W = L.o;
+        g.M = M;
+        g.layer = l;
+        g.resid = c.x;
+        g.part = opart_o;
+        hipLaunchKernelGGL(op_epi_norm_kernel, dim3(M), dim3(ILL_H), 0, s, g, ILL_NH, L.ln2, 0);
+      }
     }
     const bool fuse = M <= 16;   // the SwiGLU hand-over (the residual + norm fusion: any M)
-    if (!op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x, L.ln2, 0))
+    if (!ofuse && !op_gemm<FMT, OP_RESID>(e, c.ao, L.o, M, l, c.x, L.ln2, 0))
       hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln2, 0, M);
     int silu_S = 0;
     op_gemm<FMT, OP_SILU>(e, c.xn, L.gu, M, l, nullptr, nullptr, 0, fuse ? &silu_S : nullptr);

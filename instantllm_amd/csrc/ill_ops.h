@@ -732,18 +732,82 @@ __device__ __forceinline__ void att_combine(const float* m, const float* l, cons
   oo = acc;
 }
 
-__global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int layer, int M, int nsplit, float* scratch) {
+// The O projection of one (row, head) folded into the attention kernel (passes of up to 16
+// rows, one attention split): wave w computes output columns 112 w + lane and
+// 112 w + 64 + lane (lane < 48) of W_o[:, 64 h .. 64 h + 63] . ao, where ao is the head's
+// f16 output (LDS). Weights are dequantized as op_gemm_kernel does (q8: f16 s * q; f16 as
+// stored) and the 64 products are added in k order in fp32: the partial of slice h, which
+// op_epi_norm_kernel sums over the 14 heads in head order.
+template <int FMT>
+struct ORows {
+  uint4 q[2][FMT == 0 ? 8 : 4];
+  uint16_t s[2][2];   // q8: the scales of k 0-31 and 32-63 (equal for group 64)
+};
+template <int FMT>
+__device__ __forceinline__ void orows_fetch(const OpMat& Wo, int h, int w, int lane, ORows<FMT>& o) {
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = min(112 * w + 64 * u + lane, ILL_H - 1);
+    if constexpr (FMT == 1) {
+      const uint4* src = (const uint4*)(Wo.w + (size_t)r * Wo.K + 64 * h);
+#pragma unroll
+      for (int i = 0; i < 4; i++) o.q[u][i] = gld(src + i);
+      o.s[u][0] = gld(Wo.s + (size_t)r * (Wo.K / Wo.qg) + (64 * h) / Wo.qg);
+      o.s[u][1] = gld(Wo.s + (size_t)r * (Wo.K / Wo.qg) + (64 * h + 32) / Wo.qg);
+    } else {
+      const uint4* src = (const uint4*)(Wo.w + ((size_t)r * Wo.K + 64 * h) * 2);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o.q[u][i] = gld(src + i);
+    }
+  }
+}
+template <int FMT>
+__device__ __forceinline__ void orows_apply(const ORows<FMT>& o, const _Float16* ao, int w, int lane, float* dst) {
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int r = 112 * w + 64 * u + lane;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < (FMT == 0 ? 8 : 4); i++) {
+      const uint32_t x[4] = {o.q[u][i].x, o.q[u][i].y, o.q[u][i].z, o.q[u][i].w};
+      constexpr int PER = FMT == 0 ? 8 : 16;   // k values per uint4
+#pragma unroll
+      for (int e = 0; e < PER; e++) {
+        const int k = PER * i + e;
+        _Float16 wv;
+        if constexpr (FMT == 1) {
+          const _Float16 sc = (_Float16)h2f(o.s[u][k >> 5]);
+          wv = sc * (_Float16)(float)(int8_t)((x[e >> 2] >> (8 * (e & 3))) & 0xff);
+        } else {
+          wv = __ushort_as_half((unsigned short)((x[e >> 1] >> (16 * (e & 1))) & 0xffff));
+        }
+        acc = fmaf((float)wv, (float)ao[k], acc);
+      }
+    }
+    if (u == 0 || lane < 48) dst[r] = acc;
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int layer, int M, int nsplit, float* scratch,
+                                                               OpMat Wo, float* opart) {
   __shared__ __attribute__((aligned(16))) float qs[ILL_WAVES][64];   // a copy per wave
   __shared__ __attribute__((aligned(16))) float ps[ILL_WAVES][64];
   __shared__ int path[16];
   __shared__ float cm[OP_NSPLIT][ILL_WAVES], cl[OP_NSPLIT][ILL_WAVES], co[OP_NSPLIT][ILL_WAVES][64];
   __shared__ float sm[OP_NSPLIT], sl[OP_NSPLIT], so[OP_NSPLIT][64];
   __shared__ __attribute__((aligned(16))) uint16_t vstage[ILL_WAVES][64 * OP_VST];   // tree passes: V rows
+  __shared__ _Float16 aoh[64];   // with opart: the head's output, the O projection's input
   const OpHdr hd = op_hdr(c);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rh = blockIdx.x / nsplit, j = blockIdx.x % nsplit;
   const int t = rh / ILL_NH, h = rh % ILL_NH, g = h / 7;
   const float qv = gld(c.q + (size_t)t * ILL_H + h * 64 + lane);   // before the K/V loads
+  // with opart (nsplit 1, q8 / f16) the O projection follows (this wave's W_o rows are
+  // fetched when the chunk loop is done: held from the start they would spill)
+  constexpr bool OFUSE = FMT != 2;
+  const bool fused = OFUSE && opart != nullptr;
+  ORows<OFUSE ? FMT : 1> orw;
   const uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + g) * c.maxctx * 64;
   const uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + g) * (c.maxctx / 64) * 4096;
   // The wave's first chunk (split j, chunk 16 j + w) at its plain slots, issued before the
@@ -880,16 +944,31 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
     }
     co[q][w][lane] = O;
   }
+  if constexpr (OFUSE)
+    if (fused) orows_fetch<FMT>(Wo, h, w, lane, orw);
   __syncthreads();
+  // the head's output row: to c.ao, or (opart) through LDS into the O projection
+  auto emit = [&](float v) {
+    const __half hv = __float2half(v);
+    if (fused) aoh[lane] = (_Float16)hv;
+    else if (!hd.done) gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(hv));
+  };
+  auto oproj = [&]() {
+    if constexpr (OFUSE) {
+      __syncthreads();
+      orows_apply<FMT>(orw, aoh, w, lane, opart + ((size_t)h * M + t) * ILL_H);
+    }
+  };
   if (nsplit == 1 && nne == 1) {   // one split: its state is the row's (the general path
-    if (w == 0 && !hd.done) {      // below gives the same bits: scale 1, nothing added)
+    if (w == 0) {                  // below gives the same bits: scale 1, nothing added)
       float o[ILL_WAVES];
 #pragma unroll
       for (int ww = 0; ww < ILL_WAVES; ww++) o[ww] = co[0][ww][lane];
       float mo, lo, oo;
       att_combine<ILL_WAVES>(cm[0], cl[0], o, mo, lo, oo);
-      gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
+      emit(oo / lo);
     }
+    if (fused) oproj();
     return;
   }
   // split states: wave q combines the slots of split j + nsplit q (empty splits: m = -inf)
@@ -926,42 +1005,61 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   }
   if (nsplit > 1) return;
   __syncthreads();
-  if (w == 0 && !hd.done) {
+  if (w == 0) {
     float o[OP_NSPLIT];
 #pragma unroll
     for (int q = 0; q < OP_NSPLIT; q++) o[q] = so[q][lane];
     float mo, lo, oo;
     att_combine<OP_NSPLIT>(sm, sl, o, mo, lo, oo);
-    gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
+    emit(oo / lo);
   }
+  if (fused) oproj();
 }
 
 // The rows of op_attn_kernel launched with nsplit > 1: the eight split states of (row, head)
-// combined in split order.
-__global__ __launch_bounds__(64) void op_attn_combine_kernel(OpCtx c, const float* scratch) {
+// combined in split order (wave 0), then (opart) the head's O projection by all eight waves.
+template <int FMT>
+__global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_combine_kernel(OpCtx c, const float* scratch, OpMat Wo, float* opart,
+                                                                       int M) {
+  __shared__ _Float16 aoh[64];
   const int done = gld(&c.st->done);
-  const int rh = blockIdx.x, lane = threadIdx.x;
+  const int rh = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = rh / ILL_NH, h = rh % ILL_NH;
-  float m[OP_NSPLIT], l[OP_NSPLIT], o[OP_NSPLIT];
+  // with opart (q8 / f16) the head's O projection follows, as in op_attn_kernel
+  constexpr bool OFUSE = FMT != 2;
+  const bool fused = OFUSE && opart != nullptr;
+  ORows<OFUSE ? FMT : 1> orw;
+  if constexpr (OFUSE)
+    if (fused) orows_fetch<FMT>(Wo, h, w, lane, orw);
+  if (w == 0) {
+    float m[OP_NSPLIT], l[OP_NSPLIT], o[OP_NSPLIT];
 #pragma unroll
-  for (int s = 0; s < OP_NSPLIT; s++) {
-    const float* src = scratch + ((size_t)rh * OP_NSPLIT + s) * OP_SPLIT_W;
-    m[s] = gld(src);
-    l[s] = gld(src + 1);
-    o[s] = gld(src + 2 + lane);
+    for (int s = 0; s < OP_NSPLIT; s++) {
+      const float* src = scratch + ((size_t)rh * OP_NSPLIT + s) * OP_SPLIT_W;
+      m[s] = gld(src);
+      l[s] = gld(src + 1);
+      o[s] = gld(src + 2 + lane);
+    }
+    float mo, lo, oo;
+    att_combine<OP_NSPLIT>(m, l, o, mo, lo, oo);
+    const __half hv = __float2half(oo / lo);
+    if (fused) aoh[lane] = (_Float16)hv;
+    else if (!done) gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(hv));
   }
-  float mo, lo, oo;
-  att_combine<OP_NSPLIT>(m, l, o, mo, lo, oo);
-  if (!done) gst((uint16_t*)(c.ao + (size_t)t * ILL_H + h * 64 + lane), (uint16_t)__half_as_ushort(__float2half(oo / lo)));
+  if constexpr (OFUSE)
+    if (fused) {
+      __syncthreads();
+      orows_apply<FMT>(orw, aoh, w, lane, opart + ((size_t)h * M + t) * ILL_H);
+    }
 }
 
 // ---- attention of prefill chunks (more than 16 rows): MFMA flash attention --------------
 // One workgroup of OP_RW waves per (16-row block, query head h): chunk c goes to wave
 // c % OP_RW, which folds its chunks in order, and the waves' states are combined at the end
 // in wave order. Row t < M sits at position pos + t and attends to positions 0 .. pos + t,
-// all in the cache (this chunk's QKV kernel has written its own keys and values). Per 64-position chunk: scores (0.125 q) . k on v_mfma_f32_16x16x32_f16
-// with q split into f16 high and low parts (products as accurate as fp32 q), the causal
-// mask, the row softmax statistics (maximum, sum of exponentials) folded chunk by chunk with
+// all in the cache (this chunk's QKV kernel has written its own keys and values). Per
+// 64-position chunk: scores (0.125 q) . k on v_mfma_f32_16x16x32_f16 with q split into f16
+// high and low parts (products as accurate as fp32 q), the causal mask, the row softmax statistics (maximum, sum of exponentials) folded chunk by chunk with
 // the rule of the other attention kernels, and O += P V with P split the same way. A wave's
 // next chunk's keys and values stream in while one is evaluated.
 #define OP_RW 4

@@ -277,9 +277,12 @@ __device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float 
 
 // Epilogue of a 128-column tile (lane (kg, n) of wave w holds rows m0 + 16 i + 4 kg + r,
 // columns n0 + 32 w + 16 j + n): fp32 partials of a K slice, or the fused epilogue.
+// QKV: cs_base >= 0 gives the rotary rows cs[r] of rows m0 + 4 kg + r at position cs_base +
+// row (used when that is the row's position).
 template <int BM, int EPI>
 __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHdr& hd, const v4f (&acc)[BM / 16][2], int m0,
-                                                 int n0, int w, int kg, int n, uint64_t (&red)[4][16]) {
+                                                 int n0, int w, int kg, int n, uint64_t (&red)[4][16], int cs_base = -1,
+                                                 const float2* cs = nullptr) {
   constexpr int TM = BM / 16;
   if (hd.done) return;
   const OpCtx& c = a.c;
@@ -326,7 +329,10 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + 16 * i + 4 * kg + r;
-        if (m < a.M) epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
+        if (m < a.M) {
+          if (cs_base >= 0 && TM == 1) epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r], cs_base + m, cs[r]);
+          else epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
+        }
       }
   } else {   // OP_LMH: logits (optional) and per-tile argmax keys per row (BM == 16)
     const int wlog = hd.wlog;
@@ -540,14 +546,23 @@ __device__ __forceinline__ v8h op_bvals(const BOp<FMT>& b, int j, int ks) {
   return o;
 }
 
-template <int FMT, int EPI, bool SILU>
-__global__ __launch_bounds__(256) void op_gemv_kernel(OpGemmArgs a) {
+template <int FMT, int EPI, bool SILU, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
+  static_assert(NWV == 4 || (NWV == 1 && EPI == OP_QKV), "one-wave workgroups: the unsplit QKV GEMM");
+  constexpr int NT = 64 * NWV;
   const OpHdr hd = op_hdr(a.c);
   __shared__ __attribute__((aligned(16))) _Float16 As[16 * (OP_SMAXK + 8)];
   __shared__ uint64_t red[4][16];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
-  const int n0 = blockIdx.x * OP_BN, col0 = n0 + 32 * w;
+  const int n0 = blockIdx.x * 32 * NWV, col0 = n0 + 32 * w;
+  // QKV: the rotary rows of this lane's rows 4 kg + r at the expected position (pos_hint + row)
+  float2 cs[4];
+  if constexpr (EPI == OP_QKV) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      cs[r] = gld(a.c.rope + (size_t)min(a.pos_hint + 4 * kg + r, a.c.maxctx - 1) * 32 + ((col0 >> 5) & 1) * 16 + n);
+  }
   const int K = a.W.K;
   const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
   const int ns = (ke - kb) / OP_BK, kw = ke - kb;
@@ -563,14 +578,14 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(OpGemmArgs a) {
   // are never stored)
   if constexpr (!SILU) {
     const int per = kw / 8;   // uint4 per row
-    for (int i = tid; i < a.M * per; i += 256) {
+    for (int i = tid; i < a.M * per; i += NT) {
       const int m = i / per, c8 = i - m * per;
       *(uint4*)(As + m * lda + 8 * c8) = gld((const uint4*)(a.A + (size_t)m * K + kb) + c8);
     }
   } else {
     // units kb + 2 p, kb + 2 p + 1 of row m: gate/up columns 2 kb + 4 p .. + 3 (g, g, u, u)
     const int per = kw / 2, N2 = 2 * K;
-    for (int i = tid; i < a.M * per; i += 256) {
+    for (int i = tid; i < a.M * per; i += NT) {
       const int m = i / per, p = i - m * per;
       float4 pz[OP_MAXS];
 #pragma unroll
@@ -619,7 +634,7 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(OpGemmArgs a) {
 #pragma unroll
   for (int d = 0; d < SD - 1; d++)
     if (s0 + d < ns) kstep(d, s0 + d, false);
-  op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red);
+  op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red, a.pos_hint, cs);
 }
 
 // Split-K reduction: sum of the slices' partials in slice order, then the epilogue.

@@ -47,15 +47,20 @@ struct GemvItem {
   uint2 s[ILL_GEMV_MAXBPS];
 };
 
+template <bool ALL = false>
 __device__ __forceinline__ void gemv_fetch(const IllGemvArgs& a, int item, int lane, GemvItem& it) {
   const int nb = a.K >> 7;
   const int tile = item / a.ks, slice = item - tile * a.ks;
   const int cb0 = slice * a.bps;
   const int n = lane & 15;
+  // ALL: every block slot loads (slots past the slice reload its last block, unused): with
+  // no branch between the loads, the compiler can wait for one item's loads while the next
+  // item's stay in flight (the one-slice kernel, whose items fill the slots: lm_head 21.5
+  // -> 19.6 us). Otherwise only the slice's blocks load (few-block items of split K).
 #pragma unroll
   for (int i = 0; i < ILL_GEMV_MAXBPS; i++) {
-    const int cb = min(cb0 + i, nb - 1);   // in bounds; blocks past the slice are not used
-    if (i < a.bps) {
+    const int cb = min(cb0 + min(i, a.bps - 1), nb - 1);
+    if (ALL || i < a.bps) {
       it.w[i] = gld((const uint4*)(a.w + ((size_t)tile * nb + cb) * 1024) + lane);
       it.s[i] = gld((const uint2*)(a.s + ((size_t)tile * nb + cb) * 32) + n);
     }
@@ -142,12 +147,12 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_gemv_q4_kernel(IllGemvA
   if (a.key && blockIdx.x == 0 && tid == 0) gst(a.key + (a.par ^ 1), (uint64_t)0);
   uint64_t kbest = 0;
   GemvItem cur;
-  if (item < nitems) gemv_fetch(a, item, lane, cur);   // weights stream while x is prepared
+  gemv_fetch<true>(a, min(item, nitems - 1), lane, cur);   // weights stream while x is prepared
   gemv_prep_x(a, L);
   while (item < nitems) {
     const int nxt = item + stride;
     GemvItem nx;
-    if (nxt < nitems) gemv_fetch(a, nxt, lane, nx);
+    gemv_fetch<true>(a, min(nxt, nitems - 1), lane, nx);   // unconditional (see gemv_fetch)
     const float acc = gemv_item(a, L, cur, 0, lane);
     if (kg == 0) {
       gst(a.y + 16 * item + n, acc);

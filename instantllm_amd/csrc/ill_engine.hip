@@ -234,7 +234,8 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   // at least four k-steps per slice (the split depends on the matrix only, so 1-row and
   // 16-row passes sum the same partials in the same order)
   int S = 1;
-  // (QKV of q8 / f16: not split; 36 one-wave workgroups apply the epilogue themselves)
+  // (QKV of q8 / f16: K not split across workgroups; 36 two-wave workgroups, each wave half
+  // of K, apply the epilogue themselves)
   constexpr bool QKV1 = EPI == OP_QKV && FMT != 2;
   if (EPI != OP_LMH && !QKV1) S = std::max(1, std::min(std::min((256 + ntn - 1) / ntn, nsteps / 4), OP_MAXS));
   g.ksteps = (nsteps + S - 1) / S;
@@ -250,7 +251,7 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
     g.part = e->opart + ILL_OP_PART_SPLIT;
     hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, true>), grid, dim3(256), 0, e->stream, g);
   } else if constexpr (QKV1) {
-    hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, false, 1>), dim3(W.N / 32), dim3(64), 0, e->stream, g);
+    hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, false, 2>), dim3(W.N / 32), dim3(128), 0, e->stream, g);
   } else {
     hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI, 4>), grid, dim3(256), 0, e->stream, g);
   }

@@ -548,14 +548,18 @@ __device__ __forceinline__ v8h op_bvals(const BOp<FMT>& b, int j, int ks) {
 
 template <int FMT, int EPI, bool SILU, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
-  static_assert(NWV == 4 || (NWV == 1 && EPI == OP_QKV), "one-wave workgroups: the unsplit QKV GEMM");
+  // NWV 4: four waves, 32 columns each. NWV 2 (the unsplit QKV GEMM): two waves share 32
+  // columns and split the K steps in halves, added (wave 0's + wave 1's) before the
+  // epilogue, which wave 0 applies.
+  static_assert(NWV == 4 || (NWV == 2 && EPI == OP_QKV), "two-wave workgroups: the unsplit QKV GEMM");
+  constexpr bool KS2 = NWV == 2;
   constexpr int NT = 64 * NWV;
   const OpHdr hd = op_hdr(a.c);
   __shared__ __attribute__((aligned(16))) _Float16 As[16 * (OP_SMAXK + 8)];
   __shared__ uint64_t red[4][16];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
-  const int n0 = blockIdx.x * 32 * NWV, col0 = n0 + 32 * w;
+  const int n0 = blockIdx.x * (KS2 ? 32 : 32 * NWV), col0 = n0 + (KS2 ? 0 : 32 * w);
   // QKV: the rotary rows of this lane's rows 4 kg + r at the expected position (pos_hint + row)
   float2 cs[4];
   if constexpr (EPI == OP_QKV) {
@@ -565,13 +569,17 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
   }
   const int K = a.W.K;
   const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
-  const int ns = (ke - kb) / OP_BK, kw = ke - kb;
+  const int nsa = (ke - kb) / OP_BK, kw = ke - kb;
   const int lda = kw + 8;   // LDS row stride (halves)
+  // this wave's k-steps: all of the slice, or (KS2) its half
+  const int s_lo = KS2 ? (w == 0 ? 0 : nsa / 2) : 0;
+  const int ns = KS2 ? (w == 0 ? nsa / 2 : nsa - nsa / 2) : nsa;
+  const int kbw = kb + s_lo * OP_BK;   // the wave's first column
   constexpr int SD = OP_SDEPTH(FMT);
   BOp<FMT> ring[SD];
 #pragma unroll
   for (int d = 0; d < SD; d++) {
-    op_fetch_b<FMT>(a.W, col0, kb + min(d, ns - 1) * OP_BK, kg, n, ring[d]);
+    op_fetch_b<FMT>(a.W, col0, kbw + min(d, ns - 1) * OP_BK, kg, n, ring[d]);
     __builtin_amdgcn_sched_barrier(0);   // issue order = slot order (the waits count on it)
   }
   // A rows 0 .. M-1 of the slice into LDS (rows >= M are left as they are: their outputs
@@ -616,12 +624,12 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
       for (int ks = 0; ks < 2; ks++) bf[j][ks] = op_bvals<FMT>(ring[d], j, ks);
     if (refetch) {
       __builtin_amdgcn_sched_barrier(0);
-      op_fetch_b<FMT>(a.W, col0, kb + min(st + SD, ns - 1) * OP_BK, kg, n, ring[d]);
+      op_fetch_b<FMT>(a.W, col0, kbw + min(st + SD, ns - 1) * OP_BK, kg, n, ring[d]);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const v8h af = *(const v8h*)(As + n * lda + st * OP_BK + 16 * kg + 8 * ks);
+      const v8h af = *(const v8h*)(As + n * lda + (s_lo + st) * OP_BK + 16 * kg + 8 * ks);
 #pragma unroll
       for (int j = 0; j < 2; j++) acc[0][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j][ks], acc[0][j], 0, 0, 0);
     }
@@ -634,7 +642,22 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
 #pragma unroll
   for (int d = 0; d < SD - 1; d++)
     if (s0 + d < ns) kstep(d, s0 + d, false);
-  op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red, a.pos_hint, cs);
+  if constexpr (KS2) {
+    __shared__ v4f kacc[2][64];
+    if (w == 1) {
+      kacc[0][lane] = acc[0][0];
+      kacc[1][lane] = acc[0][1];
+    }
+    __syncthreads();
+    if (w == 1) return;
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[0][jj][r] = acc[0][jj][r] + kacc[jj][lane][r];
+    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, 0, kg, n, red, a.pos_hint, cs);
+  } else {
+    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red, a.pos_hint, cs);
+  }
 }
 
 // Split-K reduction: sum of the slices' partials in slice order, then the epilogue.

@@ -572,8 +572,8 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
   const int nsa = (ke - kb) / OP_BK, kw = ke - kb;
   const int lda = kw + 8;   // LDS row stride (halves)
   // this wave's k-steps: all of the slice, or (KS2) its half
-  const int s_lo = KS2 ? (w == 0 ? 0 : nsa / 2) : 0;
-  const int ns = KS2 ? (w == 0 ? nsa / 2 : nsa - nsa / 2) : nsa;
+  const int s_lo = KS2 ? w * nsa / NWV : 0;
+  const int ns = KS2 ? (w + 1) * nsa / NWV - s_lo : nsa;
   const int kbw = kb + s_lo * OP_BK;   // the wave's first column
   constexpr int SD = OP_SDEPTH(FMT);
   BOp<FMT> ring[SD];
@@ -643,17 +643,19 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
   for (int d = 0; d < SD - 1; d++)
     if (s0 + d < ns) kstep(d, s0 + d, false);
   if constexpr (KS2) {
-    __shared__ v4f kacc[2][64];
-    if (w == 1) {
-      kacc[0][lane] = acc[0][0];
-      kacc[1][lane] = acc[0][1];
+    __shared__ v4f kacc[NWV][2][64];
+    if (w > 0) {
+      kacc[w][0][lane] = acc[0][0];
+      kacc[w][1][lane] = acc[0][1];
     }
     __syncthreads();
-    if (w == 1) return;
+    if (w > 0) return;
 #pragma unroll
-    for (int jj = 0; jj < 2; jj++)
+    for (int ww = 1; ww < NWV; ww++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[0][jj][r] = acc[0][jj][r] + kacc[jj][lane][r];
+      for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[0][jj][r] = acc[0][jj][r] + kacc[ww][jj][lane][r];
     op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, 0, kg, n, red, a.pos_hint, cs);
   } else {
     op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red, a.pos_hint, cs);

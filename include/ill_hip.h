@@ -66,9 +66,15 @@ int ill_decode_step(ill_engine* e, int write_logits);
 int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t* toks, int write_logits);
 
 /* Record `nsteps` decode steps into one hipGraph; ill_launch_graph replays it. Steps after
- * the stop flag early-exit on the device (Shaders.swift:41). */
+ * the stop flag early-exit on the device (Shaders.swift:41). The device also sets the stop
+ * flag once a following pass of up to 16 rows would not fit in the context, and
+ * ill_set_state refuses a live state without that room, so replays never write K/V past
+ * max_context. A captured graph is dropped when tracing is switched on or off. */
 int ill_capture_steps(ill_engine* e, int nsteps);
 int ill_launch_graph(ill_engine* e);
+/* ill_launch_graph with encodeDecodeStep's writeLogits (Engine.swift:605-609) for every
+ * recorded step: afterwards ill_read_logits(e, 0, ..) holds the last executed step's logits. */
+int ill_launch_graph_logits(ill_engine* e, int write_logits);
 
 int ill_sync(ill_engine* e);
 

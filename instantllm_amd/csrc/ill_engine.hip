@@ -119,6 +119,7 @@ struct ill_engine {
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   int graph_steps = 0;
+  uint64_t passes_since_clear = 0;   // passes launched since the tagged buffers were cleared
   int pos_hint = 0;   // the State's pos as the host last knew it: picks the attention split
   IllCtl hctl{};
   IllPassArgs args{};
@@ -150,7 +151,10 @@ int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, in
   return 0;
 }
 
+int count_passes(ill_engine* e, int n);
+
 int launch(ill_engine* e, int T) {
+  if (int rc = count_passes(e, 1)) return rc;
   HCK(hipEventRecord(e->ev0, e->stream));
   if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
   else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
@@ -164,8 +168,14 @@ int check_err(ill_engine* e) {
   HCK(hipMemcpyAsync(&err, &e->ctl->err, 4, hipMemcpyDeviceToHost, e->stream));
   HCK(hipStreamSynchronize(e->stream));
   if (err) {
-    // an abandoned pass leaves partial sums behind: clear both accumulator banks
+    // An abandoned pass leaves partial sums behind (clear both accumulator banks) and tagged
+    // words of its own epoch in the published codings and the lm_head partials: the epoch
+    // moves on by two (the same bank parity), so the next pass's tags differ from them.
+    uint32_t ep = 0;
+    hipMemcpy(&ep, &e->ctl->epoch, 4, hipMemcpyDeviceToHost);
+    ep += 2;
     int32_t zero[3] = {0, 0, 0};
+    hipMemcpy(&e->ctl->epoch, &ep, 4, hipMemcpyHostToDevice);
     hipMemcpy(&e->ctl->err, zero, 4, hipMemcpyHostToDevice);
     hipMemcpy(&e->ctl->bank_rows[0], zero, 8, hipMemcpyHostToDevice);
     hipMemset(e->acc, 0, e->acc_bytes);
@@ -173,6 +183,30 @@ int check_err(ill_engine* e) {
     return fail(ILL_E_TIMEOUT, "device wait timed out (site %d); the pass was abandoned", err);
   }
   return 0;
+}
+
+// Tags are 32-bit (epoch * 32 + slot + 1), so they repeat every 2^27 passes. Words that
+// are not rewritten for that long (rows 1-15 of the published codings, written by 16-row
+// passes only) could then pass a tag check: the host clears both tagged buffers once
+// every ILL_TAG_CLEAR_PASSES launched passes, long before a tag can come round again.
+#define ILL_TAG_CLEAR_PASSES (1u << 24)
+int count_passes(ill_engine* e, int n) {
+  e->passes_since_clear += (uint64_t)n;
+  if (e->passes_since_clear < ILL_TAG_CLEAR_PASSES) return 0;
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipMemsetAsync(e->pub, 0, (size_t)ILL_PUB_WORDS * 8, e->stream));
+  HCK(hipMemsetAsync(e->lmp, 0, (size_t)ILL_WG * 16 * 2 * 8, e->stream));
+  HCK(hipStreamSynchronize(e->stream));
+  e->passes_since_clear = (uint64_t)n;
+  return 0;
+}
+
+void drop_graph(ill_engine* e) {
+  if (e->gexec) hipGraphExecDestroy(e->gexec);
+  if (e->graph) hipGraphDestroy(e->graph);
+  e->gexec = nullptr;
+  e->graph = nullptr;
+  e->graph_steps = 0;
 }
 
 int read_state(ill_engine* e, IllState* s) {
@@ -679,6 +713,13 @@ int ill_set_state(ill_engine* e, const int32_t state[16]) {
   if (s.maxctx != e->maxctx) s.maxctx = e->maxctx;
   if (s.maxsteps > e->maxsteps || s.maxsteps < 1) return fail(ILL_E_ARG, "maxsteps %d outside 1..%d", s.maxsteps, e->maxsteps);
   if (s.pos < 0 || s.pos >= e->maxctx) return fail(ILL_E_ARG, "pos %d outside the context", s.pos);
+  if (!s.done) {
+    // a live state must let the commits record into out_tokens and a pass of up to 16 rows
+    // at pos stay inside the context (the device keeps both true after every commit)
+    if (s.step < 0 || s.step >= s.maxsteps) return fail(ILL_E_ARG, "step %d outside 0..%d", s.step, s.maxsteps - 1);
+    if (s.n < 1 || s.n > e->maxctx) return fail(ILL_E_ARG, "n %d outside 1..%d", s.n, e->maxctx);
+    if (s.pos + ILL_MAXT > e->maxctx) return fail(ILL_E_ARG, "pos %d leaves no room for a pass in the context %d", s.pos, e->maxctx);
+  }
   HCK(hipMemcpyAsync(e->st, &s, sizeof s, hipMemcpyHostToDevice, e->stream));
   HCK(hipStreamSynchronize(e->stream));
   e->pos_hint = s.pos;
@@ -793,14 +834,7 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
 
 int ill_capture_steps(ill_engine* e, int nsteps) {
   if (!e || nsteps < 1) return fail(ILL_E_ARG, "bad step count");
-  if (e->gexec) {
-    hipGraphExecDestroy(e->gexec);
-    e->gexec = nullptr;
-  }
-  if (e->graph) {
-    hipGraphDestroy(e->graph);
-    e->graph = nullptr;
-  }
+  drop_graph(e);
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   const int base = e->pos_hint;
@@ -816,12 +850,16 @@ int ill_capture_steps(ill_engine* e, int nsteps) {
   return ILL_OK;
 }
 
-int ill_launch_graph(ill_engine* e) {
+int ill_launch_graph(ill_engine* e) { return ill_launch_graph_logits(e, 0); }
+
+int ill_launch_graph_logits(ill_engine* e, int write_logits) {
   if (!e || !e->gexec) return fail(ILL_E_ARG, "no captured graph");
-  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
+  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits ? 1 : 0, 1);
   if (rc) return rc;
+  if ((rc = count_passes(e, e->graph_steps))) return rc;
   HCK(hipGraphLaunch(e->gexec, e->stream));
   e->pos_hint += e->graph_steps;
+  if (write_logits) e->logits_rows_valid = 1;
   return ILL_OK;
 }
 
@@ -883,6 +921,9 @@ int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v
 int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk, int32_t* out, int* n_out, float* logits_out) {
   if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
   if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
+  // Engine.swift:934 (tokens + maxNew <= maxContext), with the 16-slot margin of a pass
+  if (ntok + max_new + ILL_MAXT > e->maxctx)
+    return fail(ILL_E_ARG, "prompt of %d tokens + %d new exceeds the context %d (less a 16-slot pass margin)", ntok, max_new, e->maxctx);
   if (chunk < 1) chunk = 1;
   *n_out = 0;
   int rc;
@@ -933,6 +974,7 @@ int ill_time_graph(ill_engine* e, int iters, float* ms) {
   HCK(hipEventCreate(&b));
   int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
   if (rc) return rc;
+  if ((rc = count_passes(e, iters * e->graph_steps))) return rc;
   HCK(hipEventRecord(a, e->stream));
   for (int i = 0; i < iters; i++) HCK(hipGraphLaunch(e->gexec, e->stream));
   HCK(hipEventRecord(b, e->stream));
@@ -946,6 +988,9 @@ int ill_time_graph(ill_engine* e, int iters, float* ms) {
 int ill_trace_enable(ill_engine* e, int on) {
   if (!e) return fail(ILL_E_ARG, "null engine");
   HCK(hipStreamSynchronize(e->stream));
+  // a captured graph holds the trace pointer in its kernel arguments: it is dropped
+  // whenever the trace buffer comes or goes (capture again after toggling)
+  if ((on != 0) != (e->args.trace != nullptr)) drop_graph(e);
   if (on && !e->args.trace) {
     void* p = nullptr;
     HCK(hipMalloc(&p, (size_t)ILL_WG * ILL_TRACE_SLOTS * 8));

@@ -1607,7 +1607,9 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
       st->step = step + 1;
       st->pos = H.pos + H.nrows;
       st->n = 1;
-      if (tok == H.eos0 || tok == H.eos1 || step + 1 >= H.maxsteps) st->done = 1;
+      // stop tokens and maxsteps (Shaders.swift:231-233); also stop before a following pass
+      // of up to 16 rows would write K/V past the end of the context
+      if (tok == H.eos0 || tok == H.eos1 || step + 1 >= H.maxsteps || H.pos + H.nrows + ILL_MAXT > a.maxctx) st->done = 1;
       a.ptoks[0] = tok;
       a.ctl->last_tok = tok;
     } else {
@@ -1647,7 +1649,7 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
       st->n = 1;
       st->nver = 1;
       st->tree = 0;
-      if (stop) st->done = 1;
+      if (stop || H.pos + m + 1 + ILL_MAXT > a.maxctx) st->done = 1;
       a.ptoks[0] = last;
       a.ctl->last_tok = last;
       C.npath = H.mode == ILL_MODE_TREE ? m : 0;

@@ -56,6 +56,7 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_verify_pass": (C.c_int, [P, C.c_int, ip, ip, C.c_int]),
         "ill_capture_steps": (C.c_int, [P, C.c_int]),
         "ill_launch_graph": (C.c_int, [P]),
+        "ill_launch_graph_logits": (C.c_int, [P, C.c_int]),
         "ill_sync": (C.c_int, [P]),
         "ill_out_tokens": (ip, [P]),
         "ill_reset_out_tokens": (C.c_int, [P]),
@@ -153,8 +154,8 @@ class Engine:
     def capture_steps(self, n: int):
         self._check(self.lib.ill_capture_steps(self.h, n))
 
-    def launch_graph(self):
-        self._check(self.lib.ill_launch_graph(self.h))
+    def launch_graph(self, write_logits: bool = False):
+        self._check(self.lib.ill_launch_graph_logits(self.h, int(write_logits)))
 
     def sync(self):
         self._check(self.lib.ill_sync(self.h))

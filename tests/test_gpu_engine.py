@@ -102,7 +102,59 @@ def _ctx(engine, rng, n):
     return ctx, engine.get_state()
 
 
-@pytest.mark.parametrize("prefix", [100, 300])
+def test_decode_across_a_chunk_end(engine, q4_small):
+    """Decode steps at positions 58-67: the chunk holding the new position runs to its
+    last slots (pos % 64 in 58-63) and then a new chunk starts."""
+    _, m = q4_small
+    rng = np.random.default_rng(13)
+    prompt = [int(t) for t in rng.integers(0, VOCAB, size=58)]
+    engine.reset_out_tokens()
+    engine.set_state(pos=0, n=len(prompt), maxsteps=64, eos=(-5, -5))
+    engine.prefill(prompt, write_logits=True)
+    cache = m.new_cache(128)
+    assert metrics.rel_l2(engine.read_logits(0), m.forward(prompt, cache)) <= REL_L2_TOL
+    tok = int(engine.out_tokens()[0])
+    for s in range(10):
+        engine.decode_step(write_logits=True)
+        lg = engine.read_logits(0)
+        assert metrics.rel_l2(lg, m.forward([tok], cache)) <= REL_L2_TOL, s
+        tok = int(engine.out_tokens()[s + 1])
+
+
+def test_overlong_requests_are_refused(engine):
+    """Engine.swift:934: a request that cannot fit in the context is refused before any
+    launch; a live state must leave room for a 16-row pass."""
+    from instantllm_amd.engine import IllError, ILL_E_ARG
+    with pytest.raises(IllError) as ei:
+        engine.generate([1] * 100, max_new=engine.max_context - 100)
+    assert ei.value.code == ILL_E_ARG
+    for bad in (dict(pos=engine.max_context - 8), dict(step=64), dict(step=-1), dict(n=0), dict(n=engine.max_context + 1)):
+        kw = dict(pos=0, n=1, maxsteps=64)
+        kw.update(bad)
+        with pytest.raises(IllError):
+            engine.set_state(**kw)
+    # a done state is accepted whatever its counters (the host parks a finished request)
+    engine.set_state(pos=engine.max_context - 8, n=1, maxsteps=64, done=1)
+
+
+def test_decode_stops_at_the_context_end(engine):
+    """Steps launched past the context early-exit: the commit sets the stop flag once a
+    following pass would not fit (pos + 16 > max_context)."""
+    rng = np.random.default_rng(14)
+    n = engine.max_context - 24
+    prompt = [int(t) for t in rng.integers(0, VOCAB, size=n)]
+    engine.reset_out_tokens()
+    engine.set_state(pos=0, n=n, maxsteps=200, eos=(-5, -5))
+    engine.prefill(prompt)
+    for _ in range(20):
+        engine.decode_step()
+    st = engine.get_state()
+    # the step at pos = max_context - 16 is the last one that runs
+    assert st["done"] == 1 and st["pos"] == engine.max_context - 15, st
+    assert st["step"] == 1 + (engine.max_context - 16 - n) + 1
+
+
+@pytest.mark.parametrize("prefix", [60, 100, 300])
 def test_tree_rows_bit_identical_to_sequential_steps(engine, prefix):
     """Config 3 invariant: every tree row's logits equal, bit for bit, the logits of the
     same token decoded as a 1-row step after its ancestors."""

@@ -1,4 +1,4 @@
-"""GPU parity of the layer-by-layer path through the C ABI: q8 (symmetric group-64) and f16
+"""GPU parity of the layer-by-layer path through the C ABI: q8 (symmetric, groups of 64 and 32) and f16
 models for every pass shape, and q4 prompts longer than 16 tokens (prefill chunks on the
 MFMA GEMMs). Small seeded models (3 layers, vocabulary 4096, real widths) against the fp32
 oracle on the same dequantized weights. Tolerances as for q4: per-step logits relative L2
@@ -23,13 +23,16 @@ def log(*a):
     print(*a, flush=True)
 
 
-@pytest.fixture(scope="module", params=[F.FMT_Q8, F.FMT_F16, F.FMT_Q4], ids=["q8", "f16", "q4"])
+# q8 in the BASELINE's group of 64 and in the reference converter's own group of 32
+# (Convert.swift:254-282; the engine reads the group size from the scale tensor's size)
+@pytest.fixture(scope="module", params=[(F.FMT_Q8, 64), (F.FMT_Q8, 32), (F.FMT_F16, 64), (F.FMT_Q4, 64)],
+                ids=["q8", "q8g32", "f16", "q4"])
 def model(request, tmp_path_factory):
     from instantllm_amd.engine import Engine
-    fmt = request.param
-    path = str(tmp_path_factory.mktemp(f"fmt{fmt}") / "m.ill")
-    synth.build_model(path, fmt, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB))
-    log(f"engine: create small model format {fmt}")
+    fmt, group = request.param
+    path = str(tmp_path_factory.mktemp(f"fmt{fmt}g{group}") / "m.ill")
+    synth.build_model(path, fmt, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB), q8_group=group)
+    log(f"engine: create small model format {fmt} group {group}")
     e = Engine(path, max_context=1024, max_pass=16, max_steps=256)
     yield fmt, e, qwen.Model(illread.load(path))
     e.close()

@@ -129,6 +129,17 @@ typedef struct ill_gemv ill_gemv;
 int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* scales, int copies, ill_gemv** out);
 int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, float* y, int32_t* argmax, float* us_per_iter);
 int ill_gemv_info(const ill_gemv* g, int* slices, int* blocks_per_slice, int64_t* bytes_per_copy);
+
+/* No counterpart in the reference: ill_gemv_run for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). One product on weight copy `copy` of g, enqueued on `stream` (a hipStream_t;
+ * NULL: g's own stream) and not waited for. x [K], gamma [K] (NULL: plain input), y [rows]
+ * and argmax (one int32) are device pointers owned by the caller; y may be NULL when
+ * argmax is not (the product then lives in the library's per-GPU scratch array, at most
+ * 262144 rows; larger products need a y buffer). The call allocates nothing: the argmax
+ * keys live in that same fixed scratch array, shared by every call on the GPU, so calls
+ * that overlap on one GPU race. Same arithmetic and results as ill_gemv_run. */
+int ill_gemv_run_noalloc(ill_gemv* g, int copy, const float* x, const float* gamma, float* y, int32_t* argmax, void* stream);
 int ill_gemv_destroy(ill_gemv* g);
 
 #ifdef __cplusplus

@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1019,7 +1020,51 @@ int ill_last_pass_ms(ill_engine* e, float* ms) {
   return ILL_OK;
 }
 
+}  // extern "C"
+
 // ---- stand-alone q4 GEMV (microbench of the decode step's matrix-vector product) -------
+// Scratch of the allocation-free entry point ill_gemv_run_noalloc: the argmax keys
+// [ILL_SCRATCH_KEYS] and, for callers that pass no y, the product itself (at most
+// ILL_SCRATCH_YMAX rows). Each GPU holds its own copy of this array until the process ends;
+// host code uses the per-device address from hipGetSymbolAddress (never the array's name).
+// Every call on a GPU shares that GPU's copy, which keeps the last call's contents (the keys
+// are cleared by a fill kernel at the start of each call): calls that overlap on one GPU
+// race.
+#define ILL_SCRATCH_KEYS 2
+#define ILL_SCRATCH_YMAX 262144
+static __device__ __align__(256) uint64_t scratch[ILL_SCRATCH_KEYS + ILL_SCRATCH_YMAX / 2];
+
+namespace {
+#define ILL_MAX_DEVICES 64
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_dev[ILL_MAX_DEVICES] = {};
+
+// Address of this GPU's scratch array (the current device), looked up once per device.
+int scratch_for_current_device(uint64_t** out) {
+  int dev = 0;
+  HCK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= ILL_MAX_DEVICES) return fail(ILL_E_HIP, "device %d outside 0..%d", dev, ILL_MAX_DEVICES - 1);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    HCK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(ILL_E_HIP, "no device address for the scratch array");
+    g_scratch_dev[dev] = (uint64_t*)p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
+__global__ void gemv_key_clear_kernel(uint64_t* key) {
+  if (threadIdx.x < ILL_SCRATCH_KEYS) gst(key + threadIdx.x, (uint64_t)0);
+}
+__global__ void gemv_key_finish_kernel(const uint64_t* key, int32_t* amax) {
+  if (threadIdx.x == 0) gst(amax, (int32_t)(0xFFFFFFFFu - (uint32_t)(gld(key) & 0xFFFFFFFFu)));
+}
+}  // namespace
+
+extern "C" {
+
 struct ill_gemv {
   int rows = 0, K = 0, nb = 0, bps = 1, ks = 1, copies = 0;
   std::vector<uint8_t*> w;
@@ -1028,6 +1073,7 @@ struct ill_gemv {
   float* gamma = nullptr;
   float* y = nullptr;
   uint64_t* key = nullptr;
+  uint64_t* scratch = nullptr;   // this GPU's scratch array (ill_gemv_run_noalloc)
   hipStream_t stream = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
 };
@@ -1079,6 +1125,7 @@ int ill_gemv_create(int rows, int K, const uint8_t* codes, const uint32_t* sb, i
   std::vector<uint32_t> hs((size_t)ntile * g->nb * 32);
   repack_rows(codes, sb, K, order, hw.data(), hs.data());
   if (hipSetDevice(0) != hipSuccess) return bad(fail(ILL_E_HIP, "no HIP device"));
+  if (int rc = scratch_for_current_device(&g->scratch)) return bad(rc);
   for (int c = 0; c < copies; c++) {
     uint8_t* pw = nullptr;
     uint32_t* ps = nullptr;
@@ -1152,6 +1199,38 @@ int ill_gemv_run(ill_gemv* g, const float* x, const float* gamma, int iters, flo
     HCK(hipMemcpy(&k, g->key + (par ^ 1), 8, hipMemcpyDeviceToHost));
     *amax = (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
   }
+  return ILL_OK;
+}
+
+int ill_gemv_run_noalloc(ill_gemv* g, int copy, const float* x, const float* gamma, float* y, int32_t* amax, void* stream) {
+  if (!g || !x) return fail(ILL_E_ARG, "null gemv or x");
+  if (copy < 0 || copy >= g->copies) return fail(ILL_E_ARG, "weight copy %d outside 0..%d", copy, g->copies - 1);
+  if (!y && !amax) return fail(ILL_E_ARG, "nothing to compute: pass y, argmax or both");
+  if (!y && g->rows > ILL_SCRATCH_YMAX)
+    return fail(ILL_E_ARG, "%d rows exceed the %d-row scratch: pass a y buffer", g->rows, ILL_SCRATCH_YMAX);
+  hipStream_t st = stream ? (hipStream_t)stream : g->stream;
+  IllGemvArgs a{};
+  a.w = g->w[copy];
+  a.s = g->s[copy];
+  a.x = x;
+  a.gamma = gamma;
+  a.rows = g->rows;
+  a.K = g->K;
+  a.bps = g->bps;
+  a.ks = g->ks;
+  a.y = y ? y : (float*)(g->scratch + ILL_SCRATCH_KEYS);
+  a.key = amax ? g->scratch : nullptr;
+  a.par = 0;
+  if (amax) hipLaunchKernelGGL(gemv_key_clear_kernel, dim3(1), dim3(64), 0, st, g->scratch);
+  if (g->ks == 1) {
+    hipLaunchKernelGGL(ill_gemv_q4_kernel, dim3(ILL_WG), dim3(ILL_WG_THREADS), 0, st, a);
+  } else {
+    const int tpr = ILL_WAVES / g->ks;
+    const int grid = std::min(ILL_WG, (g->rows / 16 + tpr - 1) / tpr);
+    hipLaunchKernelGGL(ill_gemv_q4_tiles_kernel, dim3(grid), dim3(ILL_WG_THREADS), 0, st, a);
+  }
+  if (amax) hipLaunchKernelGGL(gemv_key_finish_kernel, dim3(1), dim3(64), 0, st, (const uint64_t*)g->scratch, amax);
+  HCK(hipGetLastError());
   return ILL_OK;
 }
 

@@ -72,6 +72,7 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_gemv_run": (C.c_int, [P, C.POINTER(F32), C.POINTER(F32), C.c_int, C.POINTER(F32), ip, C.POINTER(F32)]),
         "ill_gemv_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
         "ill_gemv_destroy": (C.c_int, [P]),
+        "ill_gemv_run_noalloc": (C.c_int, [P, C.c_int, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -245,6 +246,13 @@ class Gemv:
         if rc != ILL_OK:
             raise IllError(rc, self.lib.ill_last_error().decode())
         return y, (int(am.value) if argmax else None), float(us.value)
+
+    def run_noalloc(self, x_dev: int, gamma_dev: int | None, y_dev: int | None, argmax_dev: int | None,
+                    copy: int = 0, stream: int | None = None):
+        """ill_gemv_run_noalloc: device addresses in, nothing allocated, not waited for."""
+        rc = self.lib.ill_gemv_run_noalloc(self.h, copy, x_dev, gamma_dev, y_dev, argmax_dev, stream)
+        if rc != ILL_OK:
+            raise IllError(rc, self.lib.ill_last_error().decode())
 
     def info(self) -> dict:
         ks, bps, nbytes = C.c_int(0), C.c_int(0), C.c_int64(0)

@@ -45,8 +45,18 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
 # a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (167,467.94 x 2 + 16,358.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 359_725_120
+# (167,577.06 x 2 + 16,358.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 359_948_608
+# MFMA utilisation of the 16-row verify pass and of the prefill GEMMs, from rocprofv3
+# SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
+MFMA_COUNTERS = {
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0062, "int8_TOPs": 27.7},
+    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0104, "int8_TOPs": 48.1},
+    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.143, "f16_TFLOPs": 360.3},
+    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.109, "f16_TFLOPs": 275.1},
+    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.042, "f16_TFLOPs": 105.3},
+    "prefill attention (512 rows)": {"mfma_busy": 0.060, "f16_TFLOPs": 150.5},
+}
 
 
 def step_bytes(L: float) -> float:
@@ -321,6 +331,8 @@ def main() -> int:
                              + "traffic = HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE "
                              "(profiles/pass_kernel_q4_decode_config2.md)"},
     }
+    line["mfma_counters"] = {"source": "profiles/pass_kernel_q4_decode_config2.md, "
+                                       "profiles/layer_by_layer_q8_f16_config4.md", **MFMA_COUNTERS}
     if not args.no_gemv:
         line["gemv_config1"] = gemv_config1()
     if not args.no_config4:

@@ -142,6 +142,18 @@ int ill_gemv_info(const ill_gemv* g, int* slices, int* blocks_per_slice, int64_t
 int ill_gemv_run_noalloc(ill_gemv* g, int copy, const float* x, const float* gamma, float* y, int32_t* argmax, void* stream);
 int ill_gemv_destroy(ill_gemv* g);
 
+/* The converter's quantizers (Converter.quantizeQ4Raw / quantGroup and quantizeQ8,
+ * Sources/Engine/Convert.swift:252-370), host code that needs no GPU. w is a row-major
+ * float32 [rows][cols] matrix; `threads` CPU threads split the rows (any count gives the
+ * same bytes).
+ * q4: packed [rows][cols/2] codes (column 2j in the low nibble of byte j) and sb
+ * [rows][cols/64][2] f16 bits (scale, bias): per 64 columns the clipped-range search with a
+ * least-squares refit that keeps the lowest squared error after f16 rounding.
+ * q8: codes [rows][cols] and scales [rows][cols/group] f16 bits, group 32 (the reference) or
+ * 64: symmetric, scale = f16(amax/127) raised one ulp when a code would leave -127..127. */
+int ill_quantize_q4(const float* w, int64_t rows, int cols, uint8_t* packed, uint16_t* sb, int threads);
+int ill_quantize_q8(const float* w, int64_t rows, int cols, int group, int8_t* codes, uint16_t* scales, int threads);
+
 #ifdef __cplusplus
 }
 #endif

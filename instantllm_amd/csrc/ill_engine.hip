@@ -22,6 +22,7 @@
 #include "ill_pass.h"
 #include "ill_gemv.h"
 #include "ill_ops.h"
+#include "ill_quant.h"
 
 namespace {
 
@@ -1231,6 +1232,19 @@ int ill_gemv_run_noalloc(ill_gemv* g, int copy, const float* x, const float* gam
   }
   if (amax) hipLaunchKernelGGL(gemv_key_finish_kernel, dim3(1), dim3(64), 0, st, (const uint64_t*)g->scratch, amax);
   HCK(hipGetLastError());
+  return ILL_OK;
+}
+
+int ill_quantize_q4(const float* w, int64_t rows, int cols, uint8_t* packed, uint16_t* sb, int threads) {
+  if (!w || !packed || !sb || rows < 1 || cols < 64 || cols % 64) return fail(ILL_E_ARG, "q4 quantize: bad shape %lld x %d", (long long)rows, cols);
+  illq::parallel_rows(rows, threads, [&](int64_t a, int64_t b) { illq::quant_rows_q4(w, a, b, cols, packed, sb); });
+  return ILL_OK;
+}
+
+int ill_quantize_q8(const float* w, int64_t rows, int cols, int group, int8_t* codes, uint16_t* scales, int threads) {
+  if (!w || !codes || !scales || rows < 1 || (group != 32 && group != 64) || cols < group || cols % group)
+    return fail(ILL_E_ARG, "q8 quantize: bad shape %lld x %d or group %d", (long long)rows, cols, group);
+  illq::parallel_rows(rows, threads, [&](int64_t a, int64_t b) { illq::quant_rows_q8(w, a, b, cols, group, codes, scales); });
   return ILL_OK;
 }
 

@@ -73,6 +73,8 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_gemv_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
         "ill_gemv_destroy": (C.c_int, [P]),
         "ill_gemv_run_noalloc": (C.c_int, [P, C.c_int, P, P, P, P, P]),
+        "ill_quantize_q4": (C.c_int, [C.POINTER(F32), C.c_int64, C.c_int, C.POINTER(C.c_uint8), C.POINTER(C.c_uint16), C.c_int]),
+        "ill_quantize_q8": (C.c_int, [C.POINTER(F32), C.c_int64, C.c_int, C.c_int, C.POINTER(C.c_int8), C.POINTER(C.c_uint16), C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -269,3 +271,37 @@ class Gemv:
             self.close()
         except Exception:
             pass
+
+
+def _threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)) or 1)
+
+
+def quantize_q4(w: np.ndarray, threads: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """The converter's q4 quantizer (Convert.swift:286-370) in libillhip.so (CPU code).
+    Returns (packed u8 [rows, cols/2], (scale, bias) f16 [rows, cols/64, 2])."""
+    lib = load_library()
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    packed = np.empty((rows, cols // 2), np.uint8)
+    sb = np.empty((rows, cols // 64, 2), np.uint16)
+    rc = lib.ill_quantize_q4(_ptr(w, C.c_float), rows, cols, _ptr(packed, C.c_uint8), _ptr(sb, C.c_uint16),
+                             threads or _threads())
+    if rc != ILL_OK:
+        raise IllError(rc, lib.ill_last_error().decode())
+    return packed, sb.view(np.float16)
+
+
+def quantize_q8(w: np.ndarray, group: int = 32, threads: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """The converter's q8 quantizer (Convert.swift:252-282): (codes i8 [rows, cols],
+    scales f16 [rows, cols/group])."""
+    lib = load_library()
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    codes = np.empty((rows, cols), np.int8)
+    sc = np.empty((rows, cols // group), np.uint16)
+    rc = lib.ill_quantize_q8(_ptr(w, C.c_float), rows, cols, group, _ptr(codes, C.c_int8), _ptr(sc, C.c_uint16),
+                             threads or _threads())
+    if rc != ILL_OK:
+        raise IllError(rc, lib.ill_last_error().decode())
+    return codes, sc.view(np.float16)

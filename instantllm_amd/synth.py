@@ -6,13 +6,13 @@ There is no network, so every model the engine runs is generated here from a see
 holds exactly the same values as the full model in the tensors they share.
 
 Distributions: matrices N(0, 0.02) rounded to f16, QKV biases
-N(0, 0.02), RMSNorm weights N(1, 0.1). q4 and q8 models quantize those float weights
-(`quantize_q4`, `quantize_q8`); the CPU oracle consumes the dequantized values, so any
-valid encoding is a fair test of the kernels.
-
-The quantizers are deliberately simple (min/max affine for q4, absmax for q8). The
-reference's clip-search + least-squares q4 refit (`Sources/Engine/Convert.swift:290-370`)
-only changes which codes are chosen, not the format the kernels read.
+N(0, 0.02), RMSNorm weights N(1, 0.1). q4 and q8 models quantize those float weights with
+the reference converter's own quantizers (`quantizer="reference"`, the default: the
+clipped-range search with a least-squares refit of `Sources/Engine/Convert.swift:286-370`
+and the symmetric q8 of `:252-282`, run by libillhip.so's `ill_quantize_q4` /
+`ill_quantize_q8`), so the kernels see the code distributions a converted checkpoint has.
+`quantizer="minmax"` selects the plain min/max affine q4 (`quantize_q4`) instead. The CPU
+oracle consumes the dequantized values either way.
 """
 from __future__ import annotations
 
@@ -133,23 +133,33 @@ def quantize_q8(w: np.ndarray, group: int = 64) -> tuple[np.ndarray, np.ndarray]
     return q, s16
 
 
-def _emit_matrix(fmt: int, w: np.ndarray, q8_group: int) -> tuple[bytes, bytes]:
+def _emit_matrix(fmt: int, w: np.ndarray, q8_group: int, quantizer: str = "reference") -> tuple[bytes, bytes]:
+    if quantizer not in ("reference", "minmax"):
+        raise ValueError(f"unknown quantizer {quantizer!r}")
     if fmt == F.FMT_Q4:
-        p, sb = quantize_q4(w)
+        if quantizer == "reference":
+            from .engine import quantize_q4 as lib_q4
+            p, sb = lib_q4(w)
+        else:
+            p, sb = quantize_q4(w)
         return p.tobytes(), sb.astype("<f2").tobytes()
     if fmt == F.FMT_Q8:
-        q, sc = quantize_q8(w, q8_group)
+        if quantizer == "reference":
+            from .engine import quantize_q8 as lib_q8
+            q, sc = lib_q8(w, q8_group)
+        else:
+            q, sc = quantize_q8(w, q8_group)
         return q.tobytes(), sc.astype("<f2").tobytes()
     return w.astype("<f2").tobytes(), b""
 
 
 def build_model(path: str, fmt: int, seed: int, shape: ModelShape = ModelShape(),
-                q8_group: int = 64) -> int:
+                q8_group: int = 64, quantizer: str = "reference") -> int:
     """Generate the seeded model and write it as an `.ill` v1 file. Returns its size."""
     tensors: dict[int, bytes | np.ndarray] = {}
     wparts, sparts = [], []
     for chunk in float_embed_chunks(seed, shape):
-        w, sb = _emit_matrix(fmt, chunk, q8_group)
+        w, sb = _emit_matrix(fmt, chunk, q8_group, quantizer)
         wparts.append(w)
         sparts.append(sb)
     tensors[F.EMBED], tensors[F.EMBED_SB] = b"".join(wparts), b"".join(sparts)
@@ -165,11 +175,11 @@ def build_model(path: str, fmt: int, seed: int, shape: ModelShape = ModelShape()
         bias = np.concatenate([t["bq"], t["bk"], t["bv"]])
         tensors[L(F.BQKV)] = bias[qo].astype("<f4")
         qkv = np.concatenate([t["wq"], t["wk"], t["wv"]], axis=0)[qo]
-        tensors[L(F.WQKV)], tensors[L(F.WQKV_SB)] = _emit_matrix(fmt, qkv, q8_group)
-        tensors[L(F.WO)], tensors[L(F.WO_SB)] = _emit_matrix(fmt, t["wo"], q8_group)
+        tensors[L(F.WQKV)], tensors[L(F.WQKV_SB)] = _emit_matrix(fmt, qkv, q8_group, quantizer)
+        tensors[L(F.WO)], tensors[L(F.WO_SB)] = _emit_matrix(fmt, t["wo"], q8_group, quantizer)
         gu = np.concatenate([t["wg"], t["wu"]], axis=0)[go]
-        tensors[L(F.WGU)], tensors[L(F.WGU_SB)] = _emit_matrix(fmt, gu, q8_group)
-        tensors[L(F.WD)], tensors[L(F.WD_SB)] = _emit_matrix(fmt, t["wd"], q8_group)
+        tensors[L(F.WGU)], tensors[L(F.WGU_SB)] = _emit_matrix(fmt, gu, q8_group, quantizer)
+        tensors[L(F.WD)], tensors[L(F.WD_SB)] = _emit_matrix(fmt, t["wd"], q8_group, quantizer)
     return F.write_ill(path, fmt, tensors, shape.layers)
 
 
@@ -230,7 +240,8 @@ def cached_model(fmt: int, seed: int, shape: ModelShape = ModelShape(), director
     d = directory or os.environ.get("ILL_MODEL_DIR", "/tmp/ill_models")
     os.makedirs(d, exist_ok=True)
     tag = "" if shape == ModelShape() else f"_L{shape.layers}_V{shape.vocab}"
-    p = os.path.join(d, f"qwen05b_fmt{fmt}_seed{seed}{tag}.ill")
+    qtag = "_rq" if fmt != F.FMT_F16 else ""   # the reference converter's quantizers
+    p = os.path.join(d, f"qwen05b_fmt{fmt}_seed{seed}{tag}{qtag}.ill")
     if not os.path.exists(p):
         tmp = p + f".tmp{os.getpid()}"
         build_model(tmp, fmt, seed, shape=shape)

@@ -99,6 +99,43 @@ int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v
 int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk,
                  int32_t* out, int* n_out, float* logits_out);
 
+/* ---- Speculative decoding with on-device drafting (k_commit_spec, Shaders.swift:246-418) ----
+ * With the State's tspec = T > 1, every commit of a prefill or verify pass is speculative: it
+ * accepts the longest prefix of the pass's drafts that equals the rows' argmaxes, commits
+ * those tokens, then drafts up to T - 1 tokens for the next pass on the device
+ * (self-repetition of the output, then the n-gram table, then prompt lookup;
+ * Shaders.swift:367-412) and sets up that pass as a chain over [last token, drafts...].
+ * The tokens committed equal plain greedy decoding's (every row's logits equal a 1-row
+ * step's, bit for bit). The State's passes / accepted fields count passes and accepted
+ * drafts (Engine.swift:959). */
+
+/* Engine.loadNGram (Engine.swift:747-753): an n-gram draft table in the NGramTable layout
+ * (NGram.swift:1-59): 2^20 slots of {u64 key, i32 next, u16 count, u16 total}, 16 MiB.
+ * table NULL (or bytes 0) unloads it. */
+int ill_load_ngram(ill_engine* e, const void* table, int64_t bytes);
+
+/* The prompt-lookup context of the drafter (promptRecent, Engine.swift:125, :939-942): the
+ * last <= 256 of the request's prompt tokens. ill_generate_spec sets it itself. */
+int ill_set_prompt(ill_engine* e, const int32_t* toks, int n);
+
+/* One verify pass over the rows the last speculative commit drafted (encodeSpecPass /
+ * encodeWidePass + k_commit_spec, Engine.swift:524-579), launched and waited for. */
+int ill_spec_pass(ill_engine* e, int write_logits);
+
+/* Record `npasses` such passes into one hipGraph (q4 models): each pass takes its rows from
+ * the commit before it, so the graph chains verify passes without the host; passes after
+ * the stop flag early-exit. ill_launch_graph replays it. */
+int ill_capture_spec(ill_engine* e, int npasses);
+
+/* Engine.generate with speculation on (Engine.swift:922-1038): prefill, then verify passes
+ * of up to `rows` (2..16) rows, in captured graphs of `chunk` passes for q4 models (one
+ * launch per pass otherwise), while polling out_tokens. adaptive != 0 narrows the passes to
+ * 8 rows while fewer than 1.5 drafts per pass are accepted (Engine.nextPassShape,
+ * :888-898). out / n_out as for ill_generate; stats (optional, [2]) receives the passes
+ * and accepted drafts of the request. */
+int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
+                      int32_t* out, int* n_out, int32_t* stats);
+
 /* Timing (Engine.profile / gpuTime, Engine.swift:621-729): GPU milliseconds of `iters`
  * replays of the captured graph, measured with HIP events on the engine's stream. */
 int ill_time_graph(ill_engine* e, int iters, float* ms);

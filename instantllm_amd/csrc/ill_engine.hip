@@ -118,6 +118,10 @@ struct ill_engine {
   float* logits = nullptr;
   int32_t* out_dev = nullptr;
   int32_t* out_host = nullptr;
+  int32_t* spec_host = nullptr;   // pinned [2]: passes, accepted drafts (written by spec commits)
+  int32_t* prompt = nullptr;      // [4 + 256]: prompt-lookup context of the drafter
+  uint8_t* ngram = nullptr;       // n-gram draft table (ILL_NG_SLOTS x 16 B), optional
+  bool graph_spec = false;        // the captured graph holds spec passes (their control comes from the device)
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   int graph_steps = 0;
@@ -619,8 +623,11 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   if (!ok) return cleanup(fail(ILL_E_HIP, "device buffer allocation failed"));
   if (hipMemcpy(e->dolayers, e->holayers.data(), sizeof(OpLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
-  if (hipHostMalloc((void**)&e->out_host, (size_t)max_steps * 4, hipHostMallocDefault) != hipSuccess)
+  if (hipHostMalloc((void**)&e->out_host, (size_t)max_steps * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&e->spec_host, 2 * 4, hipHostMallocDefault) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "pinned token buffer allocation failed"));
+  e->spec_host[0] = e->spec_host[1] = 0;
+  if (!dalloc((void**)&e->prompt, (4 + ILL_OB_MAX) * 4)) return cleanup(fail(ILL_E_HIP, "prompt buffer allocation failed"));
   for (int i = 0; i < max_steps; i++) e->out_host[i] = -1;
   if (hipMemcpy(e->dlayers, e->hlayers.data(), sizeof(IllLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
@@ -666,6 +673,9 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.logits = e->logits;
   a.out_dev = e->out_dev;
   a.out_host = e->out_host;
+  a.spec_host = e->spec_host;
+  a.prompt = e->prompt;
+  a.ngram = nullptr;
   a.maxctx = e->maxctx;
   a.maxsteps = max_steps;
   OpCtx& oc = e->octx;
@@ -697,6 +707,9 @@ int ill_destroy(ill_engine* e) {
   for (void* p : bufs)
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);
+  if (e->spec_host) hipHostFree(e->spec_host);
+  if (e->prompt) hipFree(e->prompt);
+  if (e->ngram) hipFree(e->ngram);
   if (e->ev0) hipEventDestroy(e->ev0);
   if (e->ev1) hipEventDestroy(e->ev1);
   if (e->stream) hipStreamDestroy(e->stream);
@@ -747,13 +760,16 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
   for (int i = 0; i < n; i++)
     if (toks[i] < 0 || toks[i] >= e->vocab) return fail(ILL_E_ARG, "token %d out of range", toks[i]);
   int pos = s.pos;
+  // encodePrefill commits through k_commit_spec when speculation is on (Engine.swift:588-601):
+  // the State's tspec > 1 makes the prompt's commit draft the first verify pass
+  const int fin = s.tspec > 1 ? 2 : 1;
   if (e->fmt != 2 || n > 16) {   // layer-by-layer path, chunks of up to ILL_OP_MAXM rows
     for (int c0 = 0; c0 < n; c0 += ILL_OP_MAXM) {
       const int rows = n - c0 < ILL_OP_MAXM ? n - c0 : ILL_OP_MAXM;
       const bool last = c0 + rows == n;
       HCK(hipMemcpyAsync(e->ptoks, toks + c0, rows * 4, hipMemcpyHostToDevice, e->stream));
       if ((rc = write_pos_n(e, pos, rows))) return rc;
-      if ((rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, last ? 1 : 0, last ? write_logits : 0, last ? 1 : 0))) return rc;
+      if ((rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, last ? 1 : 0, last ? write_logits : 0, last ? fin : 0))) return rc;
       e->pos_hint = pos;
       if ((rc = op_launch(e, rows, last ? 1 : 0))) return rc;
       pos += rows;
@@ -768,7 +784,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
     const bool last = c0 + rows == n;
     HCK(hipMemcpyAsync(e->ptoks, toks + c0, rows * 4, hipMemcpyHostToDevice, e->stream));
     if ((rc = write_pos_n(e, pos, rows))) return rc;
-    if (last) rc = set_ctl(e, ILL_MODE_ROWS, rows, rows - 1, 1, write_logits, 1);
+    if (last) rc = set_ctl(e, ILL_MODE_ROWS, rows, rows - 1, 1, write_logits, fin);
     else rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, 0, 0, 0);
     if (rc) return rc;
     if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
@@ -834,9 +850,80 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
   return ILL_OK;
 }
 
+// ---- speculative decoding with on-device drafting (k_commit_spec, Shaders.swift:246-418) ----
+int ill_load_ngram(ill_engine* e, const void* table, int64_t bytes) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  HCK(hipStreamSynchronize(e->stream));
+  if (!table || bytes == 0) {
+    if (e->ngram) HCK(hipFree(e->ngram));
+    e->ngram = nullptr;
+  } else {
+    if (bytes != (int64_t)ILL_NG_SLOTS * 16) return fail(ILL_E_ARG, "n-gram table of %lld bytes (expected %d)", (long long)bytes, ILL_NG_SLOTS * 16);
+    if (!e->ngram) HCK(hipMalloc((void**)&e->ngram, (size_t)bytes));
+    HCK(hipMemcpy(e->ngram, table, (size_t)bytes, hipMemcpyHostToDevice));
+  }
+  e->args.ngram = (const uint4*)e->ngram;
+  drop_graph(e);   // captured passes hold the table pointer
+  return ILL_OK;
+}
+
+int ill_set_prompt(ill_engine* e, const int32_t* toks, int n) {
+  if (!e || (n > 0 && !toks) || n < 0) return fail(ILL_E_ARG, "bad prompt");
+  int32_t buf[4 + ILL_OB_MAX] = {0};
+  const int np = n < ILL_OB_MAX ? n : ILL_OB_MAX;
+  buf[0] = np;
+  for (int i = 0; i < np; i++) buf[4 + i] = toks[n - np + i];
+  HCK(hipMemcpyAsync(e->prompt, buf, sizeof buf, hipMemcpyHostToDevice, e->stream));
+  HCK(hipStreamSynchronize(e->stream));
+  return ILL_OK;
+}
+
+namespace {
+// write_logits of the next launch only (a speculative pass takes its rows and commit from
+// the control block the previous commit wrote)
+int set_wlog(ill_engine* e, int wlog) {
+  e->hctl.write_logits = wlog;
+  HCK(hipMemcpyAsync(&e->ctl->write_logits, &e->hctl.write_logits, 4, hipMemcpyHostToDevice, e->stream));
+  return 0;
+}
+}  // namespace
+
+int ill_spec_pass(ill_engine* e, int write_logits) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  IllState s;
+  int rc = read_state(e, &s);
+  if (rc) return rc;
+  if (s.done) return ILL_OK;   // a stopped request: nothing to do (the device would early-exit)
+  IllCtl c;
+  HCK(hipMemcpy(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost));
+  if (c.commit != 2 || c.nrows < 1 || c.nrows > ILL_MAXT) return fail(ILL_E_ARG, "no drafted pass pending (prefill with the State's tspec > 1 first)");
+  if ((rc = set_wlog(e, write_logits))) return rc;
+  e->pos_hint = s.pos;
+  if ((rc = e->fmt == 2 ? launch(e, 16) : op_launch(e, c.nrows, c.nrows))) return rc;
+  if ((rc = check_err(e))) return rc;
+  if (write_logits) e->logits_rows_valid = c.nrows;
+  return ILL_OK;
+}
+
+int ill_capture_spec(ill_engine* e, int npasses) {
+  if (!e || npasses < 1) return fail(ILL_E_ARG, "bad pass count");
+  if (e->fmt != 2) return fail(ILL_E_FORMAT, "chained speculative passes need the q4 pass kernel (format %d passes size their launches on the host)", e->fmt);
+  drop_graph(e);
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+  for (int i = 0; i < npasses; i++)
+    hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
+  HCK(hipStreamEndCapture(e->stream, &e->graph));
+  HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
+  e->graph_steps = npasses;
+  e->graph_spec = true;
+  return ILL_OK;
+}
+
 int ill_capture_steps(ill_engine* e, int nsteps) {
   if (!e || nsteps < 1) return fail(ILL_E_ARG, "bad step count");
   drop_graph(e);
+  e->graph_spec = false;
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   const int base = e->pos_hint;
@@ -856,7 +943,7 @@ int ill_launch_graph(ill_engine* e) { return ill_launch_graph_logits(e, 0); }
 
 int ill_launch_graph_logits(ill_engine* e, int write_logits) {
   if (!e || !e->gexec) return fail(ILL_E_ARG, "no captured graph");
-  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits ? 1 : 0, 1);
+  int rc = e->graph_spec ? set_wlog(e, write_logits ? 1 : 0) : set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits ? 1 : 0, 1);
   if (rc) return rc;
   if ((rc = count_passes(e, e->graph_steps))) return rc;
   HCK(hipGraphLaunch(e->gexec, e->stream));
@@ -969,12 +1056,97 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
   return check_err(e);
 }
 
+int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
+                      int32_t* out, int* n_out, int32_t* stats) {
+  if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
+  if (rows < 2 || rows > ILL_MAXT) return fail(ILL_E_ARG, "rows per speculative pass %d outside 2..%d", rows, ILL_MAXT);
+  if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
+  if (ntok + max_new + ILL_MAXT > e->maxctx)
+    return fail(ILL_E_ARG, "prompt of %d tokens + %d new exceeds the context %d (less a 16-slot pass margin)", ntok, max_new, e->maxctx);
+  if (chunk < 1) chunk = 1;
+  *n_out = 0;
+  int rc;
+  if ((rc = ill_reset_out_tokens(e)) || (rc = ill_set_prompt(e, toks, ntok))) return rc;
+  e->spec_host[0] = e->spec_host[1] = 0;
+  int32_t s[16] = {0};
+  s[1] = ntok;
+  s[4] = e->maxctx;
+  s[5] = max_new;
+  s[6] = 151645;
+  s[7] = 151643;
+  s[8] = 1;
+  s[9] = rows;   // tspec: the prompt's commit drafts the first pass
+  if ((rc = ill_set_state(e, s))) return rc;
+  if ((rc = ill_prefill(e, toks, ntok, 0))) return rc;
+  const bool graphs = e->fmt == 2;
+  if (graphs && (!e->graph_spec || e->graph_steps != chunk) && (rc = ill_capture_spec(e, chunk))) return rc;
+  // Engine.nextPassShape (Engine.swift:888-898): the configured width while drafts are
+  // accepted (at least adaptHi = 1.5 per pass over the last few committed passes), an
+  // 8-row chain otherwise; the width takes effect from the next pass drafted
+  std::vector<std::pair<int, int>> hist;
+  int cur_rows = rows;
+  auto shape = [&]() {
+    if (!adaptive) return rows;
+    const int p = ((volatile int32_t*)e->spec_host)[0], a = ((volatile int32_t*)e->spec_host)[1];
+    if (hist.empty() || hist.back().first != p) hist.emplace_back(p, a);
+    if (hist.size() < 3) return rows;
+    const auto& first = hist[hist.size() >= 4 ? hist.size() - 4 : 0];
+    if (p - first.first < 2) return rows;
+    const double rate = (double)(a - first.second) / (double)(p - first.first);
+    return rate >= 1.5 ? rows : std::min(rows, 8);
+  };
+  volatile const int32_t* ot = e->out_host;
+  volatile const int32_t* sp = e->spec_host;
+  int got = 0, encoded = 0;   // tokens read, passes enqueued after the prefill
+  bool stopped = false;
+  while (!stopped && got < max_new) {
+    // keep at most one chunk of passes ahead of the committed ones (Engine.swift:991-1008);
+    // every pass commits at least one token, so max_new passes always suffice
+    if (encoded < max_new && (!graphs || encoded - (sp[0] - 1) <= chunk)) {
+      const int want = shape();
+      if (want != cur_rows) {   // the State's tspec, ordered after the passes before it
+        cur_rows = want;
+        HCK(hipMemcpyAsync(&e->st->tspec, &cur_rows, 4, hipMemcpyHostToDevice, e->stream));
+      }
+      if (graphs) {
+        if ((rc = ill_launch_graph(e))) return rc;
+        encoded += chunk;
+        continue;
+      }
+      if ((rc = ill_spec_pass(e, 0))) return rc;   // host-sized pass (layer-by-layer path)
+      encoded++;
+    }
+    const int t = ot[got];
+    if (t < 0) {
+      // an idle stream with no new token: the device stopped (or every pass is spent)
+      if (hipStreamQuery(e->stream) == hipSuccess && ot[got] < 0) {
+        IllState st;
+        if ((rc = check_err(e)) || (rc = read_state(e, &st))) return rc;
+        if (st.done || encoded >= max_new) break;
+      }
+      continue;
+    }
+    got++;
+    if (t == 151645 || t == 151643) break;
+    out[(*n_out)++] = t;
+  }
+  HCK(hipStreamSynchronize(e->stream));
+  if ((rc = check_err(e))) return rc;
+  if (stats) {
+    IllState st;
+    if ((rc = read_state(e, &st))) return rc;
+    stats[0] = st.passes;
+    stats[1] = st.accepted;
+  }
+  return ILL_OK;
+}
+
 int ill_time_graph(ill_engine* e, int iters, float* ms) {
   if (!e || !e->gexec || iters < 1 || !ms) return fail(ILL_E_ARG, "bad timing arguments");
   hipEvent_t a, b;
   HCK(hipEventCreate(&a));
   HCK(hipEventCreate(&b));
-  int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
+  int rc = e->graph_spec ? set_wlog(e, 0) : set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, 0, 1);
   if (rc) return rc;
   if ((rc = count_passes(e, iters * e->graph_steps))) return rc;
   HCK(hipEventRecord(a, e->stream));

@@ -53,6 +53,9 @@ struct IllPassArgs {
   int32_t* out_host;       // [maxsteps] pinned host memory
   uint64_t* trace;         // optional [256][ILL_TRACE_SLOTS] timestamps (nullptr = off)
   uint64_t* pub;           // 16-row passes: published row codings [2][ILL_MAXLAYERS + 1][16][ILL_PUB_W]
+  const uint4* ngram;      // optional n-gram draft table [ILL_NG_SLOTS] (nullptr: none)
+  const int32_t* prompt;   // [4 + ILL_OB_MAX]: count, -, -, -, the last <= 256 prompt tokens
+  int32_t* spec_host;      // pinned host [2]: passes and accepted drafts of speculative commits
   int maxctx;
   int maxsteps;
 };
@@ -70,6 +73,7 @@ struct PassHdr {
   uint32_t epoch;
   int mode, nrows, pos, lmh0, lmhn, wlog, commit, done, bank, zrows;
   int step, maxsteps, eos0, eos1, passes, accepted;   // State as the pass found it
+  int tspec, nodraft;
   int tok[16], depth[16], parent[16];
   int prow[16][16];        // prow[t][d]: pass row on row t's path at depth d
 };
@@ -98,6 +102,8 @@ __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
   H.eos1 = st->eos1;
   H.passes = st->passes;
   H.accepted = st->accepted;
+  H.tspec = st->tspec;
+  H.nodraft = st->nodraft;
   H.epoch = c->epoch;
   H.bank = c->epoch & 1;
   H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
@@ -504,11 +510,26 @@ struct LmhLds {
   int bi[ILL_WAVES][16];
 };
 
+// Speculative drafting after a commit (k_commit_spec, Shaders.swift:367-412): recent output
+// tokens, the n-gram history, and the workgroup's reduction slots.
+#define ILL_OB_MAX 256
+#define ILL_NG_SLOTS (1 << 20)
+#define ILL_NG_MAXN 6
+struct DraftLds {
+  int ob[ILL_OB_MAX + ILL_MAXT];   // recent output tokens, then this commit's drafts
+  int hist[ILL_NG_MAXN + ILL_MAXT];
+  uint32_t best[ILL_WAVES];
+  int ng[ILL_NG_MAXN][16];          // n-gram probes: 0 occupied by another key, 1 empty, 2 + next: hit
+  int L, len, d, nd;
+};
+
 struct CommitLds {
   uint64_t key[16][ILL_WG / 64];   // [row - first row][wave holding the row's partials]
   int g[16];
   int path[16];
   int npath, pos0;
+  int draft, have, last, stop;      // drafting after the commit: on, tokens committed, last token
+  DraftLds dr;
 };
 
 template <int T>
@@ -1586,6 +1607,142 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
   commit_apply(a, H, C, true);
 }
 
+// ---- drafting (k_commit_spec, Shaders.swift:367-412) ----------------------------------------
+// n-gram table key of the last n tokens ctx[0..n-1], oldest first (Shaders.swift:66-70; the
+// same hash as NGramTable.key, NGram.swift:13-21, so tables built by the reference load as is).
+__device__ __forceinline__ uint64_t ng_key(const int* ctx, int n) {
+  uint64_t h = 0xcbf29ce484222325ull ^ (uint64_t)n;
+  for (int i = 0; i < n; i++) {
+    h ^= (uint64_t)(uint32_t)ctx[i] + 0x9e3779b97f4a7c15ull;
+    h *= 0x100000001b3ull;
+    h ^= h >> 29;
+  }
+  return h | 1ull;
+}
+
+// Workgroup maximum of a 32-bit key (every thread gets it).
+__device__ __forceinline__ uint32_t wg_max_u32(uint32_t v, uint32_t* slots) {
+  const int i = threadIdx.x, w = i >> 6;
+  v = group_reduce<64>(v, OpMaxU{});
+  if ((i & 63) == 0) slots[w] = v;
+  __syncthreads();
+  uint32_t m = slots[0];
+#pragma unroll
+  for (int k = 1; k < ILL_WAVES; k++) m = slots[k] > m ? slots[k] : m;
+  __syncthreads();
+  return m;
+}
+
+// Drafts for the next pass after a speculative commit that did not stop: up to tspec - 1
+// tokens (none with nodraft), each from the first source with a guess:
+//   1. self-repetition: the most recent earlier occurrence of the longest suffix (3..8
+//      tokens) of the recent output, continued;
+//   2. the n-gram table (if one is loaded): the stored continuation of the longest known
+//      context of the last 6..1 tokens (-1 before the output starts);
+//   3. prompt lookup: the token after the latest longest (1..4 token) match of the output
+//      suffix in the last <= 256 prompt tokens.
+// Each draft is appended to the output before the next is drafted; a stop token ends the
+// drafts. The reference scans with one thread, keeping the last (highest j) candidate of
+// the longest match; here every thread takes one position j and the workgroup maximum of
+// (match length, j) picks the same one. Then the next pass is set up as a chain over
+// [last token, drafts...] with one row per token (rows, lm_head rows and commit of the
+// control block, the State's n and nver).
+__device__ __noinline__ void spec_draft(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
+  DraftLds& D = C.dr;
+  const int i = threadIdx.x;
+  const int have = C.have;
+  const int w0 = have > ILL_OB_MAX ? have - ILL_OB_MAX : 0;
+  for (int k = w0 + i; k < have; k += ILL_WG_THREADS) D.ob[k - w0] = gld(a.out_dev + k);
+  const int np = a.prompt ? min(max(gld(a.prompt), 0), ILL_OB_MAX) : 0;
+  if (i == 0) {
+    D.L = have - w0;
+    D.len = 0;
+    for (int k = ILL_NG_MAXN; k >= 1; k--) D.hist[D.len++] = have - k >= 0 ? gld(a.out_dev + have - k) : -1;
+    D.nd = 0;
+  }
+  __syncthreads();
+  const int T = min(max(H.tspec, 1), ILL_MAXT);
+  const int maxd = H.nodraft ? 0 : T - 1;
+  for (int nd = 0; nd < maxd; nd++) {
+    const int L = D.L;
+    // 1. self-repetition: position j (1 <= j <= L - 1) continues a match of m >= 3 tokens
+    uint32_t key = 0;
+    {
+      const int j = i + 1;
+      if (j <= L - 1) {
+        int m = 0;
+        while (m < 8 && j - 1 - m >= 0 && D.ob[j - 1 - m] == D.ob[L - 1 - m]) m++;
+        if (m >= 3) key = ((uint32_t)m << 16) | (uint32_t)j;
+      }
+    }
+    key = wg_max_u32(key, D.best);
+    int d = key ? D.ob[key & 0xffff] : -1;
+    // 2. n-gram table: orders 6..1, 16 linear probes each, one thread per (order, probe)
+    if (d < 0 && a.ngram) {
+      const int len = D.len;
+      if (i < ILL_NG_MAXN * 16) {
+        const int n = ILL_NG_MAXN - i / 16, pr = i % 16;
+        int v = 1;
+        if (n <= len) {
+          const uint64_t k = ng_key(D.hist + len - n, n);
+          const uint32_t slot = ((uint32_t)(k >> 12) + (uint32_t)pr) & (ILL_NG_SLOTS - 1);
+          const uint4 e = gld(a.ngram + slot);
+          const uint64_t ek = ((uint64_t)e.y << 32) | e.x;
+          v = ek == 0 ? 1 : (ek == k ? 2 + (int)e.z : 0);
+        }
+        D.ng[ILL_NG_MAXN - n][pr] = v;
+      }
+      __syncthreads();
+      if (i == 0) {
+        int got = -1;
+        for (int n = min(ILL_NG_MAXN, len); n >= 1 && got < 0; n--)
+          for (int pr = 0; pr < 16; pr++) {
+            const int v = D.ng[ILL_NG_MAXN - n][pr];
+            if (v == 1) break;
+            if (v >= 2) { got = v - 2; break; }
+          }
+        D.d = got;
+      }
+      __syncthreads();
+      d = D.d;
+    }
+    // 3. prompt lookup: position j (1 <= j <= np - 1) continues a match of m >= 1 tokens
+    if (d < 0 && np > 1) {
+      uint32_t pk = 0;
+      const int j = i + 1;
+      if (j <= np - 1) {
+        const int32_t* P = a.prompt + 4;
+        int m = 0;
+        while (m < 4 && m < L && j - 1 - m >= 0 && gld(P + j - 1 - m) == D.ob[L - 1 - m]) m++;
+        if (m >= 1) pk = ((uint32_t)m << 16) | (uint32_t)j;
+      }
+      pk = wg_max_u32(pk, D.best);
+      d = pk ? gld(a.prompt + 4 + (pk & 0xffff)) : -1;
+    }
+    if (d < 0) break;   // uniform: every thread holds the same d
+    if (i == 0) {
+      D.ob[L] = d;
+      D.L = L + 1;
+      D.hist[D.len++] = d;
+      a.ptoks[1 + nd] = d;
+      D.nd = nd + 1;
+    }
+    __syncthreads();
+    if (d == H.eos0 || d == H.eos1) break;
+  }
+  if (i == 0) {
+    const int rows = 1 + D.nd;
+    a.st->n = rows;
+    a.st->nver = rows;
+    IllCtl* c = a.ctl;
+    c->mode = ILL_MODE_ROWS;
+    c->nrows = rows;
+    c->lmh_row0 = 0;
+    c->lmh_rows = rows;
+    c->commit = 2;
+  }
+}
+
 // Commit of the pass's argmaxes C.g[t] (rows lmh0 ..): token record, State advance, stop
 // test, chain / tree accept walk and KV compaction (Shaders.swift:192-244, :246-418). The
 // pass kernel also advances the epoch and its accumulator-bank bookkeeping. The State is
@@ -1597,6 +1754,7 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
   if (i == 0) {
     C.npath = 0;
     C.pos0 = H.pos;
+    C.draft = 0;
     if (H.commit == 0) {
       st->pos = H.pos + H.nrows;
     } else if (H.commit == 1) {
@@ -1613,46 +1771,57 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
       a.ptoks[0] = tok;
       a.ctl->last_tok = tok;
     } else {
-      // speculative pass: rows 0..nrows-1 = [last token, drafts]; accept and commit
-      // (Shaders.swift:305-333)
-      const int nv = H.nrows;
+      // speculative commit (Shaders.swift:305-333): the pass's argmax rows lmh0 .. lmh0 + nv - 1
+      // are [last token, drafts...]; accept the longest matching prefix (chain) or path (tree).
+      // nv = 1 (a prefill, or a pass without drafts): the pass's rows are all context.
+      const int nv = H.lmhn;
+      const int* g = C.g + H.lmh0;
       int m = 0;
       if (H.mode == ILL_MODE_TREE) {
         int cur = 0;
         for (;;) {
           int c = -1;
           for (int r = 1; r < nv; ++r)
-            if (H.parent[r] == cur && H.tok[r] == C.g[cur]) { c = r; break; }
+            if (H.parent[r] == cur && H.tok[r] == g[cur]) { c = r; break; }
           if (c < 0) break;
           C.path[m++] = c;
           cur = c;
         }
       } else {
-        while (m < nv - 1 && H.tok[m + 1] == C.g[m]) m++;
+        while (m < nv - 1 && H.tok[H.lmh0 + m + 1] == g[m]) m++;
         for (int k = 0; k < m; k++) C.path[k] = k + 1;
       }
       st->passes = H.passes + 1;
       st->accepted = H.accepted + m;
+      if (a.spec_host) {   // for the host's choice of the next pass shape (Engine.swift:888-898)
+        __hip_atomic_store(a.spec_host + 0, H.passes + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.spec_host + 1, H.accepted + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
       bool stop = false;
-      int last = C.g[0];
+      int last = g[0];
       int step = H.step;
       for (int k = 0; k <= m && !stop; k++) {
-        const int tok = C.g[k == 0 ? 0 : C.path[k - 1]];
+        const int tok = g[k == 0 ? 0 : C.path[k - 1]];
         a.out_dev[step] = tok;
         __hip_atomic_store(a.out_host + step, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         last = tok;
         if (tok == H.eos0 || tok == H.eos1 || step + 1 >= H.maxsteps) stop = true;
         step++;
       }
+      const int newpos = nv == 1 ? H.pos + H.nrows : H.pos + m + 1;
       st->step = step;
-      st->pos = H.pos + m + 1;
+      st->pos = newpos;
       st->n = 1;
       st->nver = 1;
       st->tree = 0;
-      if (stop || H.pos + m + 1 + ILL_MAXT > a.maxctx) st->done = 1;
+      stop = stop || newpos + ILL_MAXT > a.maxctx;
+      if (stop) st->done = 1;
       a.ptoks[0] = last;
       a.ctl->last_tok = last;
       C.npath = H.mode == ILL_MODE_TREE ? m : 0;
+      C.draft = !stop;
+      C.have = step;
+      C.last = last;
     }
   }
   __syncthreads();
@@ -1672,6 +1841,7 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
     }
     __syncthreads();
   }
+  if (C.draft) spec_draft(a, H, C);   // workgroup-uniform (LDS, after the barrier)
   if (pass_kernel && i == 0) {
     a.ctl->bank_rows[H.bank] = H.nrows;   // rows of this bank to clear during the next pass
     a.ctl->bank_rows[H.bank ^ 1] = 0;     // cleared during this pass

@@ -65,6 +65,11 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_kv_copy_in": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16)]),
         "ill_generate": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), C.POINTER(F32)]),
         "ill_time_graph": (C.c_int, [P, C.c_int, C.POINTER(F32)]),
+        "ill_load_ngram": (C.c_int, [P, C.c_void_p, C.c_int64]),
+        "ill_set_prompt": (C.c_int, [P, ip, C.c_int]),
+        "ill_spec_pass": (C.c_int, [P, C.c_int]),
+        "ill_capture_spec": (C.c_int, [P, C.c_int]),
+        "ill_generate_spec": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), ip]),
         "ill_last_pass_ms": (C.c_int, [P, C.POINTER(F32)]),
         "ill_trace_enable": (C.c_int, [P, C.c_int]),
         "ill_trace_read": (C.c_int, [P, C.POINTER(C.c_uint64), C.POINTER(C.c_int)]),
@@ -198,6 +203,34 @@ class Engine:
                                           _ptr(lg, C.c_float) if lg is not None else None))
         toks = out[: n.value].tolist()
         return (toks, lg) if want_logits else toks
+
+    # ---- speculative decoding (k_commit_spec drafting on the device) ---------------------
+    def load_ngram(self, table: np.ndarray | None):
+        if table is None:
+            self._check(self.lib.ill_load_ngram(self.h, None, 0))
+            return
+        t = np.ascontiguousarray(table)
+        self._check(self.lib.ill_load_ngram(self.h, t.ctypes.data, t.nbytes))
+
+    def set_prompt(self, toks):
+        a = _i32(toks)
+        self._check(self.lib.ill_set_prompt(self.h, _ptr(a, C.c_int32), len(a)))
+
+    def spec_pass(self, write_logits: bool = False):
+        self._check(self.lib.ill_spec_pass(self.h, int(write_logits)))
+
+    def capture_spec(self, npasses: int):
+        self._check(self.lib.ill_capture_spec(self.h, npasses))
+
+    def generate_spec(self, tokens, max_new: int, rows: int = 16, chunk: int = 4, adaptive: bool = False):
+        """Engine.generate with speculation (Engine.swift:922-1038): (tokens, passes, accepted)."""
+        a = _i32(tokens)
+        out = np.zeros(max_new, np.int32)
+        n = C.c_int(0)
+        stats = np.zeros(2, np.int32)
+        self._check(self.lib.ill_generate_spec(self.h, _ptr(a, C.c_int32), len(a), max_new, rows, chunk, int(adaptive),
+                                               _ptr(out, C.c_int32), C.byref(n), _ptr(stats, C.c_int32)))
+        return out[: n.value].tolist(), int(stats[0]), int(stats[1])
 
     def last_pass_ms(self) -> float:
         ms = C.c_float(0)

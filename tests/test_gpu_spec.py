@@ -1,0 +1,159 @@
+"""GPU tests of speculative decoding with on-device drafting, through the C ABI.
+
+The invariant of the reference (README.md:90-93): speculation never changes the output, so a
+speculative request commits exactly the plain greedy tokens. The device's drafting
+(k_commit_spec, Shaders.swift:367-412) is checked end to end against the oracle's
+restatement: given the greedy continuation, oracle.draft.simulate predicts every pass's
+drafts and accepted prefix, so the State's passes / accepted counters must equal it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from instantllm_amd import synth, illfile as F, ngram
+from oracle import draft as D
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 4096
+
+
+def log(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def q4_engine(tmp_path_factory):
+    from instantllm_amd.engine import Engine
+    path = str(tmp_path_factory.mktemp("spec") / "q4.ill")
+    synth.build_model(path, F.FMT_Q4, seed=2, shape=synth.ModelShape(layers=3, vocab=VOCAB))
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=256)
+    yield e
+    e.close()
+
+
+def _prompt(seed, n=20):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, VOCAB, size=n)]
+
+
+@pytest.mark.parametrize("rows", [16, 4])
+def test_spec_generate_equals_greedy_and_oracle_counts(q4_engine, rows):
+    e = q4_engine
+    e.load_ngram(None)
+    prompt = _prompt(100 + rows)
+    gx = e.generate(prompt, max_new=48 + 16, chunk=8)   # 16 more for the last pass's drafts
+    g = gx[:48]
+    log(f"rows {rows}: greedy {g[:12]}...")
+    toks, passes, acc = e.generate_spec(prompt, 48, rows=rows, chunk=4)
+    assert toks == g
+    _, p_ref, a_ref = D.simulate(prompt, gx, 48, rows)
+    log(f"rows {rows}: passes {passes} accepted {acc} (oracle {p_ref} / {a_ref})")
+    assert (passes, acc) == (p_ref, a_ref)
+
+
+def test_spec_with_ngram_table_accepts_drafts(q4_engine):
+    e = q4_engine
+    prompt = _prompt(7)
+    gx = e.generate(prompt, max_new=64 + 16, chunk=8)
+    g = gx[:64]
+    table = ngram.build([g])
+    e.load_ngram(table)
+    try:
+        toks, passes, acc = e.generate_spec(prompt, 64, rows=16, chunk=4)
+    finally:
+        e.load_ngram(None)
+    assert toks == g
+    _, p_ref, a_ref = D.simulate(prompt, gx, 64, 16, table=table)
+    log(f"n-gram table: passes {passes} accepted {acc} (oracle {p_ref} / {a_ref})")
+    assert (passes, acc) == (p_ref, a_ref)
+    assert acc > 0 and passes < 64
+
+
+def test_graph_chained_passes_equal_single_passes(q4_engine):
+    """Passes replayed from one hipGraph (each taking its rows from the commit before it)
+    equal the same passes launched one by one."""
+    e = q4_engine
+    prompt = _prompt(8)
+    g = e.generate(prompt, max_new=40, chunk=8)
+    table = ngram.build([g[:20]])   # drafts right for the first half, then on their own
+    e.load_ngram(table)
+    try:
+        toks_g, p_g, a_g = e.generate_spec(prompt, 40, rows=16, chunk=3)
+        e.reset_out_tokens()
+        e.set_prompt(prompt)
+        e.set_state(pos=0, n=len(prompt), maxsteps=40, tspec=16)
+        e.prefill(prompt)
+        for _ in range(40):
+            if e.get_state()["done"]:
+                break
+            e.spec_pass()
+        st = e.get_state()
+    finally:
+        e.load_ngram(None)
+    toks_s = [int(t) for t in e.out_tokens()[:40]]
+    assert toks_g == g and toks_s == g
+    assert (st["passes"], st["accepted"]) == (p_g, a_g)
+
+
+def test_nodraft_passes_are_one_row(q4_engine):
+    e = q4_engine
+    prompt = _prompt(9)
+    g = e.generate(prompt, max_new=12, chunk=4)
+    e.reset_out_tokens()
+    e.set_prompt(prompt)
+    e.set_state(pos=0, n=len(prompt), maxsteps=12, tspec=16, nodraft=1)
+    e.prefill(prompt)
+    for _ in range(12):
+        if e.get_state()["done"]:
+            break
+        e.spec_pass()
+    st = e.get_state()
+    assert [int(t) for t in e.out_tokens()[:12]] == g
+    assert st["passes"] == 12 and st["accepted"] == 0
+
+
+def test_adaptive_shapes_keep_the_output(q4_engine):
+    e = q4_engine
+    prompt = _prompt(10)
+    g = e.generate(prompt, max_new=48, chunk=8)
+    toks, _, _ = e.generate_spec(prompt, 48, rows=16, chunk=2, adaptive=True)
+    assert toks == g
+
+
+def test_spec_q8_layer_by_layer_path(tmp_path):
+    """q8 passes are sized on the host: one launch per pass, the same tokens and counts."""
+    from instantllm_amd.engine import Engine
+    path = str(tmp_path / "q8.ill")
+    synth.build_model(path, F.FMT_Q8, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB), q8_group=32)
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=128)
+    try:
+        prompt = _prompt(11)
+        gx = e.generate(prompt, max_new=32 + 8, chunk=8)
+        g = gx[:32]
+        table = ngram.build([g])
+        e.load_ngram(table)
+        toks, passes, acc = e.generate_spec(prompt, 32, rows=8, chunk=4)
+    finally:
+        e.close()
+    assert toks == g
+    assert (passes, acc) == D.simulate(prompt, gx, 32, 8, table=table)[1:]
+
+
+def test_spec_fullsize_q4():
+    """The full model of seed 2: speculative tokens equal greedy ones."""
+    from instantllm_amd.engine import Engine
+    path = synth.cached_model(F.FMT_Q4, 2)
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=256)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(2).integers(0, F.VOCAB, size=64)]
+        gx = e.generate(prompt, max_new=48 + 16, chunk=8)
+        g = gx[:48]
+        table = ngram.build([g])
+        e.load_ngram(table)
+        toks, passes, acc = e.generate_spec(prompt, 48, rows=16, chunk=4)
+    finally:
+        e.close()
+    log(f"full q4: passes {passes} accepted {acc}")
+    assert toks == g
+    assert (passes, acc) == D.simulate(prompt, gx, 48, 16, table=table)[1:]

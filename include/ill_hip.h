@@ -136,6 +136,22 @@ int ill_capture_spec(ill_engine* e, int npasses);
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
                       int32_t* out, int* n_out, int32_t* stats);
 
+/* ---- Prefix reuse across requests (Engine.swift:788-838, :929-933, :1029-1031) ----------
+ * ill_generate / ill_generate_spec keep the tokens whose K/V stay valid after the call (the
+ * prompt and every generated token but the last); the next call prefills only the part of
+ * its prompt after the longest common prefix (at least one token). Any pass or K/V write
+ * launched outside those calls forgets the cached tokens.
+ * ill_prefix_info: the cached token count and the tokens the last generate call prefilled.
+ * ill_save_prefix (Engine.savePrefix): writes the K/V of the first n cached tokens (toks
+ * must be that prefix) to `path`: [u64 key: magic, model file size, mtime s, mtime ns,
+ * max_context][u64 n][n x i32 tokens][K][V], K and V as [layer][kv head][n][64] f16.
+ * ill_load_prefix (Engine.loadPrefix): loads such a file if it was saved for this model
+ * file and context (else ILL_E_FILE), makes its tokens the cached prefix and returns them
+ * in toks (max_toks entries; NULL to skip) and their count in n_out. */
+int ill_prefix_info(ill_engine* e, int* cached, int* last_prefill);
+int ill_save_prefix(ill_engine* e, const char* path, const int32_t* toks, int n);
+int ill_load_prefix(ill_engine* e, const char* path, int32_t* toks, int max_toks, int* n_out);
+
 /* Timing (Engine.profile / gpuTime, Engine.swift:621-729): GPU milliseconds of `iters`
  * replays of the captured graph, measured with HIP events on the engine's stream. */
 int ill_time_graph(ill_engine* e, int iters, float* ms);

@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -101,6 +102,7 @@ size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct ill_engine {
   int fmt = 2, layers = 0, vocab = 0, maxctx = 0, maxpass = 16, maxsteps = 0;
+  std::string path;   // the model file (the prefix-cache key)
   hipStream_t stream = nullptr;
   uint8_t* dweights = nullptr;
   IllLayerW* dlayers = nullptr;
@@ -122,6 +124,11 @@ struct ill_engine {
   int32_t* prompt = nullptr;      // [4 + 256]: prompt-lookup context of the drafter
   uint8_t* ngram = nullptr;       // n-gram draft table (ILL_NG_SLOTS x 16 B), optional
   bool graph_spec = false;        // the captured graph holds spec passes (their control comes from the device)
+  // Engine.cachedTokens (Engine.swift:929-933, :1029-1031): tokens whose K/V are valid at
+  // positions 0.. after the last generate call; any pass launched outside generate clears it
+  std::vector<int32_t> cached;
+  bool in_generate = false;
+  int last_prefill = 0;           // tokens the last generate call prefilled
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
   int graph_steps = 0;
@@ -141,6 +148,11 @@ struct ill_engine {
 };
 
 namespace {
+
+// A pass or cache write from outside generate: the generate prefix cache no longer holds.
+void touch_cache(ill_engine* e) {
+  if (!e->in_generate) e->cached.clear();
+}
 
 int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, int commit) {
   IllCtl c{};
@@ -462,6 +474,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   }
 
   ill_engine* e = new ill_engine();
+  e->path = path;
   e->fmt = fmt;
   e->q8g = q8g ? q8g : 64;
   e->layers = layers;
@@ -752,6 +765,7 @@ int ill_get_state(ill_engine* e, int32_t state[16]) {
 
 int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
   if (!e || !toks || n < 1) return fail(ILL_E_ARG, "bad prefill arguments");
+  touch_cache(e);
   IllState s;
   int rc = read_state(e, &s);
   if (rc) return rc;
@@ -806,6 +820,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
 
 int ill_decode_step(ill_engine* e, int write_logits) {
   if (!e) return fail(ILL_E_ARG, "null engine");
+  touch_cache(e);
   int rc = set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits, 1);
   if (rc) return rc;
   if ((rc = e->fmt == 2 ? launch(e, 1) : op_launch(e, 1, 1))) return rc;
@@ -817,6 +832,7 @@ int ill_decode_step(ill_engine* e, int write_logits) {
 
 int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t* toks, int write_logits) {
   if (!e || rows < 1 || rows > 16) return fail(ILL_E_ARG, "rows must be 1..16");
+  touch_cache(e);
   int32_t tk[16];
   if (tree) {
     if (tree[0] != rows) return fail(ILL_E_ARG, "tree[0] = %d but rows = %d", tree[0], rows);
@@ -890,6 +906,7 @@ int set_wlog(ill_engine* e, int wlog) {
 
 int ill_spec_pass(ill_engine* e, int write_logits) {
   if (!e) return fail(ILL_E_ARG, "null engine");
+  touch_cache(e);
   IllState s;
   int rc = read_state(e, &s);
   if (rc) return rc;
@@ -943,6 +960,7 @@ int ill_launch_graph(ill_engine* e) { return ill_launch_graph_logits(e, 0); }
 
 int ill_launch_graph_logits(ill_engine* e, int write_logits) {
   if (!e || !e->gexec) return fail(ILL_E_ARG, "no captured graph");
+  touch_cache(e);
   int rc = e->graph_spec ? set_wlog(e, write_logits ? 1 : 0) : set_ctl(e, ILL_MODE_DECODE, 1, 0, 1, write_logits ? 1 : 0, 1);
   if (rc) return rc;
   if ((rc = count_passes(e, e->graph_steps))) return rc;
@@ -992,6 +1010,7 @@ int ill_kv_copy_out(ill_engine* e, int npos, uint16_t* k, uint16_t* v) {
 
 int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v) {
   if (!e || !k || !v || npos < 0 || npos > e->maxctx) return fail(ILL_E_ARG, "bad kv copy");
+  touch_cache(e);
   HCK(hipStreamSynchronize(e->stream));
   const size_t per = (size_t)e->maxctx * 64;
   std::vector<uint16_t> kt(per), vtt(per);
@@ -1007,6 +1026,113 @@ int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v
   return ILL_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Marks the passes of one generate call as its own (they keep the prefix cache).
+struct GenScope {
+  ill_engine* e;
+  explicit GenScope(ill_engine* x) : e(x) { e->in_generate = true; }
+  ~GenScope() { e->in_generate = false; }
+};
+
+// Engine.swift:929-933: positions 0 .. common - 1 already hold this prompt's K/V (at least
+// one token is always prefilled, for its logits).
+int prefix_reuse(ill_engine* e, const int32_t* toks, int ntok) {
+  int common = 0;
+  const int lim = std::min((int)e->cached.size(), ntok);
+  while (common < lim && e->cached[common] == toks[common]) common++;
+  if (common == ntok) common--;
+  e->last_prefill = ntok - common;
+  e->cached.clear();   // set again when the call completes
+  return common;
+}
+
+// Engine.swift:1029-1031: K/V are valid for the prompt and every generated token but the
+// last one.
+void set_cached(ill_engine* e, const int32_t* toks, int ntok, const int32_t* out, int nout) {
+  e->cached.assign(toks, toks + ntok);
+  for (int i = 0; i + 1 < nout; i++) e->cached.push_back(out[i]);
+}
+
+// Engine.prefixKey (Engine.swift:790-794): the model file's size and modification time and
+// the context length; a saved prefix loads only into the same model file and context.
+bool prefix_key(const ill_engine* e, uint64_t key[5]) {
+  struct stat sb;
+  if (stat(e->path.c_str(), &sb) != 0) return false;
+  key[0] = 0x31564B4C4C49ull;
+  key[1] = (uint64_t)sb.st_size;
+  key[2] = (uint64_t)sb.st_mtim.tv_sec;
+  key[3] = (uint64_t)sb.st_mtim.tv_nsec;
+  key[4] = (uint64_t)e->maxctx;
+  return true;
+}
+}  // namespace
+
+extern "C" {
+
+int ill_prefix_info(ill_engine* e, int* cached, int* last_prefill) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  if (cached) *cached = (int)e->cached.size();
+  if (last_prefill) *last_prefill = e->last_prefill;
+  return ILL_OK;
+}
+
+// Engine.savePrefix (Engine.swift:796-811): [key 5 x u64][n u64][n x i32 tokens] then K and V
+// of positions 0..n-1 as [layer][kv head][n][64] f16 (the reference's cache layout).
+int ill_save_prefix(ill_engine* e, const char* path, const int32_t* toks, int n) {
+  if (!e || !path || !toks || n < 1) return fail(ILL_E_ARG, "bad prefix arguments");
+  if (n > (int)e->cached.size() || !std::equal(toks, toks + n, e->cached.begin()))
+    return fail(ILL_E_ARG, "the %d tokens are not a prefix of the cached tokens (%zu)", n, e->cached.size());
+  uint64_t key[6];
+  if (!prefix_key(e, key)) return fail(ILL_E_FILE, "cannot stat the model file %s", e->path.c_str());
+  key[5] = (uint64_t)n;
+  const size_t per = (size_t)e->layers * ILL_NKV * n * 64;
+  std::vector<uint16_t> k(per), v(per);
+  e->in_generate = true;   // reading the cache keeps it
+  int rc = ill_kv_copy_out(e, n, k.data(), v.data());
+  e->in_generate = false;
+  if (rc) return rc;
+  const std::string tmp = std::string(path) + ".tmp";
+  FILE* f = fopen(tmp.c_str(), "wb");
+  if (!f) return fail(ILL_E_FILE, "cannot write %s", tmp.c_str());
+  const bool ok = fwrite(key, 8, 6, f) == 6 && fwrite(toks, 4, (size_t)n, f) == (size_t)n &&
+                  fwrite(k.data(), 2, per, f) == per && fwrite(v.data(), 2, per, f) == per;
+  if (fclose(f) != 0 || !ok || rename(tmp.c_str(), path) != 0) {
+    remove(tmp.c_str());
+    return fail(ILL_E_FILE, "writing %s failed", path);
+  }
+  return ILL_OK;
+}
+
+// Engine.loadPrefix (Engine.swift:813-838): loads a prefix saved for this model file and
+// context; returns its tokens (the generate prefix cache then starts from them).
+int ill_load_prefix(ill_engine* e, const char* path, int32_t* toks, int max_toks, int* n_out) {
+  if (!e || !path || !n_out) return fail(ILL_E_ARG, "bad prefix arguments");
+  *n_out = 0;
+  FILE* f = fopen(path, "rb");
+  if (!f) return fail(ILL_E_FILE, "cannot open %s", path);
+  uint64_t hdr[6], key[5];
+  bool ok = fread(hdr, 8, 6, f) == 6 && prefix_key(e, key);
+  for (int i = 0; ok && i < 5; i++) ok = hdr[i] == key[i];
+  const uint64_t n = ok ? hdr[5] : 0;
+  ok = ok && n > 0 && n < (uint64_t)e->maxctx;
+  if (ok && toks && (int)n > max_toks) ok = false;
+  std::vector<int32_t> t(ok ? n : 0);
+  const size_t per = (size_t)e->layers * ILL_NKV * n * 64;
+  std::vector<uint16_t> k(ok ? per : 0), v(ok ? per : 0);
+  ok = ok && fread(t.data(), 4, n, f) == n && fread(k.data(), 2, per, f) == per && fread(v.data(), 2, per, f) == per &&
+       fgetc(f) == EOF;
+  fclose(f);
+  if (!ok) return fail(ILL_E_FILE, "%s is not a prefix saved for this model file and context", path);
+  int rc = ill_kv_copy_in(e, (int)n, k.data(), v.data());
+  if (rc) return rc;
+  e->cached = t;
+  if (toks) std::copy(t.begin(), t.end(), toks);
+  *n_out = (int)n;
+  return ILL_OK;
+}
+
 int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk, int32_t* out, int* n_out, float* logits_out) {
   if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
   if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
@@ -1015,11 +1141,13 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
     return fail(ILL_E_ARG, "prompt of %d tokens + %d new exceeds the context %d (less a 16-slot pass margin)", ntok, max_new, e->maxctx);
   if (chunk < 1) chunk = 1;
   *n_out = 0;
+  GenScope scope(e);
   int rc;
   if ((rc = ill_reset_out_tokens(e))) return rc;
+  const int common = prefix_reuse(e, toks, ntok);
   int32_t s[16] = {0};
-  s[0] = 0;
-  s[1] = ntok;
+  s[0] = common;
+  s[1] = ntok - common;
   s[4] = e->maxctx;
   s[5] = max_new;
   s[6] = 151645;
@@ -1027,9 +1155,9 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
   s[8] = 1;
   s[9] = 1;
   if ((rc = ill_set_state(e, s))) return rc;
-  if ((rc = ill_prefill(e, toks, ntok, logits_out != nullptr))) return rc;
+  if ((rc = ill_prefill(e, toks + common, ntok - common, logits_out != nullptr))) return rc;
   if (logits_out && (rc = ill_read_logits(e, 0, logits_out))) return rc;
-  if (e->graph_steps != chunk && (rc = ill_capture_steps(e, chunk))) return rc;
+  if ((e->graph_spec || e->graph_steps != chunk) && (rc = ill_capture_steps(e, chunk))) return rc;
   volatile const int32_t* ot = e->out_host;
   int got = 0, encoded = 1;
   bool stopped = false;
@@ -1053,7 +1181,9 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
     out[(*n_out)++] = t;
   }
   HCK(hipStreamSynchronize(e->stream));
-  return check_err(e);
+  if ((rc = check_err(e))) return rc;
+  set_cached(e, toks, ntok, out, *n_out);
+  return ILL_OK;
 }
 
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
@@ -1066,10 +1196,13 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   if (chunk < 1) chunk = 1;
   *n_out = 0;
   int rc;
+  GenScope scope(e);
   if ((rc = ill_reset_out_tokens(e)) || (rc = ill_set_prompt(e, toks, ntok))) return rc;
   e->spec_host[0] = e->spec_host[1] = 0;
+  const int common = prefix_reuse(e, toks, ntok);
   int32_t s[16] = {0};
-  s[1] = ntok;
+  s[0] = common;
+  s[1] = ntok - common;
   s[4] = e->maxctx;
   s[5] = max_new;
   s[6] = 151645;
@@ -1077,7 +1210,7 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   s[8] = 1;
   s[9] = rows;   // tspec: the prompt's commit drafts the first pass
   if ((rc = ill_set_state(e, s))) return rc;
-  if ((rc = ill_prefill(e, toks, ntok, 0))) return rc;
+  if ((rc = ill_prefill(e, toks + common, ntok - common, 0))) return rc;
   const bool graphs = e->fmt == 2;
   if (graphs && (!e->graph_spec || e->graph_steps != chunk) && (rc = ill_capture_spec(e, chunk))) return rc;
   // Engine.nextPassShape (Engine.swift:888-898): the configured width while drafts are
@@ -1132,6 +1265,7 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   }
   HCK(hipStreamSynchronize(e->stream));
   if ((rc = check_err(e))) return rc;
+  set_cached(e, toks, ntok, out, *n_out);
   if (stats) {
     IllState st;
     if ((rc = read_state(e, &st))) return rc;

@@ -66,6 +66,9 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_generate": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), C.POINTER(F32)]),
         "ill_time_graph": (C.c_int, [P, C.c_int, C.POINTER(F32)]),
         "ill_load_ngram": (C.c_int, [P, C.c_void_p, C.c_int64]),
+        "ill_prefix_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "ill_save_prefix": (C.c_int, [P, C.c_char_p, ip, C.c_int]),
+        "ill_load_prefix": (C.c_int, [P, C.c_char_p, ip, C.c_int, C.POINTER(C.c_int)]),
         "ill_set_prompt": (C.c_int, [P, ip, C.c_int]),
         "ill_spec_pass": (C.c_int, [P, C.c_int]),
         "ill_capture_spec": (C.c_int, [P, C.c_int]),
@@ -203,6 +206,23 @@ class Engine:
                                           _ptr(lg, C.c_float) if lg is not None else None))
         toks = out[: n.value].tolist()
         return (toks, lg) if want_logits else toks
+
+    # ---- prefix reuse (Engine.swift:788-838, :929-933) ---------------------------------
+    def prefix_info(self) -> tuple[int, int]:
+        """(cached tokens, tokens the last generate call prefilled)"""
+        c, p = C.c_int(0), C.c_int(0)
+        self._check(self.lib.ill_prefix_info(self.h, C.byref(c), C.byref(p)))
+        return c.value, p.value
+
+    def save_prefix(self, path: str, tokens):
+        a = _i32(tokens)
+        self._check(self.lib.ill_save_prefix(self.h, str(path).encode(), _ptr(a, C.c_int32), len(a)))
+
+    def load_prefix(self, path: str) -> list[int]:
+        buf = np.zeros(self.max_context, np.int32)
+        n = C.c_int(0)
+        self._check(self.lib.ill_load_prefix(self.h, str(path).encode(), _ptr(buf, C.c_int32), len(buf), C.byref(n)))
+        return buf[: n.value].tolist()
 
     # ---- speculative decoding (k_commit_spec drafting on the device) ---------------------
     def load_ngram(self, table: np.ndarray | None):

@@ -157,3 +157,44 @@ def test_spec_fullsize_q4():
     log(f"full q4: passes {passes} accepted {acc}")
     assert toks == g
     assert (passes, acc) == D.simulate(prompt, gx, 48, 16, table=table)[1:]
+
+
+# ---- prefix reuse across requests (Engine.swift:788-838, :929-933) ------------------------
+
+def test_prefix_reuse_prefills_only_the_new_tokens(q4_engine):
+    e = q4_engine
+    prompt = _prompt(12, 30)
+    first = e.generate(prompt, max_new=10, chunk=4)
+    cached, pre = e.prefix_info()
+    assert pre == 30 and cached == 30 + 10 - 1
+    # a follow-up prompt extending the conversation reuses the cached K/V
+    prompt2 = prompt + first[:9] + _prompt(13, 5)
+    out2 = e.generate(prompt2, max_new=12, chunk=4)
+    assert e.prefix_info()[1] == 5
+    # the same answer as from a cold cache (a pass outside generate forgets the prefix)
+    e.reset_out_tokens()
+    e.set_state(pos=0, n=4, maxsteps=4)
+    e.prefill(prompt[:4])
+    assert e.prefix_info()[0] == 0
+    cold = e.generate(prompt2, max_new=12, chunk=4)
+    assert e.prefix_info()[1] == len(prompt2)
+    assert out2 == cold
+    # the same prompt again: only its last token is prefilled; speculative calls reuse too
+    again, _, _ = e.generate_spec(prompt2, 12, rows=8, chunk=4)
+    assert e.prefix_info()[1] == 1 and again == cold
+
+
+def test_prefix_save_and_load(q4_engine, tmp_path):
+    e = q4_engine
+    prompt = _prompt(14, 40)
+    ref = e.generate(prompt, max_new=16, chunk=4)
+    f = str(tmp_path / "prefix.bin")
+    e.save_prefix(f, prompt)
+    # clobber the cache, then load the saved prefix: generation continues from it
+    e.reset_out_tokens()
+    e.set_state(pos=0, n=8, maxsteps=4)
+    e.prefill(_prompt(15, 8))
+    toks = e.load_prefix(f)
+    assert toks == prompt and e.prefix_info()[0] == 40
+    out = e.generate(prompt, max_new=16, chunk=4)
+    assert e.prefix_info()[1] == 1 and out == ref

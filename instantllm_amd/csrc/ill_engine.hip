@@ -181,6 +181,14 @@ int launch(ill_engine* e, int T) {
   return 0;
 }
 
+// The drafting kernel after a launch whose commit is speculative (it returns at once unless
+// that commit left a draft pending).
+int launch_draft(ill_engine* e) {
+  hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  HCK(hipGetLastError());
+  return 0;
+}
+
 int check_err(ill_engine* e) {
   int32_t err = 0;
   HCK(hipMemcpyAsync(&err, &e->ctl->err, 4, hipMemcpyDeviceToHost, e->stream));
@@ -621,7 +629,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     return hipMemset(*p, 0, bytes) == hipSuccess;
   };
   const size_t kvb = (size_t)layers * ILL_NKV * e->maxctx * 64 * 2;
-  e->acc_bytes = (size_t)2 * layers * ILL_NKIND * 16 * ILL_H * 8;
+  e->acc_bytes = (size_t)2 * layers * ILL_NKIND * 16 * ILL_ACC_ROW * 8;
   bool ok = dalloc((void**)&e->dlayers, sizeof(IllLayerW) * layers) && dalloc((void**)&e->st, 64) && dalloc((void**)&e->ctl, 64) &&
             dalloc((void**)&e->ptoks, ILL_OP_MAXM * 4) && dalloc((void**)&e->tree, ILL_TR_INTS * 4) &&
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
@@ -786,6 +794,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
       if ((rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, last ? 1 : 0, last ? write_logits : 0, last ? fin : 0))) return rc;
       e->pos_hint = pos;
       if ((rc = op_launch(e, rows, last ? 1 : 0))) return rc;
+      if (last && fin == 2 && (rc = launch_draft(e))) return rc;
       pos += rows;
       HCK(hipStreamSynchronize(e->stream));
     }
@@ -802,6 +811,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
     else rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, 0, 0, 0);
     if (rc) return rc;
     if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
+    if (last && fin == 2 && (rc = launch_draft(e))) return rc;
     pos += rows;
     // the staging copies above read host memory asynchronously: keep `toks` alive
     HCK(hipStreamSynchronize(e->stream));
@@ -860,6 +870,7 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
   if ((rc = set_ctl(e, tree ? ILL_MODE_TREE : ILL_MODE_ROWS, rows, 0, rows, write_logits, 2))) return rc;
   e->pos_hint = s.pos;
   if ((rc = e->fmt == 2 ? launch(e, rows == 1 ? 1 : 16) : op_launch(e, rows, rows))) return rc;
+  if ((rc = launch_draft(e))) return rc;   // the next pass's drafts (ill_spec_pass continues from here)
   e->pos_hint = s.pos + 1;   // at least the root is accepted
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = rows;
@@ -913,10 +924,12 @@ int ill_spec_pass(ill_engine* e, int write_logits) {
   if (s.done) return ILL_OK;   // a stopped request: nothing to do (the device would early-exit)
   IllCtl c;
   HCK(hipMemcpy(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost));
-  if (c.commit != 2 || c.nrows < 1 || c.nrows > ILL_MAXT) return fail(ILL_E_ARG, "no drafted pass pending (prefill with the State's tspec > 1 first)");
+  if (c.commit != 2 || c.draft || c.nrows < 1 || c.nrows > ILL_MAXT)
+    return fail(ILL_E_ARG, "no drafted pass pending (prefill with the State's tspec > 1, or run a verify pass, first)");
   if ((rc = set_wlog(e, write_logits))) return rc;
   e->pos_hint = s.pos;
   if ((rc = e->fmt == 2 ? launch(e, 16) : op_launch(e, c.nrows, c.nrows))) return rc;
+  if ((rc = launch_draft(e))) return rc;
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = c.nrows;
   return ILL_OK;
@@ -928,8 +941,10 @@ int ill_capture_spec(ill_engine* e, int npasses) {
   drop_graph(e);
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-  for (int i = 0; i < npasses; i++)
+  for (int i = 0; i < npasses; i++) {
     hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
+    hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  }
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = npasses;

@@ -160,8 +160,15 @@ __device__ __forceinline__ void fx_add(uint64_t* p, uint64_t w) {
   __hip_atomic_fetch_add((GAS unsigned long long*)p, (unsigned long long)w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Column c of an accumulator row sits ILL_ACC_STRIDE words after column c - 1, so that a
+// stride above 1 spreads the contributors' atomics over more cache lines.
+#ifndef ILL_ACC_STRIDE
+#define ILL_ACC_STRIDE 1
+#endif
+#define ILL_ACC_ROW (ILL_H * ILL_ACC_STRIDE)
+__device__ __forceinline__ size_t acc_col(int c) { return (size_t)c * ILL_ACC_STRIDE; }
 __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int l, int kind, int t) {
-  return a.acc + ((((size_t)bank * a.W.layers + l) * ILL_NKIND + kind) * 16 + t) * ILL_H;
+  return a.acc + ((((size_t)bank * a.W.layers + l) * ILL_NKIND + kind) * 16 + t) * ILL_ACC_ROW;
 }
 // Copies in use: 16-row passes read every word 16 times over, so they keep one of each.
 // Kinds per layer: XA copies 0 .. xa_copies - 1, XB copies from ILL_XA_COPIES on.
@@ -189,7 +196,7 @@ struct SrcRes {
     int64_t sum = 0;
 #pragma unroll
     for (int k = 0; k < NC; k++) {
-      const uint64_t w = aload64(base + ((size_t)k * 16 + t) * ILL_H + c);
+      const uint64_t w = aload64(base + ((size_t)k * 16 + t) * ILL_ACC_ROW + acc_col(c));
       ok &= fx_count(w) == (XB ? xb_expect<T>(k) : xa_expect<T>(k));
       sum += fx_value(w);
     }
@@ -528,8 +535,6 @@ struct CommitLds {
   int g[16];
   int path[16];
   int npath, pos0;
-  int draft, have, last, stop;      // drafting after the commit: on, tokens committed, last token
-  DraftLds dr;
 };
 
 template <int T>
@@ -826,8 +831,8 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
       return v;
     };
     const float ya = out(Sa, sa), yb = out(Sb, sb);
-    fx_add(accw + 16 * ka + n, fx_word(fx_of(ya)));
-    if (kg < 3) fx_add(accw + 16 * kb + n, fx_word(fx_of(yb)));
+    fx_add(accw + acc_col(16 * ka + n), fx_word(fx_of(ya)));
+    if (kg < 3) fx_add(accw + acc_col(16 * kb + n), fx_word(fx_of(yb)));
     return;
   }
   const uint4 xh = ahi[kg * T + arow<T>(n)];
@@ -866,7 +871,7 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
     const int t = 4 * kg + j;
     if (t < nrows) {
 #pragma unroll
-      for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_H + 16 * k + n, fx_word(fx_of(y[k][j])));
+      for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_ACC_ROW + acc_col(16 * k + n), fx_word(fx_of(y[k][j])));
     }
   }
 }
@@ -1302,7 +1307,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   wait_vm();   // this wave's staged O tiles
   trace_mark(a, ILL_TRL * l + 9);
   split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, h % xa_copies<T>(), 0) + 16 * 7 * w);
+                acc_ptr(a, H.bank, l, h % xa_copies<T>(), 0) + acc_col(16 * 7 * w));
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -1362,7 +1367,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 5);
   split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + 16 * 7 * w);
+                acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + acc_col(16 * 7 * w));
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -1381,13 +1386,14 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
   const int tid = tid_opaque();
   constexpr int PER = (T * ILL_H + ILL_WG_THREADS - 1) / ILL_WG_THREADS;
   const int n = H.nrows * ILL_H;
+  auto at = [](int i) { return (size_t)(i / ILL_H) * ILL_ACC_ROW + acc_col(i % ILL_H); };   // element i = row * 896 + column
   auto wait_full = [&](const uint64_t* src, int expect, int code) {
     return wg_wait([&]() {
       bool r = true;
 #pragma unroll
       for (int k = 0; k < PER; k++) {
         const int i = tid + k * ILL_WG_THREADS;
-        if (i < n) r &= fx_count(aload64(src + i)) == expect;
+        if (i < n) r &= fx_count(aload64(src + at(i))) == expect;
       }
       return r;
     }, a.ctl, code);
@@ -1398,35 +1404,35 @@ __device__ __forceinline__ bool role_base(const IllPassArgs& a, const PassHdr& H
 #pragma unroll
     for (int k = 0; k < PER; k++) {
       const int i = tid + k * ILL_WG_THREADS;
-      if (i < n) fx_add(xa + i, fx_word(fx_of(embed1(a.W, H.tok[i / ILL_H], i % ILL_H))));
+      if (i < n) fx_add(xa + at(i), fx_word(fx_of(embed1(a.W, H.tok[i / ILL_H], i % ILL_H))));
     }
   } else {
     const uint64_t* prev = acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0);
 #pragma unroll
     for (int c = 0; c < xb_copies<T>(); c++)
-      if (!wait_full(prev + (size_t)c * 16 * ILL_H, xb_expect<T>(c), 800 + l)) return false;
+      if (!wait_full(prev + (size_t)c * 16 * ILL_ACC_ROW, xb_expect<T>(c), 800 + l)) return false;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
       const int i = tid + k * ILL_WG_THREADS;
       if (i < n) {
         int64_t sum = 0;
 #pragma unroll
-        for (int c = 0; c < xb_copies<T>(); c++) sum += fx_value(aload64(prev + (size_t)c * 16 * ILL_H + i));
-        fx_add(xa + i, fx_word(sum));
+        for (int c = 0; c < xb_copies<T>(); c++) sum += fx_value(aload64(prev + (size_t)c * 16 * ILL_ACC_ROW + at(i)));
+        fx_add(xa + at(i), fx_word(sum));
       }
     }
   }
 #pragma unroll
   for (int c = 0; c < xa_copies<T>(); c++)
-    if (!wait_full(xa + (size_t)c * 16 * ILL_H, xa_expect<T>(c), 850 + l)) return false;
+    if (!wait_full(xa + (size_t)c * 16 * ILL_ACC_ROW, xa_expect<T>(c), 850 + l)) return false;
 #pragma unroll
   for (int k = 0; k < PER; k++) {
     const int i = tid + k * ILL_WG_THREADS;
     if (i < n) {
       int64_t sum = 0;
 #pragma unroll
-      for (int c = 0; c < xa_copies<T>(); c++) sum += fx_value(aload64(xa + (size_t)c * 16 * ILL_H + i));
-      fx_add(xb + i, fx_word(sum));
+      for (int c = 0; c < xa_copies<T>(); c++) sum += fx_value(aload64(xa + (size_t)c * 16 * ILL_ACC_ROW + at(i)));
+      fx_add(xb + at(i), fx_word(sum));
     }
   }
   return true;
@@ -1551,7 +1557,7 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
   for (size_t i = lo + tid_opaque(); i < hi; i += ILL_WG_THREADS) {
     const size_t r = i / per_row, c = i % per_row;
     const size_t lk = r / H.zrows, t = r % H.zrows;
-    gst(a.acc + ((((size_t)other * NL) * ILL_NKIND + lk) * 16 + t) * ILL_H + c, (uint64_t)0);
+    gst(a.acc + ((((size_t)other * NL) * ILL_NKIND + lk) * 16 + t) * ILL_ACC_ROW + acc_col((int)c), (uint64_t)0);
   }
 }
 
@@ -1647,10 +1653,9 @@ __device__ __forceinline__ uint32_t wg_max_u32(uint32_t v, uint32_t* slots) {
 // (match length, j) picks the same one. Then the next pass is set up as a chain over
 // [last token, drafts...] with one row per token (rows, lm_head rows and commit of the
 // control block, the State's n and nver).
-__device__ __noinline__ void spec_draft(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
-  DraftLds& D = C.dr;
+__device__ __forceinline__ void spec_draft(const IllPassArgs& a, int have, int last, int tspec, int nodraft, int eos0, int eos1,
+                                           DraftLds& D) {
   const int i = threadIdx.x;
-  const int have = C.have;
   const int w0 = have > ILL_OB_MAX ? have - ILL_OB_MAX : 0;
   for (int k = w0 + i; k < have; k += ILL_WG_THREADS) D.ob[k - w0] = gld(a.out_dev + k);
   const int np = a.prompt ? min(max(gld(a.prompt), 0), ILL_OB_MAX) : 0;
@@ -1661,8 +1666,8 @@ __device__ __noinline__ void spec_draft(const IllPassArgs& a, const PassHdr& H, 
     D.nd = 0;
   }
   __syncthreads();
-  const int T = min(max(H.tspec, 1), ILL_MAXT);
-  const int maxd = H.nodraft ? 0 : T - 1;
+  const int T = min(max(tspec, 1), ILL_MAXT);
+  const int maxd = nodraft ? 0 : T - 1;
   for (int nd = 0; nd < maxd; nd++) {
     const int L = D.L;
     // 1. self-repetition: position j (1 <= j <= L - 1) continues a match of m >= 3 tokens
@@ -1728,10 +1733,11 @@ __device__ __noinline__ void spec_draft(const IllPassArgs& a, const PassHdr& H, 
       D.nd = nd + 1;
     }
     __syncthreads();
-    if (d == H.eos0 || d == H.eos1) break;
+    if (d == eos0 || d == eos1) break;
   }
   if (i == 0) {
     const int rows = 1 + D.nd;
+    a.ptoks[0] = last;
     a.st->n = rows;
     a.st->nver = rows;
     IllCtl* c = a.ctl;
@@ -1740,7 +1746,29 @@ __device__ __noinline__ void spec_draft(const IllPassArgs& a, const PassHdr& H, 
     c->lmh_row0 = 0;
     c->lmh_rows = rows;
     c->commit = 2;
+    c->draft = 0;
   }
+}
+
+// The drafting step after a speculative commit, as its own launch (one workgroup) so that
+// the pass kernel carries none of its code: it runs when the commit left a draft pending
+// (a speculative commit that did not stop) and returns at once otherwise.
+__global__ __launch_bounds__(ILL_WG_THREADS) void ill_draft_kernel(IllPassArgs a) {
+  __shared__ DraftLds D;
+  __shared__ int go, have, last, tspec, nodraft, eos0, eos1;
+  if (threadIdx.x == 0) {
+    const IllState* st = a.st;
+    go = a.ctl->draft && !st->done;
+    have = st->step;
+    last = a.ctl->last_tok;
+    tspec = st->tspec;
+    nodraft = st->nodraft;
+    eos0 = st->eos0;
+    eos1 = st->eos1;
+  }
+  __syncthreads();
+  if (!go) return;
+  spec_draft(a, have, last, tspec, nodraft, eos0, eos1, D);
 }
 
 // Commit of the pass's argmaxes C.g[t] (rows lmh0 ..): token record, State advance, stop
@@ -1754,7 +1782,6 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
   if (i == 0) {
     C.npath = 0;
     C.pos0 = H.pos;
-    C.draft = 0;
     if (H.commit == 0) {
       st->pos = H.pos + H.nrows;
     } else if (H.commit == 1) {
@@ -1819,9 +1846,7 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
       a.ptoks[0] = last;
       a.ctl->last_tok = last;
       C.npath = H.mode == ILL_MODE_TREE ? m : 0;
-      C.draft = !stop;
-      C.have = step;
-      C.last = last;
+      a.ctl->draft = stop ? 0 : 1;   // ill_draft_kernel drafts the next pass
     }
   }
   __syncthreads();
@@ -1841,7 +1866,6 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
     }
     __syncthreads();
   }
-  if (C.draft) spec_draft(a, H, C);   // workgroup-uniform (LDS, after the barrier)
   if (pass_kernel && i == 0) {
     a.ctl->bank_rows[H.bank] = H.nrows;   // rows of this bank to clear during the next pass
     a.ctl->bank_rows[H.bank ^ 1] = 0;     // cleared during this pass

@@ -171,11 +171,20 @@ int set_ctl(ill_engine* e, int mode, int nrows, int lmh0, int lmhn, int wlog, in
 
 int count_passes(ill_engine* e, int n);
 
+// The pass-kernel instantiation for a pass of `rows` rows: 1, up to 4, up to 16 (a row's
+// arithmetic is the same in each).
+int pass_T(int rows) { return rows <= 1 ? 1 : (rows <= 4 ? 4 : 16); }
+
+void enqueue_pass(ill_engine* e, int T) {
+  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
+  else if (T == 4) hipLaunchKernelGGL(ill_pass_kernel<4>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(4), e->stream, e->args);
+  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
+}
+
 int launch(ill_engine* e, int T) {
   if (int rc = count_passes(e, 1)) return rc;
   HCK(hipEventRecord(e->ev0, e->stream));
-  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
-  else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
+  enqueue_pass(e, T);
   HCK(hipGetLastError());
   HCK(hipEventRecord(e->ev1, e->stream));
   return 0;
@@ -552,13 +561,16 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   if (hipSetDevice(0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "no HIP device"));
   int maxb = 0, maxb1 = 0;
   if (hipFuncSetAttribute((const void*)ill_pass_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, ill_stage_bytes(1)) != hipSuccess ||
+      hipFuncSetAttribute((const void*)ill_pass_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, ill_stage_bytes(4)) != hipSuccess ||
       hipFuncSetAttribute((const void*)ill_pass_kernel<16>, hipFuncAttributeMaxDynamicSharedMemorySize, ill_stage_bytes(16)) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "cannot raise the pass kernel's LDS limit to %d B", ill_stage_bytes(1)));
+  int maxb4 = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb, ill_pass_kernel<16>, ILL_WG_THREADS, ill_stage_bytes(16)) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb1, ill_pass_kernel<1>, ILL_WG_THREADS, ill_stage_bytes(1)) != hipSuccess ||
-      maxb < 1 || maxb1 < 1)
-    return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d / %d)", maxb1, maxb));
-  maxb = std::min(maxb, maxb1);
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&maxb4, ill_pass_kernel<4>, ILL_WG_THREADS, ill_stage_bytes(4)) != hipSuccess ||
+      maxb < 1 || maxb1 < 1 || maxb4 < 1)
+    return cleanup(fail(ILL_E_HIP, "pass kernel cannot be resident (occupancy %d / %d / %d)", maxb1, maxb4, maxb));
+  maxb = std::min(std::min(maxb, maxb1), maxb4);
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return cleanup(fail(ILL_E_HIP, "hipGetDeviceProperties failed"));
   if (prop.multiProcessorCount * maxb < ILL_WG)
@@ -810,7 +822,7 @@ int ill_prefill(ill_engine* e, const int32_t* toks, int n, int write_logits) {
     if (last) rc = set_ctl(e, ILL_MODE_ROWS, rows, rows - 1, 1, write_logits, fin);
     else rc = set_ctl(e, ILL_MODE_ROWS, rows, 0, 0, 0, 0);
     if (rc) return rc;
-    if ((rc = launch(e, rows == 1 ? 1 : 16))) return rc;
+    if ((rc = launch(e, pass_T(rows)))) return rc;
     if (last && fin == 2 && (rc = launch_draft(e))) return rc;
     pos += rows;
     // the staging copies above read host memory asynchronously: keep `toks` alive
@@ -869,7 +881,7 @@ int ill_verify_pass(ill_engine* e, int rows, const int32_t* tree, const int32_t*
   if ((rc = write_pos_n(e, s.pos, rows))) return rc;
   if ((rc = set_ctl(e, tree ? ILL_MODE_TREE : ILL_MODE_ROWS, rows, 0, rows, write_logits, 2))) return rc;
   e->pos_hint = s.pos;
-  if ((rc = e->fmt == 2 ? launch(e, rows == 1 ? 1 : 16) : op_launch(e, rows, rows))) return rc;
+  if ((rc = e->fmt == 2 ? launch(e, pass_T(rows)) : op_launch(e, rows, rows))) return rc;
   if ((rc = launch_draft(e))) return rc;   // the next pass's drafts (ill_spec_pass continues from here)
   e->pos_hint = s.pos + 1;   // at least the root is accepted
   if ((rc = check_err(e))) return rc;
@@ -928,7 +940,7 @@ int ill_spec_pass(ill_engine* e, int write_logits) {
     return fail(ILL_E_ARG, "no drafted pass pending (prefill with the State's tspec > 1, or run a verify pass, first)");
   if ((rc = set_wlog(e, write_logits))) return rc;
   e->pos_hint = s.pos;
-  if ((rc = e->fmt == 2 ? launch(e, 16) : op_launch(e, c.nrows, c.nrows))) return rc;
+  if ((rc = e->fmt == 2 ? launch(e, pass_T(c.nrows)) : op_launch(e, c.nrows, c.nrows))) return rc;
   if ((rc = launch_draft(e))) return rc;
   if ((rc = check_err(e))) return rc;
   if (write_logits) e->logits_rows_valid = c.nrows;
@@ -939,10 +951,14 @@ int ill_capture_spec(ill_engine* e, int npasses) {
   if (!e || npasses < 1) return fail(ILL_E_ARG, "bad pass count");
   if (e->fmt != 2) return fail(ILL_E_FORMAT, "chained speculative passes need the q4 pass kernel (format %d passes size their launches on the host)", e->fmt);
   drop_graph(e);
+  // every pass has at most the State's tspec rows: the smallest instantiation that holds them
+  IllState s;
+  if (int rc = read_state(e, &s)) return rc;
+  const int T = pass_T(std::max(2, std::min(s.tspec, ILL_MAXT)));
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   for (int i = 0; i < npasses; i++) {
-    hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
+    enqueue_pass(e, T);
     hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
   }
   HCK(hipStreamEndCapture(e->stream, &e->graph));

@@ -174,6 +174,10 @@ __device__ __forceinline__ uint64_t* acc_ptr(const IllPassArgs& a, int bank, int
 // Kinds per layer: XA copies 0 .. xa_copies - 1, XB copies from ILL_XA_COPIES on.
 template <int T>
 __host__ __device__ constexpr int xa_copies() { return T == 1 ? ILL_XA_COPIES : 1; }
+// 16-row passes read their RMSNorm codings from PREP publications; passes of up to 4 rows
+// code the accumulators themselves, as 1-row passes do.
+template <int T>
+__host__ __device__ constexpr bool ill_pub() { return T > 4; }
 template <int T>
 __host__ __device__ constexpr int xb_copies() { return T == 1 ? ILL_XB_COPIES : 1; }
 #define ILL_KIND_XB ILL_XA_COPIES
@@ -899,7 +903,8 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
   // SP: lane (kg, n) holds q_t . k_n for rows t = 4 kg + j
   v4f sp = {0.f, 0.f, 0.f, 0.f};
   {
-    const v8h k0 = u4_to_v8h(*(const uint4*)&A.k[n][8 * kg]), k1 = u4_to_v8h(*(const uint4*)&A.k[n][32 + 8 * kg]);
+    const int kr = arow<T>(n);   // pass rows beyond T: copies (their columns are never gathered)
+    const v8h k0 = u4_to_v8h(*(const uint4*)&A.k[kr][8 * kg]), k1 = u4_to_v8h(*(const uint4*)&A.k[kr][32 + 8 * kg]);
     sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][0], k0, sp, 0, 0, 0);
     sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[0][1], k0, sp, 0, 0, 0);
     sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], k1, sp, 0, 0, 0);
@@ -949,7 +954,8 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
 #pragma unroll
   for (int j = 0; j < 4; j++) {
 #pragma unroll
-    for (int b = 0; b < 4; b++) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
+    for (int b = 0; b < 4; b++)
+      if (4 * kg + j < T) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
   }
   wave_lds_sync();
   v8h ph[2], pl[2];
@@ -957,7 +963,7 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
   for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float p = pb[n * 64 + 32 * ks + 8 * kg + i];
+      const float p = pb[arow<T>(n) * 64 + 32 * ks + 8 * kg + i];
       const _Float16 hi = (_Float16)p;
       ph[ks][i] = hi;
       pl[ks][i] = (_Float16)(p - (float)hi);
@@ -1074,7 +1080,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   // ---- input x_l: embedding (layer 0) or the completed accumulator XB[l-1]
   bool ok;
   float rs[4];   // RMSNorm scale of this lane's rows
-  if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 1, l, 0), tagof_pub(H.epoch, l), nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
+  if constexpr (ill_pub<T>()) ok = pub_read<T>(pub_ptr(a, 1, l, 0), tagof_pub(H.epoch, l), nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
   else if (l == 0) ok = prep896<T>(SrcEmbed{a.W, H.tok}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs);
   else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, l - 1, ILL_KIND_XB, 0)}, L.ln1, nrows, A.u.prep, a.ctl, 100 + l, a, rs, ILL_TRL * l + 15);
   if (!ok) return false;
@@ -1159,9 +1165,9 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   if constexpr (T > 1) {   // path values of the pass rows at positions 8 (pos / 8) + q, q < 24 (part_eval16)
     uint4* vq = (uint4*)(stage + ILL_ST_VPT);
     const int d0 = 8 * (pos >> 3) - pos;   // depth of q = 0 (-7 .. 0)
-    static_assert(T * 32 == ILL_WG_THREADS, "one thread per (row, dim pair)");
-    const int t1 = tid >> 5, dp = tid & 31;   // row t1, dims 2 dp and 2 dp + 1
-    const int dep = t1 < nrows ? H.depth[t1] : -1;
+    static_assert(T * 32 <= ILL_WG_THREADS, "one thread per (row, dim pair)");
+    const int t1 = min(tid >> 5, T - 1), dp = tid & 31;   // row t1, dims 2 dp and 2 dp + 1
+    const int dep = (tid >> 5) < nrows ? H.depth[t1] : -1;
     uint32_t e[24];   // both dims' values (low half: dim 2 dp)
 #pragma unroll
     for (int q = 0; q < 24; q++) {
@@ -1175,7 +1181,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
       for (int q = 0; q < 24; q++) h[q] = hf ? e[q] >> 16 : e[q] & 0xffffu;
 #pragma unroll
       for (int s3 = 0; s3 < 3; s3++)
-        vq[(t1 * 64 + 2 * dp + hf) * 3 + s3] = make_uint4(h[8 * s3] | (h[8 * s3 + 1] << 16), h[8 * s3 + 2] | (h[8 * s3 + 3] << 16),
+        if ((tid >> 5) < T) vq[(t1 * 64 + 2 * dp + hf) * 3 + s3] = make_uint4(h[8 * s3] | (h[8 * s3 + 1] << 16), h[8 * s3 + 2] | (h[8 * s3 + 3] << 16),
                                                          h[8 * s3 + 4] | (h[8 * s3 + 5] << 16), h[8 * s3 + 6] | (h[8 * s3 + 7] << 16));
     }
     lds_barrier();
@@ -1334,7 +1340,7 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   constexpr int RPL = T >= 4 ? 4 : T;
   float rs[4];   // RMSNorm scale of this lane's rows
   bool ok;
-  if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 0, l, 0), tagof_pub(H.epoch, l), nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6);
+  if constexpr (ill_pub<T>()) ok = pub_read<T>(pub_ptr(a, 0, l, 0), tagof_pub(H.epoch, l), nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6);
   else ok = prep896<T>(SrcXA<T>{acc_ptr(a, H.bank, l, 0, 0)}, L.ln2, nrows, G.prep, a.ctl, 400 + l, a, rs, ILL_TRL * l + 6);
   if (!ok) return false;
   trace_mark(a, ILL_TRL * l + 1);
@@ -1489,7 +1495,7 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
     float rs[4];   // final-norm scale of this lane's rows
     bool ok;
-    if constexpr (T > 1) ok = pub_read<T>(pub_ptr(a, 1, NL, 0), tagof_pub(H.epoch, NL), H.nrows, Lm.prep, a.ctl, 600, a, rs);
+    if constexpr (ill_pub<T>()) ok = pub_read<T>(pub_ptr(a, 1, NL, 0), tagof_pub(H.epoch, NL), H.nrows, Lm.prep, a.ctl, 600, a, rs);
     else ok = prep896<T>(SrcXB<T>{acc_ptr(a, H.bank, NL - 1, ILL_KIND_XB, 0)}, a.W.fnorm, H.nrows, Lm.prep, a.ctl, 600, a, rs);
     if (!ok) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
@@ -1918,7 +1924,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       if (!role_base<T>(a, H, l)) return;
       trace_mark(a, ILL_TRL * l + 11);
     }
-  } else if (T > 1 && wg >= ILL_R_PREP0 && wg < ILL_R_PREP0 + ILL_MAXT) {
+  } else if (ill_pub<T>() && wg >= ILL_R_PREP0 && wg < ILL_R_PREP0 + ILL_MAXT) {
     const int t = wg - ILL_R_PREP0;
     if (t < H.nrows) {
       if (!role_prep<T>(a, H, S.prep1, t)) return;

@@ -195,8 +195,10 @@ def _decode_vs_chain(e, prompt, nsteps=15):
     return steps, graph_last, rows
 
 
-def test_decode_steps_equal_chain_pass_rows_small():
-    """Small q4 model, prompt of 58 (the steps cross the 64-position chunk boundary)."""
+@pytest.mark.parametrize("nsteps", [15, 4, 3])
+def test_decode_steps_equal_chain_pass_rows_small(nsteps):
+    """Small q4 model, prompt of 58 (the steps cross the 64-position chunk boundary); chains
+    of 15 rows (the 16-row kernel) and of 4 and 3 rows (the 4-row kernel)."""
     from instantllm_amd.engine import Engine
     import tempfile
     import os
@@ -206,7 +208,7 @@ def test_decode_steps_equal_chain_pass_rows_small():
         e = Engine(path, max_context=1024, max_pass=16, max_steps=256)
         try:
             prompt = [int(t) for t in np.random.default_rng(21).integers(0, 4096, size=58)]
-            steps, graph_last, rows = _decode_vs_chain(e, prompt)
+            steps, graph_last, rows = _decode_vs_chain(e, prompt, nsteps)
         finally:
             e.close()
     for r in range(len(rows)):

@@ -174,6 +174,24 @@ def test_tree_rows_bit_identical_to_sequential_steps(engine, prefix):
             assert np.array_equal(one.view(np.uint32), rows[r].view(np.uint32)), (p, k, r)
 
 
+@pytest.mark.parametrize("prefix,nrows", [(61, 4), (300, 3)])
+def test_small_tree_rows_bit_identical(engine, prefix, nrows):
+    """Trees of up to 4 rows run on the 4-row kernel: still equal to 1-row steps bit for bit."""
+    rng = np.random.default_rng(25 + prefix)
+    ctx, st = _ctx(engine, rng, prefix)
+    tr = T.random_tree(rng, nrows, VOCAB)
+    engine.set_state(pos=st["pos"], n=nrows, maxsteps=200, eos=(-5, -5))
+    engine.verify_pass(nrows, tree=tr, write_logits=True)
+    rows = np.stack([engine.read_logits(r) for r in range(nrows)])
+    tok = tr[T.TR_TOK:T.TR_TOK + nrows]
+    for p in T.paths(tr):
+        for k, r in enumerate(p):
+            engine.set_state(pos=st["pos"] + k, n=1, maxsteps=200, eos=(-5, -5))
+            engine.prefill([int(tok[r])], write_logits=True)
+            one = engine.read_logits(0)
+            assert np.array_equal(one.view(np.uint32), rows[r].view(np.uint32)), (p, k, r)
+
+
 def test_tree_logits_match_oracle(engine, q4_small):
     _, m = q4_small
     rng = np.random.default_rng(30)

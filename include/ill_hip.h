@@ -136,6 +136,47 @@ int ill_capture_spec(ill_engine* e, int npasses);
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
                       int32_t* out, int* n_out, int32_t* stats);
 
+/* ---- Learned drafter (ILDraft.swift:1-209, k_ildraft Shaders.swift:421-872) ----------------
+ * A table in the ILDRAFT1 format (tools/draft/ildraft.py:16-53) scores the candidates of the
+ * n-gram statistics, self-repetition, prompt lookup, the request's TF-IDF neighbours'
+ * outputs and the copy candidates with 53 features and a small MLP; a drafting kernel runs
+ * it after each speculative commit and proposes the next pass: a chain of up to
+ * chain_rows - 1 tokens, or a best-first tree of up to tree_budget tokens (8 children per
+ * expansion) verified in one tree pass. Speculation never changes the tokens committed.
+ *
+ * ill_ildraft_open (ILDraft.init, :38-84): reads and checks a table (NULL on error, see
+ * ill_last_error). ill_ildraft_prepare (ILDraft.prepare, :110-208): the per-request context
+ * from the user prompt's ids inside the chat template, its text and the tokenizer
+ * (`encode` writes the ids of a text into ids[0..cap) and returns their count; NULL: no
+ * space-variant candidates). ill_ildraft_request copies the prepared context (the
+ * IllDraftReq layout of instantllm_amd/csrc/ill_ildraft.h) and returns its size in bytes. */
+typedef struct ill_ildraft ill_ildraft;
+typedef int (*ill_encode_fn)(void* user, const char* text, int32_t* ids, int cap);
+ill_ildraft* ill_ildraft_open(const char* path);
+void ill_ildraft_close(ill_ildraft* d);
+int ill_ildraft_prepare(ill_ildraft* d, const int32_t* prompt, int n, const char* text, ill_encode_fn encode, void* user);
+int64_t ill_ildraft_request(const ill_ildraft* d, void* out, int64_t bytes);
+
+/* Engine.loadLearnedDrafter (Engine.swift:901-904): loads a table into the engine. */
+int ill_load_ildraft(ill_engine* e, const char* path);
+
+/* Engine.setDraftContext (Engine.swift:908-913): prepares the next ill_generate_spec
+ * request's drafter context (at once, on the CPU). That call then drafts with the learned
+ * drafter (Engine.swift:950-956) and consumes the context. */
+int ill_set_draft_context(ill_engine* e, const int32_t* prompt, int n, const char* text, ill_encode_fn encode, void* user);
+
+/* Engine.useLearned / learnedT / learnedTree (Engine.swift:871-880): use != 0 lets a
+ * prepared context switch ill_generate_spec to the learned drafter; its passes are chains
+ * of chain_rows (2..16) rows, or with tree_budget > 0 trees of min(tree_budget, 15) drafts
+ * (passes of that + 1 rows; adaptive generation falls back to 8-row chains while fewer than
+ * 1.5 drafts per pass are accepted). Defaults 1, 8, 15. */
+int ill_set_learned(ill_engine* e, int use, int chain_rows, int tree_budget);
+
+/* The pass the last speculative commit set up (no reference counterpart: inspection for
+ * tests and tools): info = [mode (1 chain, 2 tree), rows, commit, drafting still pending];
+ * toks [16] the rows' tokens; tree [65] the tree buffer (Shaders.swift:23-30 layout). */
+int ill_pending_pass(ill_engine* e, int32_t info[4], int32_t toks[16], int32_t tree[65]);
+
 /* ---- Prefix reuse across requests (Engine.swift:788-838, :929-933, :1029-1031) ----------
  * ill_generate / ill_generate_spec keep the tokens whose K/V stay valid after the call (the
  * prompt and every generated token but the last); the next call prefills only the part of

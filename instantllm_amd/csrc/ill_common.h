@@ -58,8 +58,9 @@ struct IllCtl {
   int32_t commit;       // 0: advance pos only (prefill chunk), 1: greedy commit, 2: spec commit
   int32_t last_tok;     // last committed token (decode input)
   int32_t bank_rows[2]; // rows of each residual-accumulator bank still to be cleared
-  int32_t draft;        // a speculative commit left the next pass's drafting to ill_draft_kernel
-  int32_t pad[4];
+  int32_t draft;        // a speculative commit left the next pass's drafting to a drafting kernel
+  int32_t tree_b;       // learned drafter: > 0 drafts a best-first tree of this many tokens
+  int32_t pad[3];
 };
 
 enum IllMode { ILL_MODE_DECODE = 0, ILL_MODE_ROWS = 1, ILL_MODE_TREE = 2 };

@@ -24,6 +24,7 @@
 #include "ill_gemv.h"
 #include "ill_ops.h"
 #include "ill_quant.h"
+#include "ill_ildraft_host.h"
 
 namespace {
 
@@ -123,7 +124,19 @@ struct ill_engine {
   int32_t* spec_host = nullptr;   // pinned [2]: passes, accepted drafts (written by spec commits)
   int32_t* prompt = nullptr;      // [4 + 256]: prompt-lookup context of the drafter
   uint8_t* ngram = nullptr;       // n-gram draft table (ILL_NG_SLOTS x 16 B), optional
+  // learned drafter (ILDraft.swift): host table, device copies, per-request context
+  illd::Table* ild = nullptr;
+  uint8_t* dtab = nullptr;
+  uint8_t* dtflg = nullptr;
+  IllDraftReq* dreq = nullptr;
+  IllDraftArgs dargs{};
+  bool draft_ctx_ready = false;   // a context was prepared for the next generate_spec call
+  bool learned_active = false;    // the State's `learned`: commits leave drafting to ill_ildraft_kernel
+  bool use_learned = true;
+  int learned_T = 8, learned_tree = 15;
   bool graph_spec = false;        // the captured graph holds spec passes (their control comes from the device)
+  int graph_T = 0;                // pass instantiation of the captured spec graph
+  bool graph_learned = false;     // its drafting kernel is the learned drafter's
   // Engine.cachedTokens (Engine.swift:929-933, :1029-1031): tokens whose K/V are valid at
   // positions 0.. after the last generate call; any pass launched outside generate clears it
   std::vector<int32_t> cached;
@@ -191,9 +204,17 @@ int launch(ill_engine* e, int T) {
 }
 
 // The drafting kernel after a launch whose commit is speculative (it returns at once unless
-// that commit left a draft pending).
+// that commit left a draft pending): the learned drafter's while the State says so, else the
+// commit's own drafting (self-repetition, n-gram table, prompt lookup).
+void enqueue_draft(ill_engine* e) {
+  if (e->learned_active)
+    hipLaunchKernelGGL(ill_ildraft_kernel, dim3(1), dim3(ILD_THREADS), 0, e->stream, e->args, e->dargs);
+  else
+    hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+}
+
 int launch_draft(ill_engine* e) {
-  hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+  enqueue_draft(e);
   HCK(hipGetLastError());
   return 0;
 }
@@ -242,6 +263,7 @@ void drop_graph(ill_engine* e) {
   e->gexec = nullptr;
   e->graph = nullptr;
   e->graph_steps = 0;
+  e->graph_T = 0;
 }
 
 int read_state(ill_engine* e, IllState* s) {
@@ -736,13 +758,14 @@ int ill_destroy(ill_engine* e) {
   if (e->graph) hipGraphDestroy(e->graph);
   void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
                   e->lmp, e->pub, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
-                  e->octx.q, e->octx.ao, e->octx.h, e->octx.amax, e->opart};
+                  e->octx.q, e->octx.ao, e->octx.h, e->octx.amax, e->opart, e->dtab, e->dtflg, e->dreq};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);
   if (e->spec_host) hipHostFree(e->spec_host);
   if (e->prompt) hipFree(e->prompt);
   if (e->ngram) hipFree(e->ngram);
+  delete e->ild;
   if (e->ev0) hipEventDestroy(e->ev0);
   if (e->ev1) hipEventDestroy(e->ev1);
   if (e->stream) hipStreamDestroy(e->stream);
@@ -768,9 +791,14 @@ int ill_set_state(ill_engine* e, const int32_t state[16]) {
     if (s.n < 1 || s.n > e->maxctx) return fail(ILL_E_ARG, "n %d outside 1..%d", s.n, e->maxctx);
     if (s.pos + ILL_MAXT > e->maxctx) return fail(ILL_E_ARG, "pos %d leaves no room for a pass in the context %d", s.pos, e->maxctx);
   }
+  if (s.learned && !e->ild) return fail(ILL_E_ARG, "the State asks for the learned drafter but no table is loaded");
   HCK(hipMemcpyAsync(e->st, &s, sizeof s, hipMemcpyHostToDevice, e->stream));
+  // the learned drafter's shape: trees of learned_tree drafts, else chains of tspec rows
+  const int32_t tb = s.learned && e->learned_tree > 0 ? std::min(e->learned_tree, ILL_MAXT - 1) : 0;
+  HCK(hipMemcpyAsync(&e->ctl->tree_b, &tb, 4, hipMemcpyHostToDevice, e->stream));
   HCK(hipStreamSynchronize(e->stream));
   e->pos_hint = s.pos;
+  e->learned_active = s.learned != 0;
   return ILL_OK;
 }
 
@@ -959,12 +987,14 @@ int ill_capture_spec(ill_engine* e, int npasses) {
   HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
   for (int i = 0; i < npasses; i++) {
     enqueue_pass(e, T);
-    hipLaunchKernelGGL(ill_draft_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, e->stream, e->args);
+    enqueue_draft(e);
   }
   HCK(hipStreamEndCapture(e->stream, &e->graph));
   HCK(hipGraphInstantiate(&e->gexec, e->graph, nullptr, nullptr, 0));
   e->graph_steps = npasses;
   e->graph_spec = true;
+  e->graph_T = T;
+  e->graph_learned = e->learned_active;
   return ILL_OK;
 }
 
@@ -1220,11 +1250,17 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
                       int32_t* out, int* n_out, int32_t* stats) {
   if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
+  // Requests with a drafter context use the learned drafter (Engine.swift:950-956): chains
+  // of learned_T rows or trees of learned_tree drafts; others the commit's own drafting
+  const bool learned = e->draft_ctx_ready && e->use_learned && e->ild;
+  const int treeb = learned && e->learned_tree > 0 ? std::min(e->learned_tree, ILL_MAXT - 1) : 0;
+  if (learned) rows = treeb > 0 ? treeb + 1 : e->learned_T;
   if (rows < 2 || rows > ILL_MAXT) return fail(ILL_E_ARG, "rows per speculative pass %d outside 2..%d", rows, ILL_MAXT);
   if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
   if (ntok + max_new + ILL_MAXT > e->maxctx)
     return fail(ILL_E_ARG, "prompt of %d tokens + %d new exceeds the context %d (less a 16-slot pass margin)", ntok, max_new, e->maxctx);
   if (chunk < 1) chunk = 1;
+  e->draft_ctx_ready = false;
   *n_out = 0;
   int rc;
   GenScope scope(e);
@@ -1240,24 +1276,30 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   s[7] = 151643;
   s[8] = 1;
   s[9] = rows;   // tspec: the prompt's commit drafts the first pass
+  s[14] = learned ? 1 : 0;
   if ((rc = ill_set_state(e, s))) return rc;
+  int cur_tree = treeb;
+  HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
   if ((rc = ill_prefill(e, toks + common, ntok - common, 0))) return rc;
   const bool graphs = e->fmt == 2;
-  if (graphs && (!e->graph_spec || e->graph_steps != chunk) && (rc = ill_capture_spec(e, chunk))) return rc;
-  // Engine.nextPassShape (Engine.swift:888-898): the configured width while drafts are
+  if (graphs && (!e->graph_spec || e->graph_steps != chunk || e->graph_T != pass_T(rows) || e->graph_learned != learned) &&
+      (rc = ill_capture_spec(e, chunk)))
+    return rc;
+  // Engine.nextPassShape (Engine.swift:888-898): the configured shape while drafts are
   // accepted (at least adaptHi = 1.5 per pass over the last few committed passes), an
-  // 8-row chain otherwise; the width takes effect from the next pass drafted
+  // 8-row chain otherwise; the shape takes effect from the next pass drafted
   std::vector<std::pair<int, int>> hist;
   int cur_rows = rows;
-  auto shape = [&]() {
-    if (!adaptive) return rows;
+  auto shape = [&]() -> std::pair<int, int> {
+    const std::pair<int, int> base(rows, treeb);
+    if (!adaptive) return base;
     const int p = ((volatile int32_t*)e->spec_host)[0], a = ((volatile int32_t*)e->spec_host)[1];
     if (hist.empty() || hist.back().first != p) hist.emplace_back(p, a);
-    if (hist.size() < 3) return rows;
+    if (hist.size() < 3) return base;
     const auto& first = hist[hist.size() >= 4 ? hist.size() - 4 : 0];
-    if (p - first.first < 2) return rows;
+    if (p - first.first < 2) return base;
     const double rate = (double)(a - first.second) / (double)(p - first.first);
-    return rate >= 1.5 ? rows : std::min(rows, 8);
+    return rate >= 1.5 ? base : std::pair<int, int>(std::min(rows, 8), 0);
   };
   volatile const int32_t* ot = e->out_host;
   volatile const int32_t* sp = e->spec_host;
@@ -1267,10 +1309,12 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     // keep at most one chunk of passes ahead of the committed ones (Engine.swift:991-1008);
     // every pass commits at least one token, so max_new passes always suffice
     if (encoded < max_new && (!graphs || encoded - (sp[0] - 1) <= chunk)) {
-      const int want = shape();
-      if (want != cur_rows) {   // the State's tspec, ordered after the passes before it
-        cur_rows = want;
+      const std::pair<int, int> want = shape();
+      if (want.first != cur_rows || want.second != cur_tree) {   // ordered after the passes before it
+        cur_rows = want.first;
+        cur_tree = want.second;
         HCK(hipMemcpyAsync(&e->st->tspec, &cur_rows, 4, hipMemcpyHostToDevice, e->stream));
+        HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
       }
       if (graphs) {
         if ((rc = ill_launch_graph(e))) return rc;
@@ -1303,6 +1347,99 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     stats[0] = st.passes;
     stats[1] = st.accepted;
   }
+  return ILL_OK;
+}
+
+// ---- learned drafter (ILDraft.swift, Engine.swift:865-913) -------------------------------
+struct ill_ildraft {
+  illd::Table t;
+};
+
+ill_ildraft* ill_ildraft_open(const char* path) {
+  if (!path) {
+    fail(ILL_E_ARG, "null path");
+    return nullptr;
+  }
+  ill_ildraft* d = new ill_ildraft();
+  const std::string err = illd::load(d->t, path);
+  if (!err.empty()) {
+    delete d;
+    fail(ILL_E_FILE, "%s", err.c_str());
+    return nullptr;
+  }
+  return d;
+}
+
+void ill_ildraft_close(ill_ildraft* d) { delete d; }
+
+int ill_ildraft_prepare(ill_ildraft* d, const int32_t* prompt, int n, const char* text, ill_encode_fn encode, void* user) {
+  if (!d || n < 0 || (n > 0 && !prompt)) return fail(ILL_E_ARG, "bad drafter context");
+  illd::prepare(d->t, prompt, n, text, encode, user);
+  return ILL_OK;
+}
+
+int64_t ill_ildraft_request(const ill_ildraft* d, void* out, int64_t bytes) {
+  if (!d) return fail(ILL_E_ARG, "null drafter");
+  if (out && bytes >= (int64_t)sizeof(IllDraftReq)) memcpy(out, &d->t.req, sizeof(IllDraftReq));
+  return (int64_t)sizeof(IllDraftReq);
+}
+
+int ill_load_ildraft(ill_engine* e, const char* path) {
+  if (!e || !path) return fail(ILL_E_ARG, "null argument");
+  illd::Table* t = new illd::Table();
+  const std::string err = illd::load(*t, path);
+  if (!err.empty()) {
+    delete t;
+    return fail(ILL_E_FILE, "%s", err.c_str());
+  }
+  HCK(hipStreamSynchronize(e->stream));
+  if (e->dtab) HCK(hipFree(e->dtab));
+  e->dtab = nullptr;
+  HCK(hipMalloc((void**)&e->dtab, t->blob.size()));
+  HCK(hipMemcpy(e->dtab, t->blob.data(), t->blob.size(), hipMemcpyHostToDevice));
+  if (!e->dtflg) HCK(hipMalloc((void**)&e->dtflg, ILD_VOCAB));
+  HCK(hipMemcpy(e->dtflg, t->tflg.data(), ILD_VOCAB, hipMemcpyHostToDevice));
+  if (!e->dreq) HCK(hipMalloc((void**)&e->dreq, sizeof(IllDraftReq)));
+  HCK(hipMemset(e->dreq, 0, sizeof(IllDraftReq)));
+  delete e->ild;
+  e->ild = t;
+  e->dargs = illd::device_args(*t, e->dtab, e->dtflg, e->dreq);
+  e->draft_ctx_ready = false;
+  drop_graph(e);   // captured drafting kernels hold the old table's pointers
+  return ILL_OK;
+}
+
+int ill_set_draft_context(ill_engine* e, const int32_t* prompt, int n, const char* text, ill_encode_fn encode, void* user) {
+  if (!e || n < 0 || (n > 0 && !prompt)) return fail(ILL_E_ARG, "bad drafter context");
+  if (!e->ild) return ILL_OK;   // no table: the request drafts with the commit's own drafter
+  illd::prepare(*e->ild, prompt, n, text, encode, user);
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipMemcpy(e->dreq, &e->ild->req, sizeof(IllDraftReq), hipMemcpyHostToDevice));
+  e->draft_ctx_ready = true;
+  return ILL_OK;
+}
+
+int ill_set_learned(ill_engine* e, int use, int chain_rows, int tree_budget) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  if (chain_rows < 2 || chain_rows > ILL_MAXT) return fail(ILL_E_ARG, "chain rows %d outside 2..%d", chain_rows, ILL_MAXT);
+  if (tree_budget < 0) return fail(ILL_E_ARG, "negative tree budget");
+  e->use_learned = use != 0;
+  e->learned_T = chain_rows;
+  e->learned_tree = tree_budget;
+  return ILL_OK;
+}
+
+int ill_pending_pass(ill_engine* e, int32_t info[4], int32_t toks[16], int32_t tree[65]) {
+  if (!e || !info) return fail(ILL_E_ARG, "null argument");
+  IllCtl c;
+  HCK(hipStreamSynchronize(e->stream));
+  HCK(hipMemcpy(&c, e->ctl, sizeof c, hipMemcpyDeviceToHost));
+  info[0] = c.mode;
+  info[1] = c.nrows;
+  info[2] = c.commit;
+  info[3] = c.draft;
+  if (toks) HCK(hipMemcpy(toks, e->ptoks, 16 * 4, hipMemcpyDeviceToHost));
+  if (tree) HCK(hipMemcpy(tree, e->tree, ILL_TR_INTS * 4, hipMemcpyDeviceToHost));
   return ILL_OK;
 }
 

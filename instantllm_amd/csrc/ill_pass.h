@@ -42,7 +42,7 @@ struct IllPassArgs {
   IllState* st;
   IllCtl* ctl;
   int32_t* ptoks;          // [16] row tokens of the pass (commit writes [0] for the next step)
-  const int32_t* tree;     // [65]
+  int32_t* tree;           // [65] (written by the host or the learned drafter)
   const float2* rope;      // [maxctx + 16][32] (cos, sin)
   uint16_t* kc;            // K cache [layer][kvh][maxctx][64] f16
   uint16_t* vt;            // V cache transposed per 64 slots [layer][kvh][maxctx/64][64 dims][64] f16

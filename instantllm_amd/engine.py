@@ -23,6 +23,32 @@ STATE_FIELDS = ("pos", "n", "step", "done", "maxctx", "maxsteps", "eos0", "eos1"
 
 _lib = None
 
+# int encode(void* user, const char* text, int32_t* ids, int cap): the tokenizer callback of
+# the learned drafter's request context
+ENCODE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.POINTER(C.c_int32), C.c_int)
+
+# The learned drafter's request context as the device reads it (IllDraftReq, ill_ildraft.h)
+DRAFT_REQ = np.dtype([("np", "<i4"), ("ncopy", "<i4"), ("nnb", "<i4"), ("nas", "<i4"),
+                      ("P", "<i4", 256), ("pprop", "<f4", 256), ("copyTok", "<i4", 256), ("copyInP", "<i4", 256),
+                      ("copyPt", "<f4", 256), ("nbScore", "<f4", 16), ("nbOff", "<i4", 17), ("pad", "<i4", 3),
+                      ("nbTok", "<i4", 16 * 80), ("asTok", "<i4", 1024), ("asMax", "<f4", 1024), ("asCnt", "<i4", 1024)])
+
+
+def _encode_cb(encode):
+    """A C callback for `encode(text: str) -> list[int]` (None: no callback)."""
+    if encode is None:
+        return ENCODE_FN()
+
+    def cb(_user, text, ids, cap):
+        try:
+            got = list(encode(text.decode("utf-8")))
+        except Exception:
+            return 0
+        for i, t in enumerate(got[:cap]):
+            ids[i] = int(t)
+        return len(got)
+    return ENCODE_FN(cb)
+
 
 class IllError(RuntimeError):
     def __init__(self, code: int, msg: str):
@@ -83,6 +109,14 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_gemv_run_noalloc": (C.c_int, [P, C.c_int, P, P, P, P, P]),
         "ill_quantize_q4": (C.c_int, [C.POINTER(F32), C.c_int64, C.c_int, C.POINTER(C.c_uint8), C.POINTER(C.c_uint16), C.c_int]),
         "ill_quantize_q8": (C.c_int, [C.POINTER(F32), C.c_int64, C.c_int, C.c_int, C.POINTER(C.c_int8), C.POINTER(C.c_uint16), C.c_int]),
+        "ill_ildraft_open": (P, [C.c_char_p]),
+        "ill_ildraft_close": (None, [P]),
+        "ill_ildraft_prepare": (C.c_int, [P, ip, C.c_int, C.c_char_p, ENCODE_FN, P]),
+        "ill_ildraft_request": (C.c_int64, [P, P, C.c_int64]),
+        "ill_load_ildraft": (C.c_int, [P, C.c_char_p]),
+        "ill_set_draft_context": (C.c_int, [P, ip, C.c_int, C.c_char_p, ENCODE_FN, P]),
+        "ill_set_learned": (C.c_int, [P, C.c_int, C.c_int, C.c_int]),
+        "ill_pending_pass": (C.c_int, [P, ip, ip, ip]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -252,6 +286,27 @@ class Engine:
                                                _ptr(out, C.c_int32), C.byref(n), _ptr(stats, C.c_int32)))
         return out[: n.value].tolist(), int(stats[0]), int(stats[1])
 
+    # ---- learned drafter (ILDraft.swift, Engine.swift:865-913) ------------------------------
+    def load_ildraft(self, path: str):
+        self._check(self.lib.ill_load_ildraft(self.h, str(path).encode()))
+
+    def set_draft_context(self, prompt_ids, text: str, encode=None):
+        """Engine.setDraftContext: the next generate_spec call drafts with the learned drafter."""
+        a = _i32(prompt_ids)
+        cb = _encode_cb(encode)
+        self._check(self.lib.ill_set_draft_context(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, None))
+
+    def set_learned(self, use: bool = True, chain_rows: int = 8, tree_budget: int = 15):
+        self._check(self.lib.ill_set_learned(self.h, int(use), chain_rows, tree_budget))
+
+    def pending_pass(self):
+        """(mode, rows, tokens, tree) of the pass the last speculative commit set up."""
+        info = np.zeros(4, np.int32)
+        toks = np.zeros(16, np.int32)
+        tree = np.zeros(TR_INTS, np.int32)
+        self._check(self.lib.ill_pending_pass(self.h, _ptr(info, C.c_int32), _ptr(toks, C.c_int32), _ptr(tree, C.c_int32)))
+        return int(info[0]), int(info[1]), toks[: info[1]].tolist(), tree
+
     def last_pass_ms(self) -> float:
         ms = C.c_float(0)
         self._check(self.lib.ill_last_pass_ms(self.h, C.byref(ms)))
@@ -358,3 +413,38 @@ def quantize_q8(w: np.ndarray, group: int = 32, threads: int | None = None) -> t
     if rc != ILL_OK:
         raise IllError(rc, lib.ill_last_error().decode())
     return codes, sc.view(np.float16)
+
+
+class DraftTable:
+    """A learned-drafter table on the host (ILDraft.init / prepare): the per-request context
+    the engine would upload, for inspection."""
+
+    def __init__(self, path: str):
+        self.lib = load_library()
+        h = self.lib.ill_ildraft_open(str(path).encode())
+        if not h:
+            raise IllError(ILL_E_FILE, self.lib.ill_last_error().decode())
+        self.h = h
+
+    def prepare(self, prompt_ids, text: str, encode=None) -> np.ndarray:
+        a = _i32(prompt_ids)
+        cb = _encode_cb(encode)
+        rc = self.lib.ill_ildraft_prepare(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, None)
+        if rc != ILL_OK:
+            raise IllError(rc, self.lib.ill_last_error().decode())
+        n = self.lib.ill_ildraft_request(self.h, None, 0)
+        assert n == DRAFT_REQ.itemsize, (n, DRAFT_REQ.itemsize)
+        buf = np.zeros(1, DRAFT_REQ)
+        self.lib.ill_ildraft_request(self.h, buf.ctypes.data, n)
+        return buf[0]
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.ill_ildraft_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -11,7 +11,8 @@
 // GPU shape: one workgroup of 1024 threads (16 waves). Per drafted token the waves split
 // the sources (wave 0 the six n-gram orders as a cooperative 11-ary search over the sorted
 // keys, 1 self-repetition, 2 prompt lookup, 3 the copy context, 4-11 two neighbours each),
-// then one thread per distinct candidate computes its features and score. The candidate
+// then one thread per distinct candidate writes its 53 features to LDS, and the scorer
+// runs with one lane per hidden unit (16 or 32 lanes per candidate). The candidate
 // set is deduplicated through an LDS hash set, so its order in memory is arbitrary: every
 // decision depends on the set only (argmax by (score desc, token asc); the tree's top 8 by
 // the same order; the softmax normaliser summed in float64 and rounded to float32).
@@ -25,17 +26,19 @@
 #define ILD_MAXAS 1024
 #define ILD_NF 53
 #define ILD_MAXH 32
-#define ILD_W1S 56               // LDS row stride of W1 (16-byte aligned rows)
+#define ILD_W1S 57               // LDS row stride of W1 (odd: the lanes of 16 hidden units hit distinct banks)
 #define ILD_THREADS 1024
 #define ILD_NRAW (85 + ILD_MAXCOPY)
 #define ILD_HASH 1024
 #define ILD_HEAP 128
 #define ILD_OB (ILL_OB_MAX + ILL_MAXT)
 #define ILD_VOCAB 151936
+#define ILD_LG1P 512
 
 // The per-request context (DraftReq, ILDraft.swift:20-35 / Shaders.swift:432-447), with the
-// request-constant copy rates looked up on the host: pprop[i] = rate of P[i] (CPTK, default
-// 0.2), copyPt[i] = rate of copyTok[i] if it is a prompt id, else 0.3.
+// request-constant copy features computed on the host: pprop[i] = rate of P[i] (CPTK,
+// default 0.2), copyPt[i] = rate of copyTok[i] if it is a prompt id, else 0.3, copyF33[i]
+// its feature 33 (the logit over 4).
 struct IllDraftReq {
   int32_t np, ncopy, nnb, nas;
   int32_t P[ILD_MAXP];
@@ -43,6 +46,7 @@ struct IllDraftReq {
   int32_t copyTok[ILD_MAXCOPY];   // ascending
   int32_t copyInP[ILD_MAXCOPY];
   float copyPt[ILD_MAXCOPY];
+  float copyF33[ILD_MAXCOPY];     // ln(pt / (1 - pt)) / 4 of copyPt (float32 ops, ln in float64)
   float nbScore[ILD_MAXNB];
   int32_t nbOff[ILD_MAXNB + 1];
   int32_t pad[3];
@@ -71,11 +75,15 @@ struct IldLds {
   float w1[ILD_MAXH * ILD_W1S];
   float b1[ILD_MAXH], w2[ILD_MAXH], wl[ILD_W1S];
   float b2;
+  float lg1p[ILD_LG1P];      // ln(1 + c) of the counts c < ILD_LG1P
   int ob[ILD_OB];
   int used[ILD_HASH];        // tokens of the output window (hash set)
   int cset[ILD_HASH];        // candidates (hash set)
   int uniq[ILD_NRAW];
   uint64_t ckey[ILD_NRAW];
+  float csc[ILD_NRAW];
+  int ctf[ILD_NRAW];         // '`' count of each candidate
+  float F[ILD_NRAW * ILD_NF]; // feature rows
   int pm[ILD_MAXP];
   // phase A results
   int dist_tot[8], dist_cnt[8], top_tok[8][8], top_cnt[8][8];
@@ -91,16 +99,16 @@ struct IldLds {
   int tr_par[ILL_MAXT], tr_tok[ILL_MAXT], tr_dep[ILL_MAXT];
   uint32_t tr_anc[ILL_MAXT];
   float tr_cum[ILL_MAXT];
+  int tr_tf[ILL_MAXT];
   float h_cum[ILD_HEAP];
-  int h_par[ILD_HEAP], h_tok[ILD_HEAP], h_ord[ILD_HEAP];
+  int h_par[ILD_HEAP], h_tok[ILD_HEAP], h_ord[ILD_HEAP], h_tf[ILD_HEAP];
   int h_n, h_ctr;
-  int tk_tok[8];
+  int tk_tok[8], tk_tf[8];
   float tk_e[8];
   uint64_t red64[ILD_THREADS / 64];
   double redd[ILD_THREADS / 64];
-  int redi[ILD_THREADS / 64];
-  float best_s;
-  int best_t;
+  int best_tf;
+  int flag;
 };
 
 static_assert(ILD_HASH == ILD_THREADS, "the hash sets are cleared one slot per thread");
@@ -264,6 +272,7 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     }
     if (tid < ILD_W1S) S.wl[tid] = tid < ILD_NF ? m[H * ILD_NF + 2 * H + 1 + tid] : 0.f;
     if (tid == 0) S.b2 = m[H * ILD_NF + 2 * H];
+    if (tid < ILD_LG1P) S.lg1p[tid] = ild_logf(1.f + (float)tid);
   }
   for (int k = tid; k < base; k += ILD_THREADS) S.ob[k] = a.out_dev[w0 + k];
   {
@@ -289,6 +298,7 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     S.tr_dep[0] = 0;
     S.tr_anc[0] = 1u;
     S.tr_cum[0] = 1.f;
+    S.tr_tf[0] = 0;
     S.next_rows[0] = last;
   }
   const int MAXM = d.MAXM;
@@ -361,12 +371,15 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
       int toplong = -1, entlow = 0;
       if (ln > 0) {
         toplong = __shfl(etok, (ln - 1) * 10, 64);
-        float ent = 0.f;
-        for (int r = 0; r < lcnt; ++r) {
-          const int c = __shfl(ecnt, (ln - 1) * 10 + r, 64);
-          const float pr = (float)c / (float)ltot;
-          ent = ent - pr * ild_logf(pr);
+        // entropy of the longest order's continuations: the terms pr * ln(pr) in parallel
+        // (lane r of that order's group), summed in order r = 0, 1, ...
+        float term = 0.f;
+        if (g == ln - 1 && gl < lcnt) {
+          const float pr = (float)ecnt / (float)ltot;
+          term = pr * ild_logf(pr);
         }
+        float ent = 0.f;
+        for (int r = 0; r < lcnt; ++r) ent = ent - __shfl(term, (ln - 1) * 10 + r, 64);
         entlow = ent < 0.3f ? 1 : 0;
       }
       if (lane == 0) {
@@ -489,18 +502,14 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     }
     __syncthreads();
     const int nu = S.nu;
-    // ---- phase C: features and score, one thread per candidate ----
-    uint64_t key = 0;
-    float score = 0.f;
-    int tok = 0x7fffffff;
+    // ---- phase C1: features, one thread per candidate, into LDS rows ----
     if (tid < nu) {
-      tok = S.uniq[tid];
-      float f[ILD_NF];
-#pragma unroll
+      const int tok = S.uniq[tid];
+      float* f = S.F + tid * ILD_NF;
       for (int i = 0; i < ILD_NF; ++i) f[i] = 0.f;
       f[0] = 1.f;
+      float f2 = 0.f, f17 = 0.f, f25;
       const int ln = S.s_long;
-#pragma unroll
       for (int n = 1; n <= 6; ++n) {
         const int tot = S.dist_tot[n];
         if (tot < 0) continue;
@@ -520,20 +529,20 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
           if (n == ln) {
             f[1] = p;
             f[3] = ((float)n / 6.f) * p;
-            f[4] = ild_logf(1.f + (float)c);
+            f[4] = c < ILD_LG1P ? S.lg1p[c] : ild_logf(1.f + (float)c);
           }
           if (n == S.s_supp3) f[5] = p;
           if (n == S.s_supp10) f[6] = p;
         }
       }
       if (tok == S.s_toplong) {
-        f[2] = 1.f;
+        f[2] = f2 = 1.f;
         if (S.s_entlow) f[15] = 1.f;
       }
       const int sn = S.self_n;
       if (sn > 0 && tok == S.self_tok) {
         f[16] = (float)sn / 4.f;
-        f[17] = 1.f;
+        f[17] = f17 = 1.f;
         f[18] = sn >= 3 ? 1.f : 0.f;
       }
       for (int q = 0; q < S.pr_cnt; ++q)
@@ -561,15 +570,14 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
         }
         f[23] = nbs;
         f[24] = nbm;
-        f[25] = (float)nbc / (float)max(1, nnb);
+        f[25] = f25 = (float)nbc / (float)max(1, nnb);
         f[26] = nbx;
       }
       const int ci = ild_bsearch(S.R.copyTok, S.R.ncopy, tok);
       const bool usedt = ild_has(S.used, tok);
       const bool inp = ci >= 0 && S.R.copyInP[ci] != 0;
       if (ci >= 0) {
-        const float pt = S.R.copyPt[ci];
-        f[33] = ild_logf(pt / (1.f - pt)) / 4.f;
+        f[33] = S.R.copyF33[ci];
         f[34] = S.c1;
         f[35] = S.c2;
         f[36] = usedt ? 0.f : 1.f;
@@ -578,8 +586,8 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
       }
       f[29] = (tok == 151645 || tok == 151643) ? 1.f : 0.f;
       f[30] = inp ? 1.f : 0.f;
-      f[31] = f[2] * fminf(1.f, 2.f * f[25]);
-      f[32] = f[17] * fminf(1.f, 2.f * f[25]);
+      f[31] = f2 * fminf(1.f, 2.f * f25);
+      f[32] = f17 * fminf(1.f, 2.f * f25);
       f[39] = (Lfull > 0 && (first_out == 73594 || first_out == 13874)) ? 1.f : 0.f;
       f[40] = (Lfull > 0 && first_out == 63) ? 1.f : 0.f;
       const uint32_t tf = tok < ILD_VOCAB ? (uint32_t)d.tflg[tok] : 0u;
@@ -593,24 +601,46 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
         f[46] = S.R.asMax[ai] / 4.f;
         f[47] = (float)min(S.R.asCnt[ai], 4) / 4.f;
       }
-      // scorer: sc = b2 + WL.f + sum_h W2[h] relu(b1[h] + W1[h].f), every step rounded
-      float sc = S.b2;
-#pragma unroll
-      for (int i = 0; i < ILD_NF; ++i) sc = sc + S.wl[i] * f[i];
-      for (int h = 0; h < d.H; ++h) {
-        const float* wr = S.w1 + h * ILD_W1S;
-        float acc = S.b1[h];
-#pragma unroll
-        for (int i = 0; i < ILD_NF; ++i) acc = acc + wr[i] * f[i];
-        sc = sc + S.w2[h] * fmaxf(acc, 0.f);
+      S.ctf[tid] = (int)(tf & 7u);
+    }
+    __syncthreads();
+    // ---- phase C2: the scorer, HL lanes per candidate (lane h: hidden unit h) ----
+    //   a_h = b1[h] + W1[h][0] f[0] + ... + W1[h][52] f[52]        (left to right)
+    //   sc  = b2 + WL[0] f[0] + ... + WL[52] f[52] + W2[0] relu(a_0) + ... + W2[H-1] relu(a_{H-1})
+    // every product and sum rounded to float32 (no contraction), the order of a one-thread loop
+    uint64_t mykey = 0;
+    {
+      const int H = d.H;
+      const int HL = H <= 16 ? 16 : 32;
+      const int h = tid & (HL - 1), gbase = lane & ~(HL - 1);
+      for (int c0 = 0; c0 < nu; c0 += ILD_THREADS / HL) {
+        const int c = c0 + tid / HL;
+        const float* fr = S.F + min(c, nu - 1) * ILD_NF;
+        float acc = 0.f;
+        if (h < H) {
+          const float* wr = S.w1 + h * ILD_W1S;
+          acc = S.b1[h];
+#pragma unroll 8
+          for (int i = 0; i < ILD_NF; ++i) acc = acc + wr[i] * fr[i];
+        }
+        float sc = S.b2;
+#pragma unroll 8
+        for (int i = 0; i < ILD_NF; ++i) sc = sc + S.wl[i] * fr[i];
+        for (int hh = 0; hh < H; ++hh) {
+          const float ah = __shfl(acc, gbase + hh, 64);
+          sc = sc + S.w2[hh] * fmaxf(ah, 0.f);
+        }
+        if (h == 0 && c < nu) {
+          const uint64_t key = ((uint64_t)ild_fkey(sc) << 32) | (uint64_t)(0xffffffffu - (uint32_t)S.uniq[c]);
+          S.csc[c] = sc;
+          S.ckey[c] = key;
+          mykey = key > mykey ? key : mykey;
+        }
       }
-      score = sc;
-      key = ((uint64_t)ild_fkey(sc) << 32) | (uint64_t)(0xffffffffu - (uint32_t)tok);
-      S.ckey[tid] = key;
     }
     // ---- phase D: the best candidate; for trees the top 8 and the normaliser ----
     {
-      const uint64_t m = ild_max64(key, 64);
+      const uint64_t m = ild_max64(mykey, 64);
       if (lane == 0) S.red64[w] = m;
       __syncthreads();
       uint64_t best = 0;
@@ -623,80 +653,113 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
         const float mx = fmaxf(nu > 0 ? bs : 0.f, 0.f);
         double ez = 0.0;
         if (tid < nu) {
-          const float e = ild_expf(score - mx);
+          const uint64_t key = S.ckey[tid];
+          const float e = ild_expf(S.csc[tid] - mx);
           ez = (double)e;
           int rank = 0;
           for (int j = 0; j < nu; ++j) rank += S.ckey[j] > key ? 1 : 0;
           if (rank < 8) {
-            S.tk_tok[rank] = tok;
+            S.tk_tok[rank] = S.uniq[tid];
             S.tk_e[rank] = e;
+            S.tk_tf[rank] = S.ctf[tid];
           }
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) ez += __shfl_xor(ez, off, 64);
         if (lane == 0) S.redd[w] = ez;
         __syncthreads();
-        if (tid == 0) {
+        if (w == 0) {
+          // push the expanded row's top children, then pop best-first (cumulative
+          // probability desc, insertion order asc) until a row to expand or a full tree
           double z = (double)ild_expf(-mx);
           for (int k = 0; k < ILD_THREADS / 64; ++k) z += S.redd[k];
           const float Z = (float)z;
-          const int ntop = min(8, nu);
-          const float pc = S.tr_cum[S.erow];
-          for (int k = 0; k < ntop && S.h_n < ILD_HEAP; ++k) {
-            const int hn = S.h_n;
-            S.h_cum[hn] = (pc * S.tk_e[k]) / Z;
-            S.h_par[hn] = S.erow;
-            S.h_tok[hn] = S.tk_tok[k];
-            S.h_ord[hn] = S.h_ctr++;
-            S.h_n = hn + 1;
+          const int hn0 = S.h_n, ctr0 = S.h_ctr, erow0 = S.erow;
+          const int npush = min(min(8, nu), ILD_HEAP - hn0);
+          const float pc = S.tr_cum[erow0];
+          if (lane < npush) {
+            const int q = hn0 + lane;
+            S.h_cum[q] = (pc * S.tk_e[lane]) / Z;
+            S.h_par[q] = erow0;
+            S.h_tok[q] = S.tk_tok[lane];
+            S.h_tf[q] = S.tk_tf[lane];
+            S.h_ord[q] = ctr0 + lane;
           }
+          ild_wave_sync();
+          if (lane == 0) {
+            S.h_n = hn0 + npush;
+            S.h_ctr = ctr0 + npush;
+          }
+          ild_wave_sync();
           int go = 0;
-          while (S.rows < K + 1 && S.h_n > 0) {
-            int b = 0;
-            for (int q = 1; q < S.h_n; ++q)
-              if (S.h_cum[q] > S.h_cum[b] || (S.h_cum[q] == S.h_cum[b] && S.h_ord[q] < S.h_ord[b])) b = q;
-            const float cum = S.h_cum[b];
-            const int par = S.h_par[b], tkn = S.h_tok[b];
-            const int hn = --S.h_n;
-            S.h_cum[b] = S.h_cum[hn];
-            S.h_par[b] = S.h_par[hn];
-            S.h_tok[b] = S.h_tok[hn];
-            S.h_ord[b] = S.h_ord[hn];
-            const int i = S.rows++;
-            S.tr_par[i] = par;
-            S.tr_tok[i] = tkn;
-            S.tr_dep[i] = S.tr_dep[par] + 1;
-            S.tr_anc[i] = S.tr_anc[par] | (1u << i);
-            S.tr_cum[i] = cum;
-            if (tkn == eos0 || tkn == eos1 || S.rows == K + 1) continue;   // not expanded
-            int r = i, dpos = S.tr_dep[i], tk2 = S.ticks0;
-            while (r > 0) {
-              const int t = S.tr_tok[r];
-              S.ob[base + dpos - 1] = t;
-              tk2 += (t >= 0 && t < ILD_VOCAB) ? (d.tflg[t] & 7) : 0;
-              dpos--;
-              r = S.tr_par[r];
+          for (int pop = 0; pop < ILD_HEAP; ++pop) {
+            const int hn = S.h_n;
+            if (!(S.rows < K + 1 && hn > 0)) break;
+            uint64_t kk = 0;
+            for (int q = lane; q < hn; q += 64) {
+              const uint64_t kq = ((uint64_t)__float_as_uint(S.h_cum[q]) << 32) |
+                                  ((uint64_t)(0xffff - S.h_ord[q]) << 16) | (uint64_t)q;
+              kk = kq > kk ? kq : kk;
             }
-            S.depth = S.tr_dep[i];
-            S.erow = i;
-            S.ticks = tk2;
-            go = 1;
-            break;
+            kk = ild_max64(kk, 64);
+            if (lane == 0) {
+              const int b = (int)(kk & 0xffff);
+              const float cum = S.h_cum[b];
+              const int par = S.h_par[b], tkn = S.h_tok[b], tkf = S.h_tf[b];
+              const int hl = hn - 1;
+              S.h_cum[b] = S.h_cum[hl];
+              S.h_par[b] = S.h_par[hl];
+              S.h_tok[b] = S.h_tok[hl];
+              S.h_tf[b] = S.h_tf[hl];
+              S.h_ord[b] = S.h_ord[hl];
+              S.h_n = hl;
+              const int i = S.rows;
+              S.rows = i + 1;
+              S.tr_par[i] = par;
+              S.tr_tok[i] = tkn;
+              S.tr_tf[i] = tkf;
+              S.tr_dep[i] = S.tr_dep[par] + 1;
+              S.tr_anc[i] = S.tr_anc[par] | (1u << i);
+              S.tr_cum[i] = cum;
+              const int expand = !(tkn == eos0 || tkn == eos1 || i + 1 == K + 1);
+              if (expand) {
+                int r = i, dpos = S.tr_dep[i], tk2 = S.ticks0;
+                while (r > 0) {
+                  S.ob[base + dpos - 1] = S.tr_tok[r];
+                  tk2 += S.tr_tf[r];
+                  dpos--;
+                  r = S.tr_par[r];
+                }
+                S.depth = S.tr_dep[i];
+                S.erow = i;
+                S.ticks = tk2;
+              }
+              S.flag = expand;
+            }
+            ild_wave_sync();
+            if (S.flag) {
+              go = 1;
+              break;
+            }
           }
-          S.go = go;
+          if (lane == 0) S.go = go;
         }
-      } else if (tid == 0) {
-        if (nu == 0) {
-          S.go = 0;
-        } else {
-          const int bt = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-          const int nd = S.nd;
-          S.next_rows[nd + 1] = bt;
-          S.ob[Lo] = bt;
-          S.nd = nd + 1;
-          S.depth = nd + 1;
-          S.ticks = ticks + ((bt < ILD_VOCAB) ? (d.tflg[bt] & 7) : 0);
-          S.go = (nd + 1 < K && bt != eos0 && bt != eos1) ? 1 : 0;
+      } else {
+        if (tid < nu && S.ckey[tid] == best) S.best_tf = S.ctf[tid];
+        __syncthreads();
+        if (tid == 0) {
+          if (nu == 0) {
+            S.go = 0;
+          } else {
+            const int bt = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+            const int nd = S.nd;
+            S.next_rows[nd + 1] = bt;
+            S.ob[Lo] = bt;
+            S.nd = nd + 1;
+            S.depth = nd + 1;
+            S.ticks = ticks + S.best_tf;
+            S.go = (nd + 1 < K && bt != eos0 && bt != eos1) ? 1 : 0;
+          }
         }
       }
     }

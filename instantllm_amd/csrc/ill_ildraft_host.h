@@ -285,7 +285,9 @@ inline void prepare(Table& t, const int32_t* prompt, int n, const char* text, En
     const bool inp = pset.count(x) != 0;
     r.copyTok[nc] = x;
     r.copyInP[nc] = inp ? 1 : 0;
-    r.copyPt[nc] = inp ? t.prop(x) : 0.3f;
+    const float pt = inp ? t.prop(x) : 0.3f;
+    r.copyPt[nc] = pt;
+    r.copyF33[nc] = (float)std::log((double)(pt / (1.f - pt))) / 4.f;
     nc++;
   }
   r.ncopy = nc;

@@ -30,7 +30,7 @@ ENCODE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.POINTER(C.c_int32), C
 # The learned drafter's request context as the device reads it (IllDraftReq, ill_ildraft.h)
 DRAFT_REQ = np.dtype([("np", "<i4"), ("ncopy", "<i4"), ("nnb", "<i4"), ("nas", "<i4"),
                       ("P", "<i4", 256), ("pprop", "<f4", 256), ("copyTok", "<i4", 256), ("copyInP", "<i4", 256),
-                      ("copyPt", "<f4", 256), ("nbScore", "<f4", 16), ("nbOff", "<i4", 17), ("pad", "<i4", 3),
+                      ("copyPt", "<f4", 256), ("copyF33", "<f4", 256), ("nbScore", "<f4", 16), ("nbOff", "<i4", 17), ("pad", "<i4", 3),
                       ("nbTok", "<i4", 16 * 80), ("asTok", "<i4", 1024), ("asMax", "<f4", 1024), ("asCnt", "<i4", 1024)])
 
 

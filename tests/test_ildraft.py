@@ -203,6 +203,8 @@ def test_host_request_context_equals_oracle(golden, tmp_path):
             assert q["copyTok"][:n].tolist() == o.copy
             assert q["copyInP"][:n].tolist() == [int(x) for x in o.copy_inp]
             assert q["copyPt"][:n].tolist() == [float(x) for x in o.copy_pt]
+            f33 = [float(O._logf(pt / O.F32(O.F32(1) - pt)) / O.F32(4)) for pt in o.copy_pt]
+            assert q["copyF33"][:n].tolist() == f33
             assert q["asTok"][:q["nas"]].tolist() == o.as_tok
             assert q["asMax"][:q["nas"]].tolist() == [float(x) for x in o.as_max]
             assert q["asCnt"][:q["nas"]].tolist() == o.as_cnt

@@ -197,6 +197,68 @@ def config4(steps: int = 64, single: bool = False) -> dict:
     return out
 
 
+def speculative(path: str, n_new: int = 96) -> dict:
+    """Speculative generation on the config-2 model (not the headline workload): the learned
+    drafter with a table built from the model's own greedy outputs of 8 requests
+    (instantllm_amd.ildraft; random scorer weights with the n-gram / self-repetition /
+    neighbour features emphasized). `seen`: requests whose outputs the table holds (drafts
+    mostly right: an upper end); `unseen`: new requests (drafts mostly wrong: the cost of
+    speculating when it does not pay). Tokens equal plain greedy decoding in every run
+    (checked); tok/s from the host clock over each whole generate call."""
+    import tempfile
+    from instantllm_amd import ildraft as DW, illfile as F
+    from instantllm_amd.engine import Engine
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=n_new + 32)
+    rng = np.random.default_rng(11)
+    words = ["w%d" % i for i in range(300)]
+    def req():
+        return [int(t) for t in rng.integers(100, F.VOCAB, 24)], " ".join(rng.choice(words, 6))
+    seen = [req() for _ in range(8)]
+    unseen = [req() for _ in range(3)]
+    recs = [{"prompt": t, "pids": p, "y": e.generate(p, max_new=n_new, chunk=8)} for p, t in seen]
+    out = {"n_new": n_new,
+           "note": "learned drafter, table from the model's own greedy outputs of 8 requests; seen = requests "
+                   "the table holds (drafts mostly right), unseen = new requests; tokens checked equal to greedy; "
+                   "tok/s from the host clock over whole generate calls"}
+    with tempfile.TemporaryDirectory() as td:
+        tp = os.path.join(td, "t.bin")
+        DW.save(tp, recs, DW.DraftConfig(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
+        e.load_ildraft(tp)
+
+    def timed(fn):
+        fn()   # warm (graph capture)
+        t0 = time.perf_counter()
+        r = fn()
+        return r, time.perf_counter() - t0
+
+    for name, group in (("seen", seen[:3]), ("unseen", unseen)):
+        res = {}
+        for label, tree, rows in (("greedy", None, 1), ("commit_drafter_chain4", 0, 4), ("learned_chain8", 0, 8),
+                                  ("learned_tree16", 15, 16)):
+            toks_n, secs, passes, acc = 0, 0.0, 0, 0
+            for p, t in group:
+                g = e.generate(p, max_new=n_new, chunk=8)
+                if label == "greedy":
+                    (_, dt) = timed(lambda: e.generate(p, max_new=n_new, chunk=8))
+                    toks_n += len(g); secs += dt
+                    continue
+                def run():
+                    if label.startswith("learned"):
+                        e.set_learned(True, 8, tree)
+                        e.set_draft_context(p, t, None)
+                    return e.generate_spec(p, n_new, rows=rows, chunk=4)
+                (toks, np_, na), dt = timed(run)
+                if toks != g:
+                    raise RuntimeError(f"speculative tokens differ from greedy ({label}, {name})")
+                toks_n += len(toks); secs += dt; passes += np_; acc += na
+            res[label] = {"tok_s": round(toks_n / secs, 1)}
+            if label != "greedy":
+                res[label]["accepted_per_pass"] = round(acc / max(passes, 1), 2)
+        out[name] = res
+    e.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,6 +269,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV microbench")
     ap.add_argument("--no-config4", action="store_true", help="skip the q8 / f16 prefill and decode runs")
+    ap.add_argument("--no-spec", action="store_true", help="skip the speculative-decoding runs")
     ap.add_argument("--dispatch", choices=("graph", "single"), default="graph",
                     help="graph: the timed steps are one captured hipGraph (default); single: each "
                          "step is its own launch, timed with HIP events around its kernel, and prompts "
@@ -294,6 +357,14 @@ def main() -> int:
         e.set_state(pos=st["pos"], n=16, maxsteps=64, eos=no_eos)
         e.verify_pass(16, tree=tree)
         verify_us.append(e.last_pass_ms() * 1e3)
+    # 4-row chain pass (the 4-row instantiation; the reference's default speculative pass
+    # has 3 rows) at the same prefix: the last token and three drafts
+    chain = [int(tree[33])] + [int(t) for t in vr.integers(0, F.VOCAB, size=3)]
+    verify4_us = []
+    for _ in range(5):
+        e.set_state(pos=st["pos"], n=4, maxsteps=64, eos=no_eos)
+        e.verify_pass(4, toks=chain)
+        verify4_us.append(e.last_pass_ms() * 1e3)
     e.set_state(pos=st["pos"], n=1, maxsteps=64, eos=no_eos)
     one_us = []
     for _ in range(5):
@@ -313,6 +384,7 @@ def main() -> int:
         "us_per_token": round(us_tok, 2),
         "wall_ms_per_step": round(wall_ms / K, 5),
         "verify16_us": round(float(np.median(verify_us)), 2),
+        "verify4_us": round(float(np.median(verify4_us)), 2),
         "decode1_single_launch_us": round(float(np.median(one_us)), 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -337,6 +409,8 @@ def main() -> int:
         line["gemv_config1"] = gemv_config1()
     if not args.no_config4:
         line["config4"] = config4(single=single)
+    if not args.no_spec and not single:
+        line["speculative"] = speculative(path)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_steps)
     print(json.dumps(line), flush=True)

@@ -26,7 +26,9 @@ Nothing in the product imports this module; tests compare the engine's drafting 
 
 Where the engine differs from the Python drafter, the engine is followed: the output window
 is the last 256 committed tokens plus the drafts, neighbour sequences are cut to 80 tokens,
-at most 32 prompt-lookup occurrences and 6 continuations per n-gram order are candidates,
+the context keeps the first 256 prompt ids and copy candidates and 1024 associations
+(`Req(python=True)` drops these caps), at most 32 prompt-lookup occurrences and 6
+continuations per n-gram order are candidates,
 the edited-neighbour and association-candidate options are not used, neighbour scores enter
 the features as float32. Candidates outside the model's vocabulary are dropped (a table
 built for the full 151936-token vocabulary never has one).
@@ -163,9 +165,13 @@ class Table:
 class Req:
     """The per-request context (ILDraft.swift:110-208)."""
 
-    def __init__(self, table: Table, pids, text: str, encode=None):
+    def __init__(self, table: Table, pids, text: str, encode=None, python: bool = False):
+        """python: the Python drafter's context, without the engine's caps (DraftReq,
+        ILDraft.swift:20-35): all prompt ids (not the first 256), each neighbour's whole
+        TAIL + output (not its first 80 tokens), every copy candidate and association (not
+        the first 256 / 1024)."""
         t = table
-        self.P = [int(x) for x in pids[:MAXP]]
+        self.P = [int(x) for x in (pids if python else pids[:MAXP])]
         pset = set(self.P)
         words = prompt_words(text)
         score = defaultdict(float)
@@ -183,14 +189,17 @@ class Req:
         ranked = sorted(((s / (qn * float(t.dnrm[d])), d) for d, s in score.items()), key=lambda x: (-x[0], x[1]))
         self.nb = []                                  # (score f32, doc, sequence <= 80)
         for s, d in ranked[:min(t.KNB, MAXNB)]:
-            self.nb.append((F32(s), d, (list(TAIL) + t.seqs[d])[:NBSEQ]))
+            seq = list(TAIL) + t.seqs[d]
+            self.nb.append((F32(s), d, seq if python else seq[:NBSEQ]))
         sv = set()
         if encode is not None:
             for w in spacevar_words(text):
                 ids = encode(" " + w)
                 if ids and ids[0] not in pset:
                     sv.add(int(ids[0]))
-        self.copy = sorted(pset | sv)[:MAXCOPY]
+        self.copy = sorted(pset | sv)
+        if not python:
+            self.copy = self.copy[:MAXCOPY]
         self.copy_inp = [c in pset for c in self.copy]
         amap = {}
         if t.flags & 1:
@@ -198,7 +207,7 @@ class Req:
                 for tok, ll in t.assoc.get(fnv1a64(w), ()):
                     e = amap.get(tok)
                     amap[tok] = (max(e[0], ll), e[1] + 1) if e else (ll, 1)
-        self.as_tok = sorted(amap)[:MAXAS]
+        self.as_tok = sorted(amap) if python else sorted(amap)[:MAXAS]
         self.as_max = [amap[x][0] for x in self.as_tok]
         self.as_cnt = [amap[x][1] for x in self.as_tok]
         # request-constant lookups of the copy features

@@ -10,9 +10,13 @@ outputs and the real tokenizer, which are not in the tree, so the vectors are ma
 * the reference's `Tables.load` reads that file and its `Drafter` (with the corpus's
   stand-in tokenizer for the space variants) drafts for held-in and held-out requests:
   the neighbour ranking, copy candidates and associations of `begin`, and at every output
-  position the top-3 probabilities of `probs` and the 7-draft `chain`, at four positions
+  position the top-3 probabilities of `probs` and the 7-draft `chain`, at two positions
   per request the candidates and feature rows of `features`; 15-node `tree`s at a few
-  positions -> `ildraft_small.json`.
+  positions -> `ildraft_small.json`;
+* the same recordings on the reference's own shipped table (`tools/draft/ildraft-q4.bin`:
+  its real n-gram statistics, TF-IDF index, associations, token flags and trained scorer)
+  for requests taken from its drafting corpus (`corpus-q4.jsonl`) -> `ildraft_real.json`
+  (the table itself stays in the reference; its SHA-256 is recorded).
 
 Only inputs and outputs are stored, never reference code; the reference is not needed at
 test time. Usage: python tests/golden/make_ildraft_fixtures.py [/root/reference]
@@ -52,6 +56,61 @@ class _Tok:
         raise AssertionError("token flags come from the table")
 
 
+REAL_VECTORS = HERE / "ildraft_real.json"
+REAL_TABLE = "tools/draft/ildraft-q4.bin"
+REAL_CORPUS = "tools/draft/corpus-q4.jsonl"
+
+
+def real_requests(ref_root, n=12):
+    """Requests drawn from the reference's drafting corpus (real greedy outputs of its q4
+    model: the table's training outputs): prompt text and output ids as recorded; the prompt
+    ids are a stand-in (the tokenizer is not in the tree): the output's first distinct ids
+    and the stand-in ids of the prompt's words, so that prompt-lookup and copy features fire."""
+    import json as J
+    from ildraft_corpus import tok_id
+    lines = Path(ref_root, REAL_CORPUS).read_text().splitlines()
+    out = []
+    for k in range(n):
+        r = J.loads(lines[(k * 1877) % len(lines)])
+        y = list(r["ids"]) + ([r["stop"]] if r.get("stop", -1) in (151645, 151643) else [])
+        seen = []
+        for t in y:
+            if t not in seen and len(seen) < 6:
+                seen.append(t)
+        pids = [tok_id(w) for w in r["prompt"].split()][:20] + seen
+        out.append({"prompt": r["prompt"], "pids": pids, "y": y[:96]})
+    return out
+
+
+def real_main(ref_root, R):
+    """Vectors of the reference drafter on the reference's own shipped table."""
+    tab = R.Tables.load(str(Path(ref_root, REAL_TABLE)))
+    d = R.Drafter(tab, _Tok())
+    out = []
+    for r in real_requests(ref_root):
+        d.begin(r["pids"], r["prompt"])
+        y = r["y"]
+        pos = []
+        for i in range(1, len(y)):
+            pr = d.probs(y[:i])
+            e = {"top": [[int(t), float(p)] for t, p in pr[:3]], "chain": [int(t) for t in d.chain(y[:i], 7)]}
+            if i in (1, len(y) // 2):
+                toks, rows = d.features(y[:i])
+                e["feat"] = {"toks": [int(t) for t in toks], "rows": [[round(float(x), 9) for x in row] for row in rows]}
+            pos.append(e)
+        par, toks = d.tree(y[:2], 15)
+        out.append({"prompt": r["prompt"], "pids": r["pids"], "y": y,
+                    "nb_seqs": [[int(t) for t in seq] for _, seq, _ in d.nb],
+                    "nb_scores": [float(s) for s, _, _ in d.nb],
+                    "copy": [int(x) for x in d.copy_cands],
+                    "assoc": {str(k): [float(v[0]), int(v[1])] for k, v in sorted(d.as_map.items())},
+                    "pos": pos, "trees": [{"at": 2, "parents": par, "tokens": [int(t) for t in toks]}]})
+    import hashlib as HL
+    sha = HL.sha256(Path(ref_root, REAL_TABLE).read_bytes()).hexdigest()
+    REAL_VECTORS.write_text(json.dumps({"table_sha256": sha, "requests": out}))
+    print(f"real table: {len(out)} requests / {sum(len(x['pos']) for x in out)} positions -> {REAL_VECTORS.name}")
+
+
 def main(ref_root="/root/reference"):
     blob, reqs = make_table()
     sys.path.insert(0, str(Path(ref_root) / "tools" / "draft"))
@@ -68,7 +127,7 @@ def main(ref_root="/root/reference"):
         for i in range(1, len(y)):
             pr = d.probs(y[:i])
             e = {"top": [[int(t), float(p)] for t, p in pr[:3]], "chain": [int(t) for t in d.chain(y[:i], 7)]}
-            if i in (1, 2, len(y) // 2, len(y) - 1):
+            if i in (1, len(y) // 2):
                 toks, rows = d.features(y[:i])
                 e["feat"] = {"toks": [int(t) for t in toks], "rows": [[round(float(x), 9) for x in row] for row in rows]}
             pos.append(e)
@@ -85,6 +144,7 @@ def main(ref_root="/root/reference"):
     VECTORS.write_text(json.dumps({"table_sha256": hashlib.sha256(blob).hexdigest(), "requests": out}))
     n = sum(len(x["pos"]) for x in out)
     print(f"table {len(blob)} B; {len(out)} requests / {n} positions -> {VECTORS.name}")
+    real_main(ref_root, R)
 
 
 if __name__ == "__main__":

@@ -185,3 +185,54 @@ def test_learned_fullsize_q4():
         assert (passes, acc) == (p_ref, a_ref)
     finally:
         e.close()
+
+
+@pytest.fixture(scope="module")
+def corpus_engine(tmp_path_factory):
+    """An engine (the 3-layer model) with the fixture table of the synthetic request corpus."""
+    from instantllm_amd.engine import Engine
+    from make_ildraft_fixtures import make_table
+    d = tmp_path_factory.mktemp("corpus")
+    path = str(d / "q4.ill")
+    synth.build_model(path, F.FMT_Q4, seed=2, shape=synth.ModelShape(layers=3, vocab=VOCAB))
+    blob, reqs = make_table()
+    (d / "corpus.bin").write_bytes(blob)
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=256)
+    e.load_ildraft(str(d / "corpus.bin"))
+    yield e, O.Table(blob), reqs
+    e.close()
+
+
+@pytest.mark.parametrize("tree", [0, 15])
+def test_pending_passes_match_oracle_corpus_table(corpus_engine, tree):
+    """The fixture table of the synthetic request corpus (300 requests: neighbours, copy
+    candidates, associations and space variants all in play; the reference drafter's golden
+    vectors pin the oracle on it): each pass's drafts equal the oracle's, request by request."""
+    e, tab, reqs = corpus_engine
+    rows = tree + 1 if tree else 8
+    checked = 0
+    for r in reqs[6:10]:
+        pids = [t for t in r["pids"] if t < VOCAB]
+        e.set_learned(True, 8, tree)
+        e.set_draft_context(pids, r["prompt"], mock_encode)
+        dr = O.Drafter(tab, O.Req(tab, pids, r["prompt"], mock_encode), vocab=VOCAB)
+        e.reset_out_tokens()
+        e.set_prompt(pids)
+        e.set_state(pos=0, n=len(pids), maxsteps=24, tspec=rows, learned=1)
+        e.prefill(pids)
+        for _ in range(6):
+            st = e.get_state()
+            if st["done"]:
+                break
+            out = [int(t) for t in e.out_tokens()[:st["step"]]]
+            mode, nrows, toks, trbuf = e.pending_pass()
+            if tree:
+                par, tk = dr.tree(out, tree)
+                rt, dep, _ = O.tree_rows(par, tk, out[-1])
+                assert mode == 2 and toks == rt and list(trbuf[1:1 + nrows]) == dep
+            else:
+                assert mode == 1 and toks == [out[-1]] + dr.chain(out, rows - 1)
+            checked += 1
+            e.spec_pass()
+    log(f"corpus table, {'tree' if tree else 'chain'}: {checked} passes checked")
+    assert checked >= 12

@@ -218,7 +218,7 @@ def speculative(path: str, n_new: int = 96) -> dict:
     recs = [{"prompt": t, "pids": p, "y": e.generate(p, max_new=n_new, chunk=8)} for p, t in seen]
     out = {"n_new": n_new,
            "note": "learned drafter, table from the model's own greedy outputs of 8 requests; seen = requests "
-                   "the table holds (drafts mostly right), unseen = new requests; tokens checked equal to greedy; "
+                   "the table holds (drafts mostly right), unseen = new requests; tokens checked equal to greedy (both from a cold prefix cache); "
                    "tok/s from the host clock over whole generate calls"}
     with tempfile.TemporaryDirectory() as td:
         tp = os.path.join(td, "t.bin")
@@ -234,19 +234,24 @@ def speculative(path: str, n_new: int = 96) -> dict:
     for name, group in (("seen", seen[:3]), ("unseen", unseen)):
         res = {}
         for label, tree, rows in (("greedy", None, 1), ("commit_drafter_chain4", 0, 4), ("learned_chain8", 0, 8),
-                                  ("learned_tree16", 15, 16)):
+                                  ("learned_tree16", 15, 16), ("learned_tree16_adaptive", 15, 16),
+                                  ("commit_drafter_16_adaptive", 0, 16)):
             toks_n, secs, passes, acc = 0, 0.0, 0, 0
             for p, t in group:
-                g = e.generate(p, max_new=n_new, chunk=8)
+                def greedy():
+                    e.truncate_cache(0)   # every run from a cold prefix cache
+                    return e.generate(p, max_new=n_new, chunk=8)
+                g = greedy()
                 if label == "greedy":
-                    (_, dt) = timed(lambda: e.generate(p, max_new=n_new, chunk=8))
+                    (_, dt) = timed(greedy)
                     toks_n += len(g); secs += dt
                     continue
                 def run():
+                    e.truncate_cache(0)
                     if label.startswith("learned"):
                         e.set_learned(True, 8, tree)
                         e.set_draft_context(p, t, None)
-                    return e.generate_spec(p, n_new, rows=rows, chunk=4)
+                    return e.generate_spec(p, n_new, rows=rows, chunk=4, adaptive=label.endswith("adaptive"))
                 (toks, np_, na), dt = timed(run)
                 if toks != g:
                     raise RuntimeError(f"speculative tokens differ from greedy ({label}, {name})")

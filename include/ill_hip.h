@@ -129,10 +129,13 @@ int ill_capture_spec(ill_engine* e, int npasses);
 
 /* Engine.generate with speculation on (Engine.swift:922-1038): prefill, then verify passes
  * of up to `rows` (2..16) rows, in captured graphs of `chunk` passes for q4 models (one
- * launch per pass otherwise), while polling out_tokens. adaptive != 0 narrows the passes to
- * 8 rows while fewer than 1.5 drafts per pass are accepted (Engine.nextPassShape,
- * :888-898). out / n_out as for ill_generate; stats (optional, [2]) receives the passes
- * and accepted drafts of the request. */
+ * launch per pass otherwise), while polling out_tokens. adaptive != 0 chooses each launch's
+ * shape from the accepted drafts per pass (Engine.nextPassShape, :888-898, with thresholds
+ * from this engine's pass costs, which grow with the kernel's row count): the configured
+ * shape while at least 3.4 are accepted, 4-row chains while at least 1.4 are (back to the
+ * configured shape at 2.5), else one-row passes with a 4-row probe every 16 passes.
+ * out / n_out as for ill_generate; stats (optional, [2]) receives the passes and accepted
+ * drafts of the request. */
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
                       int32_t* out, int* n_out, int32_t* stats);
 
@@ -190,6 +193,11 @@ int ill_pending_pass(ill_engine* e, int32_t info[4], int32_t toks[16], int32_t t
  * file and context (else ILL_E_FILE), makes its tokens the cached prefix and returns them
  * in toks (max_toks entries; NULL to skip) and their count in n_out. */
 int ill_prefix_info(ill_engine* e, int* cached, int* last_prefill);
+/* Engine.truncateCache (Engine.swift:850-853): forget the cached K/V beyond the first n
+ * tokens (0 clears the cache). A reused prefix changes where the prompt's last tokens are
+ * computed (its K/V come from the earlier request's passes), so a near tie can resolve
+ * differently than from a cold cache; callers comparing runs clear it first. */
+int ill_truncate_cache(ill_engine* e, int n);
 int ill_save_prefix(ill_engine* e, const char* path, const int32_t* toks, int n);
 int ill_load_prefix(ill_engine* e, const char* path, int32_t* toks, int max_toks, int* n_out);
 

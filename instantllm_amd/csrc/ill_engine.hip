@@ -137,6 +137,13 @@ struct ill_engine {
   bool graph_spec = false;        // the captured graph holds spec passes (their control comes from the device)
   int graph_T = 0;                // pass instantiation of the captured spec graph
   bool graph_learned = false;     // its drafting kernel is the learned drafter's
+  // generate_spec's own graphs of chained passes, one per pass instantiation (1, 4, 16 rows)
+  struct SpecGraph {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+    int steps = 0;
+    bool learned = false;
+  } sg[3];
   // Engine.cachedTokens (Engine.swift:929-933, :1029-1031): tokens whose K/V are valid at
   // positions 0.. after the last generate call; any pass launched outside generate clears it
   std::vector<int32_t> cached;
@@ -236,6 +243,7 @@ int check_err(ill_engine* e) {
     hipMemcpy(&e->ctl->bank_rows[0], zero, 8, hipMemcpyHostToDevice);
     hipMemset(e->acc, 0, e->acc_bytes);
     hipDeviceSynchronize();
+    if (err == ILL_ERR_SHAPE) return fail(ILL_E_ARG, "a pass had more rows than its kernel instantiation; it was abandoned");
     return fail(ILL_E_TIMEOUT, "device wait timed out (site %d); the pass was abandoned", err);
   }
   return 0;
@@ -264,6 +272,11 @@ void drop_graph(ill_engine* e) {
   e->graph = nullptr;
   e->graph_steps = 0;
   e->graph_T = 0;
+  for (auto& g : e->sg) {
+    if (g.x) hipGraphExecDestroy(g.x);
+    if (g.g) hipGraphDestroy(g.g);
+    g = ill_engine::SpecGraph{};
+  }
 }
 
 int read_state(ill_engine* e, IllState* s) {
@@ -998,6 +1011,34 @@ int ill_capture_spec(ill_engine* e, int npasses) {
   return ILL_OK;
 }
 
+namespace {
+// generate_spec's graph of `npasses` chained passes on the T-row instantiation (cached per
+// T, drafting kernel and pass count), then launched: the passes take their rows from the
+// device, so every pending pass must hold at most T rows.
+int launch_spec_graph(ill_engine* e, int T, int npasses) {
+  ill_engine::SpecGraph& g = e->sg[T == 1 ? 0 : (T == 4 ? 1 : 2)];
+  if (!g.x || g.steps != npasses || g.learned != e->learned_active) {
+    if (g.x) HCK(hipGraphExecDestroy(g.x));
+    if (g.g) HCK(hipGraphDestroy(g.g));
+    g = ill_engine::SpecGraph{};
+    HCK(hipStreamSynchronize(e->stream));
+    HCK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < npasses; i++) {
+      enqueue_pass(e, T);
+      enqueue_draft(e);
+    }
+    HCK(hipStreamEndCapture(e->stream, &g.g));
+    HCK(hipGraphInstantiate(&g.x, g.g, nullptr, nullptr, 0));
+    g.steps = npasses;
+    g.learned = e->learned_active;
+  }
+  if (int rc = set_wlog(e, 0)) return rc;
+  if (int rc = count_passes(e, npasses)) return rc;
+  HCK(hipGraphLaunch(g.x, e->stream));
+  return 0;
+}
+}  // namespace
+
 int ill_capture_steps(ill_engine* e, int nsteps) {
   if (!e || nsteps < 1) return fail(ILL_E_ARG, "bad step count");
   drop_graph(e);
@@ -1131,6 +1172,12 @@ bool prefix_key(const ill_engine* e, uint64_t key[5]) {
 }  // namespace
 
 extern "C" {
+
+int ill_truncate_cache(ill_engine* e, int n) {
+  if (!e || n < 0) return fail(ILL_E_ARG, "bad truncate arguments");
+  if ((int)e->cached.size() > n) e->cached.resize((size_t)n);
+  return ILL_OK;
+}
 
 int ill_prefix_info(ill_engine* e, int* cached, int* last_prefill) {
   if (!e) return fail(ILL_E_ARG, "null engine");
@@ -1282,25 +1329,35 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
   if ((rc = ill_prefill(e, toks + common, ntok - common, 0))) return rc;
   const bool graphs = e->fmt == 2;
-  if (graphs && (!e->graph_spec || e->graph_steps != chunk || e->graph_T != pass_T(rows) || e->graph_learned != learned) &&
-      (rc = ill_capture_spec(e, chunk)))
-    return rc;
-  // Engine.nextPassShape (Engine.swift:888-898): the configured shape while drafts are
-  // accepted (at least adaptHi = 1.5 per pass over the last few committed passes), an
-  // 8-row chain otherwise; the shape takes effect from the next pass drafted
+  // Pass shapes (Engine.nextPassShape, Engine.swift:888-898, with thresholds from this
+  // engine's pass costs, which grow with the kernel's row count: about 345 us for 1 row,
+  // 830 us for 4 and 1.24 ms for 16, plus the drafting): a pass of 1 + r tokens beats plain
+  // decoding when r >= 1.4 accepted drafts (4 rows) or r >= 3.4 (16 rows with drafting).
+  // Level 0 is the configured shape, kept while r >= 3.4 over the last few passes at that
+  // level; level 1 a 4-row chain (3 drafts), back to level 0 at r >= 2.5, kept at r >= 1.4;
+  // level 2 one-row passes without drafts (a decode step's cost), left for a 4-row probe
+  // after 16 passes. Passes at a level only count toward its own rate.
+  int level = 0, level_p0 = 0;
   std::vector<std::pair<int, int>> hist;
-  int cur_rows = rows;
-  auto shape = [&]() -> std::pair<int, int> {
-    const std::pair<int, int> base(rows, treeb);
-    if (!adaptive) return base;
+  auto shape_of = [&](int lv) -> std::pair<int, int> {
+    if (lv == 0) return std::pair<int, int>(rows, treeb);
+    if (lv == 1) return std::pair<int, int>(std::min(rows, 4), 0);
+    return std::pair<int, int>(1, 0);
+  };
+  auto next_level = [&]() -> int {
+    if (!adaptive) return 0;
     const int p = ((volatile int32_t*)e->spec_host)[0], a = ((volatile int32_t*)e->spec_host)[1];
     if (hist.empty() || hist.back().first != p) hist.emplace_back(p, a);
-    if (hist.size() < 3) return base;
+    if (level == 2) return p - level_p0 >= 16 ? 1 : 2;
+    if (hist.size() < 3) return level;
     const auto& first = hist[hist.size() >= 4 ? hist.size() - 4 : 0];
-    if (p - first.first < 2) return base;
+    if (p - first.first < 2) return level;
     const double rate = (double)(a - first.second) / (double)(p - first.first);
-    return rate >= 1.5 ? base : std::pair<int, int>(std::min(rows, 8), 0);
+    if (level == 0) return rate >= 3.4 ? 0 : (rows > 4 ? 1 : (rate >= 1.4 ? 0 : 2));
+    return rate >= 2.5 ? 0 : (rate >= 1.4 ? 1 : 2);
   };
+  int cur_rows = rows;
+  int drafted_rows = rows;   // the most rows a pending pass can hold (the prompt's commit drafted it)
   volatile const int32_t* ot = e->out_host;
   volatile const int32_t* sp = e->spec_host;
   int got = 0, encoded = 0;   // tokens read, passes enqueued after the prefill
@@ -1309,7 +1366,13 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     // keep at most one chunk of passes ahead of the committed ones (Engine.swift:991-1008);
     // every pass commits at least one token, so max_new passes always suffice
     if (encoded < max_new && (!graphs || encoded - (sp[0] - 1) <= chunk)) {
-      const std::pair<int, int> want = shape();
+      const int lv = next_level();
+      if (lv != level) {
+        level = lv;
+        level_p0 = sp[0];
+        hist.clear();
+      }
+      const std::pair<int, int> want = shape_of(level);
       if (want.first != cur_rows || want.second != cur_tree) {   // ordered after the passes before it
         cur_rows = want.first;
         cur_tree = want.second;
@@ -1317,7 +1380,11 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
         HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
       }
       if (graphs) {
-        if ((rc = ill_launch_graph(e))) return rc;
+        // the first pass of this launch holds what the previous launch drafted (under the
+        // rows then in effect); its later passes hold cur_rows
+        const int T = pass_T(std::max(drafted_rows, cur_rows));
+        drafted_rows = cur_rows;
+        if ((rc = launch_spec_graph(e, T, chunk))) return rc;
         encoded += chunk;
         continue;
       }

@@ -69,6 +69,8 @@ __device__ __forceinline__ void trace_mark(const IllPassArgs& a, int slot) {
   if (a.trace && threadIdx.x == 0) a.trace[blockIdx.x * ILL_TRACE_SLOTS + slot] = wall_clock64();
 }
 
+#define ILL_ERR_SHAPE 990   // error code: a pass's rows do not fit the kernel instantiation
+
 struct PassHdr {
   uint32_t epoch;
   int mode, nrows, pos, lmh0, lmhn, wlog, commit, done, bank, zrows;
@@ -1891,6 +1893,11 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   if (threadIdx.x == 0) load_hdr(a, H);
   __syncthreads();
   if (H.done) return;
+  // a pass must fit this instantiation: every workgroup reads the same header and leaves
+  if (H.nrows < 1 || H.nrows > T || H.lmhn < 0 || H.lmh0 < 0 || H.lmh0 + H.lmhn > T) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) set_err(a.ctl, ILL_ERR_SHAPE);
+    return;
+  }
   const int wg = blockIdx.x;
   const int NL = a.W.layers;
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;

@@ -96,6 +96,7 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_save_prefix": (C.c_int, [P, C.c_char_p, ip, C.c_int]),
         "ill_load_prefix": (C.c_int, [P, C.c_char_p, ip, C.c_int, C.POINTER(C.c_int)]),
         "ill_set_prompt": (C.c_int, [P, ip, C.c_int]),
+        "ill_truncate_cache": (C.c_int, [P, C.c_int]),
         "ill_spec_pass": (C.c_int, [P, C.c_int]),
         "ill_capture_spec": (C.c_int, [P, C.c_int]),
         "ill_generate_spec": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), ip]),
@@ -265,6 +266,10 @@ class Engine:
             return
         t = np.ascontiguousarray(table)
         self._check(self.lib.ill_load_ngram(self.h, t.ctypes.data, t.nbytes))
+
+    def truncate_cache(self, n: int = 0):
+        """Engine.truncateCache: forget the cached prefix beyond its first n tokens."""
+        self._check(self.lib.ill_truncate_cache(self.h, n))
 
     def set_prompt(self, toks):
         a = _i32(toks)

@@ -116,10 +116,12 @@ def test_learned_generate_equals_greedy_and_oracle_counts(setup, tree):
     e, tab, reqs = setup
     for k in (0, 5):
         pids, text = reqs[k]
+        e.truncate_cache(0)   # compare cold runs
         gx = e.generate(pids, max_new=48 + 16, chunk=8)
         g = gx[:48]
         e.set_learned(True, 8, tree)
         e.set_draft_context(pids, text, mock_encode)
+        e.truncate_cache(0)   # compare cold runs
         toks, passes, acc = e.generate_spec(pids, 48, chunk=4)
         assert toks == g
         req = O.Req(tab, pids, text, mock_encode)
@@ -135,9 +137,11 @@ def test_learned_unseen_request_and_adaptive(setup):
     output is still exactly greedy."""
     e, tab, _ = setup
     pids, text = _requests(99, 1, VOCAB)[0]
+    e.truncate_cache(0)   # compare cold runs
     g = e.generate(pids, max_new=40, chunk=8)
     e.set_learned(True, 8, 15)
     e.set_draft_context(pids, text, mock_encode)
+    e.truncate_cache(0)   # compare cold runs
     toks, passes, acc = e.generate_spec(pids, 40, chunk=2, adaptive=True)
     log(f"unseen adaptive: passes {passes} accepted {acc}")
     assert toks == g
@@ -147,11 +151,14 @@ def test_context_is_consumed_and_ngram_path_returns(setup):
     """Without a fresh context, generate_spec drafts with the commit's own drafter again."""
     e, tab, reqs = setup
     pids, text = reqs[1]
+    e.truncate_cache(0)   # compare cold runs
     g = e.generate(pids, max_new=24, chunk=8)
     e.set_learned(True, 8, 0)
     e.set_draft_context(pids, text, mock_encode)
+    e.truncate_cache(0)   # compare cold runs
     t1, _, _ = e.generate_spec(pids, 24, rows=16, chunk=4)
     assert e.get_state()["learned"] == 1
+    e.truncate_cache(0)   # compare cold runs
     t2, _, _ = e.generate_spec(pids, 24, rows=16, chunk=4)
     assert e.get_state()["learned"] == 0
     assert t1 == g and t2 == g
@@ -174,9 +181,11 @@ def test_learned_fullsize_q4():
             e.load_ildraft(tp)
             tab = O.Table.load(tp)
         pids, text = reqs[2]
+        e.truncate_cache(0)   # compare cold runs
         gx = e.generate(pids, max_new=40 + 16, chunk=8)
         e.set_learned(True, 8, 15)
         e.set_draft_context(pids, text, mock_encode)
+        e.truncate_cache(0)   # compare cold runs
         toks, passes, acc = e.generate_spec(pids, 40, chunk=4)
         req = O.Req(tab, pids, text, mock_encode)
         _, p_ref, a_ref = O.simulate(pids, gx, 40, _oracle_plan(tab, req, F.VOCAB, 16, 15))

@@ -112,6 +112,33 @@ __device__ __forceinline__ bool wave_wait(F&& ready, IllCtl* ctl, int code) {
   }
 }
 
+// Two-stage wave-wide bounded wait: polls `light()` (a word or two per row, loaded by every
+// lane from one address, so one memory request each) until it holds, then `ready()` (the
+// whole input) as wave_wait does. The input completes as a whole, so the light words turn
+// ready with it, and a wave that waits long costs a request per row per poll instead of
+// its whole input's. `ready()` alone decides success.
+template <class L, class F>
+__device__ __forceinline__ bool wave_wait2(L&& light, F&& ready, IllCtl* ctl, int code) {
+  const uint64_t t0 = clk();
+  bool lit = false;
+  for (int it = 1;; it++) {
+    if (!lit) lit = __all(light());
+    if (lit && __all(ready())) return true;
+    if ((it & 31) == 0) {
+      if (aload32(&ctl->err) != 0) return false;
+      if (clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); return false; }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// A wave-uniform value held in a vector register, so that loads from addresses built on it
+// stay vector memory loads.
+__device__ __forceinline__ int vgpr_uniform(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ bool wg_failed(IllCtl* ctl) {
   int bad = 0;
   if (threadIdx.x == 0) bad = aload32(&ctl->err) != 0;

@@ -305,7 +305,15 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   const int c0 = 64 * w + lane, c1 = 64 * (two ? G1 : w) + lane;
   const float g0 = gld(gamma + c0), g1 = gld(gamma + c1);
   float v0[T], v1[T];
-  const bool alive = wave_wait([&]() {
+  const int cl = vgpr_uniform(64 * w);   // light poll: the wave's first column of each row
+  const bool alive = wave_wait2([&]() {
+    bool ok = true;
+    float x;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+      if (t < nrows) ok &= src.load1(t, cl, x);
+    return ok;
+  }, [&]() {
     bool ok = true;
 #pragma unroll
     for (int t = 0; t < T; t++) {
@@ -426,7 +434,11 @@ __device__ __forceinline__ bool pub_read(const uint64_t* src, uint32_t tag, int 
   const bool live = t < nrows;
   const uint64_t* rp = src + (size_t)t * ILL_PUB_W + l32;
   uint32_t v[15];
-  const bool alive = wave_wait([&]() {
+  // light poll: the row's last word (its scale), the same address for the half-wave
+  const uint64_t* lp = src + (size_t)t * ILL_PUB_W + (ILL_PUB_PAY - 1);
+  const bool alive = wave_wait2([&]() {
+    return !live || (uint32_t)(aload64(lp) >> 32) == tag;
+  }, [&]() {
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < 15; j++) {

@@ -11,8 +11,9 @@
 // GPU shape: one workgroup of 1024 threads (16 waves). Per drafted token the waves split
 // the sources (wave 0 the six n-gram orders as a cooperative 11-ary search over the sorted
 // keys, 1 self-repetition, 2 prompt lookup, 3 the copy context, 4-11 two neighbours each),
-// then one thread per distinct candidate writes its 53 features to LDS, and the scorer
-// runs with one lane per hidden unit (16 or 32 lanes per candidate). The candidate
+// then two threads per distinct candidate (in waves 0-7 and 8-15) write its 53 features to
+// LDS, and the scorer runs with one lane per hidden unit (16 or 32 lanes per candidate),
+// the hidden unit's and the linear term's sums advancing together. The candidate
 // set is deduplicated through an LDS hash set, so its order in memory is arbitrary: every
 // decision depends on the set only (argmax by (score desc, token asc); the tree's top 8 by
 // the same order; the softmax normaliser summed in float64 and rounded to float32).
@@ -502,106 +503,115 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     }
     __syncthreads();
     const int nu = S.nu;
-    // ---- phase C1: features, one thread per candidate, into LDS rows ----
-    if (tid < nu) {
-      const int tok = S.uniq[tid];
-      float* f = S.F + tid * ILD_NF;
-      for (int i = 0; i < ILD_NF; ++i) f[i] = 0.f;
-      f[0] = 1.f;
-      float f2 = 0.f, f17 = 0.f, f25;
-      const int ln = S.s_long;
-      for (int n = 1; n <= 6; ++n) {
-        const int tot = S.dist_tot[n];
-        if (tot < 0) continue;
-        const int cnt = S.dist_cnt[n];
-        int c = 0, rank = -1;
-        for (int r = 0; r < cnt; ++r)
-          if (S.top_tok[n][r] == tok) {
-            c = S.top_cnt[n][r];
-            rank = r;
-            break;
-          }
-        if (n == ln && rank == 1) f[13] = 1.f;
-        if (n == ln && rank >= 2) f[14] = 1.f;
-        if (c > 0) {
-          const float p = (float)c / (float)tot;
-          f[6 + n] = p;
-          if (n == ln) {
-            f[1] = p;
-            f[3] = ((float)n / 6.f) * p;
-            f[4] = c < ILD_LG1P ? S.lg1p[c] : ild_logf(1.f + (float)c);
-          }
-          if (n == S.s_supp3) f[5] = p;
-          if (n == S.s_supp10) f[6] = p;
-        }
-      }
-      if (tok == S.s_toplong) {
-        f[2] = f2 = 1.f;
-        if (S.s_entlow) f[15] = 1.f;
-      }
-      const int sn = S.self_n;
-      if (sn > 0 && tok == S.self_tok) {
-        f[16] = (float)sn / 4.f;
-        f[17] = f17 = 1.f;
-        f[18] = sn >= 3 ? 1.f : 0.f;
-      }
-      for (int q = 0; q < S.pr_cnt; ++q)
-        if (S.pr_tok[q] == tok) {
-          f[19] = (float)S.pr_n / 4.f;
-          f[20] = 1.f;
-          f[21] = S.pr_n >= 2 ? 1.f : 0.f;
-          if (q == 0) f[22] = 1.f;
-        }
-      {
-        const int nnb = S.R.nnb;
-        float nbs = 0.f, nbm = 0.f, nbx = 0.f;
-        int nbc = 0;
-        for (int k = 0; k < nnb; ++k) {
-          if (S.vote_tok[k] != tok) continue;
-          const float sk = S.R.nbScore[k], mk = (float)min(S.vote_n[k], 8) / 8.f;
-          nbs = nbs + sk;
-          nbm = nbm + sk * mk;
-          nbc++;
-          nbx = fmaxf(nbx, mk);
-          if (k == 0) {
-            f[27] = 1.f;
-            f[28] = mk;
+    // ---- phase C1: features into LDS rows, two threads per candidate: waves 0-7 the
+    // n-gram, self-repetition, prompt and neighbour features (0-28, 31, 32), waves 8-15 the
+    // copy, association and token features (29, 30, 33-52) ----
+    if ((tid & 511) < nu) {
+      const int c = tid & 511;
+      const int tok = S.uniq[c];
+      float* f = S.F + c * ILD_NF;
+      if (tid < 512) {
+        for (int i = 0; i < 29; ++i) f[i] = 0.f;
+        f[0] = 1.f;
+        float f2 = 0.f, f17 = 0.f, f25;
+        const int ln = S.s_long;
+        for (int n = 1; n <= 6; ++n) {
+          const int tot = S.dist_tot[n];
+          if (tot < 0) continue;
+          const int cnt = S.dist_cnt[n];
+          int cn = 0, rank = -1;
+          for (int r = 0; r < cnt; ++r)
+            if (S.top_tok[n][r] == tok) {
+              cn = S.top_cnt[n][r];
+              rank = r;
+              break;
+            }
+          if (n == ln && rank == 1) f[13] = 1.f;
+          if (n == ln && rank >= 2) f[14] = 1.f;
+          if (cn > 0) {
+            const float p = (float)cn / (float)tot;
+            f[6 + n] = p;
+            if (n == ln) {
+              f[1] = p;
+              f[3] = ((float)n / 6.f) * p;
+              f[4] = cn < ILD_LG1P ? S.lg1p[cn] : ild_logf(1.f + (float)cn);
+            }
+            if (n == S.s_supp3) f[5] = p;
+            if (n == S.s_supp10) f[6] = p;
           }
         }
-        f[23] = nbs;
-        f[24] = nbm;
-        f[25] = f25 = (float)nbc / (float)max(1, nnb);
-        f[26] = nbx;
+        if (tok == S.s_toplong) {
+          f[2] = f2 = 1.f;
+          if (S.s_entlow) f[15] = 1.f;
+        }
+        const int sn = S.self_n;
+        if (sn > 0 && tok == S.self_tok) {
+          f[16] = (float)sn / 4.f;
+          f[17] = f17 = 1.f;
+          f[18] = sn >= 3 ? 1.f : 0.f;
+        }
+        for (int q = 0; q < S.pr_cnt; ++q)
+          if (S.pr_tok[q] == tok) {
+            f[19] = (float)S.pr_n / 4.f;
+            f[20] = 1.f;
+            f[21] = S.pr_n >= 2 ? 1.f : 0.f;
+            if (q == 0) f[22] = 1.f;
+          }
+        {
+          const int nnb = S.R.nnb;
+          float nbs = 0.f, nbm = 0.f, nbx = 0.f;
+          int nbc = 0;
+          for (int k = 0; k < nnb; ++k) {
+            if (S.vote_tok[k] != tok) continue;
+            const float sk = S.R.nbScore[k], mk = (float)min(S.vote_n[k], 8) / 8.f;
+            nbs = nbs + sk;
+            nbm = nbm + sk * mk;
+            nbc++;
+            nbx = fmaxf(nbx, mk);
+            if (k == 0) {
+              f[27] = 1.f;
+              f[28] = mk;
+            }
+          }
+          f[23] = nbs;
+          f[24] = nbm;
+          f[25] = f25 = (float)nbc / (float)max(1, nnb);
+          f[26] = nbx;
+        }
+        f[31] = f2 * fminf(1.f, 2.f * f25);
+        f[32] = f17 * fminf(1.f, 2.f * f25);
+      } else {
+        f[29] = 0.f;
+        f[30] = 0.f;
+        for (int i = 33; i < ILD_NF; ++i) f[i] = 0.f;
+        const int ci = ild_bsearch(S.R.copyTok, S.R.ncopy, tok);
+        const bool usedt = ild_has(S.used, tok);
+        const bool inp = ci >= 0 && S.R.copyInP[ci] != 0;
+        if (ci >= 0) {
+          f[33] = S.R.copyF33[ci];
+          f[34] = S.c1;
+          f[35] = S.c2;
+          f[36] = usedt ? 0.f : 1.f;
+          f[37] = tok == S.firstun ? 1.f : 0.f;
+          f[38] = inp ? 0.f : 1.f;
+        }
+        f[29] = (tok == 151645 || tok == 151643) ? 1.f : 0.f;
+        f[30] = inp ? 1.f : 0.f;
+        f[39] = (Lfull > 0 && (first_out == 73594 || first_out == 13874)) ? 1.f : 0.f;
+        f[40] = (Lfull > 0 && first_out == 63) ? 1.f : 0.f;
+        const uint32_t tf = tok < ILD_VOCAB ? (uint32_t)d.tflg[tok] : 0u;
+        f[41] = (tf & 7u) ? 1.f : 0.f;
+        f[42] = (tf & 8u) ? 1.f : 0.f;
+        f[43] = (float)(ticks & 1);
+        f[44] = (float)min(Lfull, 32) / 32.f;
+        f[45] = usedt ? 1.f : 0.f;
+        const int ai = ild_bsearch(S.R.asTok, S.R.nas, tok);
+        if (ai >= 0) {
+          f[46] = S.R.asMax[ai] / 4.f;
+          f[47] = (float)min(S.R.asCnt[ai], 4) / 4.f;
+        }
+        S.ctf[c] = (int)(tf & 7u);
       }
-      const int ci = ild_bsearch(S.R.copyTok, S.R.ncopy, tok);
-      const bool usedt = ild_has(S.used, tok);
-      const bool inp = ci >= 0 && S.R.copyInP[ci] != 0;
-      if (ci >= 0) {
-        f[33] = S.R.copyF33[ci];
-        f[34] = S.c1;
-        f[35] = S.c2;
-        f[36] = usedt ? 0.f : 1.f;
-        f[37] = tok == S.firstun ? 1.f : 0.f;
-        f[38] = inp ? 0.f : 1.f;
-      }
-      f[29] = (tok == 151645 || tok == 151643) ? 1.f : 0.f;
-      f[30] = inp ? 1.f : 0.f;
-      f[31] = f2 * fminf(1.f, 2.f * f25);
-      f[32] = f17 * fminf(1.f, 2.f * f25);
-      f[39] = (Lfull > 0 && (first_out == 73594 || first_out == 13874)) ? 1.f : 0.f;
-      f[40] = (Lfull > 0 && first_out == 63) ? 1.f : 0.f;
-      const uint32_t tf = tok < ILD_VOCAB ? (uint32_t)d.tflg[tok] : 0u;
-      f[41] = (tf & 7u) ? 1.f : 0.f;
-      f[42] = (tf & 8u) ? 1.f : 0.f;
-      f[43] = (float)(ticks & 1);
-      f[44] = (float)min(Lfull, 32) / 32.f;
-      f[45] = usedt ? 1.f : 0.f;
-      const int ai = ild_bsearch(S.R.asTok, S.R.nas, tok);
-      if (ai >= 0) {
-        f[46] = S.R.asMax[ai] / 4.f;
-        f[47] = (float)min(S.R.asCnt[ai], 4) / 4.f;
-      }
-      S.ctf[tid] = (int)(tf & 7u);
     }
     __syncthreads();
     // ---- phase C2: the scorer, HL lanes per candidate (lane h: hidden unit h) ----
@@ -616,16 +626,18 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
       for (int c0 = 0; c0 < nu; c0 += ILD_THREADS / HL) {
         const int c = c0 + tid / HL;
         const float* fr = S.F + min(c, nu - 1) * ILD_NF;
-        float acc = 0.f;
-        if (h < H) {
-          const float* wr = S.w1 + h * ILD_W1S;
-          acc = S.b1[h];
-#pragma unroll 8
-          for (int i = 0; i < ILD_NF; ++i) acc = acc + wr[i] * fr[i];
-        }
+        // the hidden unit's chain and the linear term's chain advance together (two
+        // independent dependency chains in one loop; each keeps its own order)
+        const float* wr = S.w1 + min(h, H - 1) * ILD_W1S;
+        float acc = S.b1[min(h, H - 1)];
         float sc = S.b2;
 #pragma unroll 8
-        for (int i = 0; i < ILD_NF; ++i) sc = sc + S.wl[i] * fr[i];
+        for (int i = 0; i < ILD_NF; ++i) {
+          const float x = fr[i];
+          acc = acc + wr[i] * x;
+          sc = sc + S.wl[i] * x;
+        }
+        if (h >= H) acc = 0.f;
         for (int hh = 0; hh < H; ++hh) {
           const float ah = __shfl(acc, gbase + hh, 64);
           sc = sc + S.w2[hh] * fmaxf(ah, 0.f);

@@ -390,70 +390,102 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
 // 16 x 896 fixed-point words (114 KB) per consumer workgroup, read by 14 ATT, 76 GUD and
 // 256 lm_head workgroups, each then running the same RMSNorm coding over 16 rows. Instead,
 // one PREP workgroup per row runs prep896 on its row once (the arithmetic of a 1-row pass,
-// so codes, group scales and row scale are bit-identical to it) and publishes the result
-// as ILL_PUB_PAY tagged words (payload | tag << 32, tag = epoch * 32 + slot + 1):
+// so codes, group scales and row scale are bit-identical to it) and publishes the result,
+// ILL_PUB_PAY payload dwords k:
 //   [0, 224)    A-operand high bytes, 56 uint4 (column group g, k-group gi at 4 g + gi)
 //   [224, 448)  low bytes
 //   [448, 476)  group scales, 14 float2 (d, d * sum of the codes)
 //   476         the row scale rsqrt(ss / 896 + eps)
-// Consumers read the published rows (61 KB for 16 rows) straight into PrepLds<16>.
+// in ILL_PUB_Q 128-bit words: word m = 32 j + r (j < 5, r < 32) holds payload dwords
+// k = 32 (3 j + i) + r, i < 3 (zero past 476), and a check dword tag ^ pub_mix(the three),
+// tag = epoch * 32 + slot + 1. A word left from another epoch fails the check (its tag
+// differs); one read torn between its halves fails it unless the mix collides (about 1 in
+// 2^32). Words are written and read whole at device scope (sc1), and a consumer polls until
+// every word it reads passes, so no ordering between the words is assumed.
+// Consumer half-wave r reads row r: its lane's 5 words are the payload dwords lane + 32 j'
+// (j' < 15) in order, which place into PrepLds<16> by shifts alone (16 rows: 40 KB).
 // Buffers: kind 0 holds the GUD inputs (slot l: XA[l] under ln2), kind 1 the ATT inputs
 // (slot l: x_l under ln1) and the final norm (slot = layers).
-#define ILL_PUB_W 480
 #define ILL_PUB_PAY 477
+#define ILL_PUB_Q 160                       // 128-bit words per row
+#define ILL_PUB_W (ILL_PUB_Q * 2)           // in 64-bit units
+#define ILL_PUB_LIGHT 156                   // the word holding the row scale (k = 476)
 #define ILL_PUB_WORDS (2 * (ILL_MAXLAYERS + 1) * ILL_MAXT * ILL_PUB_W)
+#define ILL_BUF_SC1 16   // buffer access cache policy: device scope (sc1)
+typedef uint32_t ill_v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint32_t tagof_pub(uint32_t epoch, int slot) { return epoch * 32u + (uint32_t)slot + 1u; }
 __device__ __forceinline__ uint64_t* pub_ptr(const IllPassArgs& a, int kind, int slot, int t) {
   return a.pub + (((size_t)kind * (ILL_MAXLAYERS + 1) + slot) * ILL_MAXT + t) * ILL_PUB_W;
 }
+__device__ __forceinline__ uint32_t pub_mix(uint32_t x, uint32_t y, uint32_t z) {
+  uint32_t h = x * 0x9E3779B1u;
+  h = (h ^ (h >> 15)) + y * 0x85EBCA77u;
+  h = (h ^ (h >> 13)) + z * 0xC2B2AE3Du;
+  return h ^ (h >> 16);
+}
+__device__ __forceinline__ bool pub_ok(const ill_v4u& q, uint32_t tag) { return q[3] == (tag ^ pub_mix(q[0], q[1], q[2])); }
+// byte-addressed buffer resource over n bytes from p (raw, untyped dword access)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pub_rsrc(const void* p, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, n, 0x00020000);
+}
 
-// Publish a 1-row coding (PrepLds<1> as prep896<1> left it, rs = its row scale).
+// Publish a 1-row coding (PrepLds<1> as prep896<1> left it, rs = its row scale): thread m
+// writes word m.
 __device__ __forceinline__ void pub_write(const PrepLds<1>& P, float rs, uint64_t* dst, uint32_t tag) {
-  const int k = tid_opaque();
-  if (k < ILL_PUB_PAY) {
-    uint32_t v;
-    if (k < 224) v = ((const uint32_t*)P.ahi)[k];
-    else if (k < 448) v = ((const uint32_t*)P.alo)[k - 224];
-    else if (k < 476) v = ((const uint32_t*)P.sc)[k - 448];
-    else v = __float_as_uint(rs);
-    astore64(dst + k, mkwu(v, tag));
+  static_assert(offsetof(PrepLds<1>, ahi) == 0 && offsetof(PrepLds<1>, alo) == 896 && offsetof(PrepLds<1>, sc) == 1792,
+                "payload dwords 0 .. 475 contiguous");
+  const int m = tid_opaque();
+  if (m < ILL_PUB_Q) {
+    const uint32_t* pw = (const uint32_t*)P.ahi;
+    uint32_t x[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int k = 32 * (3 * (m >> 5) + i) + (m & 31);
+      x[i] = k < 476 ? pw[k] : (k == 476 ? __float_as_uint(rs) : 0u);
+    }
+    const ill_v4u q = {x[0], x[1], x[2], tag ^ pub_mix(x[0], x[1], x[2])};
+    __builtin_amdgcn_raw_buffer_store_b128(q, pub_rsrc(dst, ILL_PUB_Q * 16), m * 16, 0, ILL_BUF_SC1);
   }
 }
 
 // The consumer side: rows 0 .. nrows - 1 of a published coding (src = row 0) into P, as
 // prep896<T> would have left it (rows >= nrows coded as zeros), and the row scales of this
-// lane's rows 4 kg + j in rs[j]. Half-wave r of the workgroup reads row r, words lane + 32 j
-// (j < 15): for j < 14 the word's kind (high / low bytes) and place follow from j and the
-// lane by shifts, so placing a word costs no division.
+// lane's rows 4 kg + j in rs[j]. Half-wave r of the workgroup reads row r: payload dwords
+// lane + 32 j (j < 15) into v[j]; for j < 14 the dword's kind (high / low bytes) and place
+// follow from j and the lane by shifts, so placing it costs no division.
 template <int T>
 __device__ __forceinline__ bool pub_read(const uint64_t* src, uint32_t tag, int nrows, PrepLds<T>& P, IllCtl* ctl,
                                          int code, const IllPassArgs& a, float rs[4], int trs = -1) {
-  static_assert(T == ILL_MAXT && ILL_PUB_W == 15 * 32 && T * 32 == ILL_WG_THREADS, "one half-wave per row");
+  static_assert(T == ILL_MAXT && ILL_PUB_Q == 5 * 32 && T * 32 == ILL_WG_THREADS, "one half-wave per row");
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int t = tid >> 5, l32 = tid & 31;
   const bool live = t < nrows;
-  const uint64_t* rp = src + (size_t)t * ILL_PUB_W + l32;
+  const __amdgpu_buffer_rsrc_t rsrc = pub_rsrc(src, ILL_MAXT * ILL_PUB_Q * 16);
+  const int rbase = t * (ILL_PUB_Q * 16) + l32 * 16;
   uint32_t v[15];
-  // light poll: the row's last word (its scale), the same address for the half-wave
-  const uint64_t* lp = src + (size_t)t * ILL_PUB_W + (ILL_PUB_PAY - 1);
+  // light poll: the word of the row scale, the same address for the half-wave. (Offsets
+  // pass through opq, so every poll issues its loads afresh.)
   const bool alive = wave_wait2([&]() {
-    return !live || (uint32_t)(aload64(lp) >> 32) == tag;
+    if (!live) return true;
+    return pub_ok(__builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(t * (ILL_PUB_Q * 16) + ILL_PUB_LIGHT * 16), 0, ILL_BUF_SC1), tag);
   }, [&]() {
     bool ok = true;
 #pragma unroll
-    for (int j = 0; j < 15; j++) {
-      v[j] = 0u;
-      if (live && 32 * j + l32 < ILL_PUB_PAY) {
-        const uint64_t x = aload64(rp + 32 * j);
-        ok &= (uint32_t)(x >> 32) == tag;
-        v[j] = (uint32_t)x;
+    for (int j = 0; j < 5; j++) {
+      ill_v4u q = {0u, 0u, 0u, 0u};
+      if (live) {
+        q = __builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(rbase + j * 512), 0, ILL_BUF_SC1);
+        ok &= pub_ok(q, tag);
       }
+      v[3 * j] = q[0];
+      v[3 * j + 1] = q[1];
+      v[3 * j + 2] = q[2];
     }
     return ok;
   }, ctl, code);
   if (trs >= 0) trace_mark(a, trs);
 #pragma unroll
-  for (int j = 0; j < 14; j++) {   // codes: word k = 32 j + l32 holds uint4 k / 4 (group, k-group), dword k % 4
+  for (int j = 0; j < 14; j++) {   // codes: dword k = 32 j + l32 is dword k % 4 of uint4 k / 4 (group, k-group)
     const int k = (j % 7) * 32 + l32;
     uint32_t* dst = (uint32_t*)(j < 7 ? P.ahi : P.alo);
     dst[((k >> 2) * T + t) * 4 + (k & 3)] = v[j];

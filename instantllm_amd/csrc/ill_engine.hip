@@ -117,6 +117,7 @@ struct ill_engine {
   uint16_t* kc = nullptr;
   uint16_t* vt = nullptr;
   uint64_t *acc = nullptr, *lmp = nullptr, *pub = nullptr;
+  uint4* part = nullptr;   // 16-row passes: down-projection partials (ILL_PART_WORDS 16-byte words)
   size_t acc_bytes = 0;
   float* logits = nullptr;
   int32_t* out_dev = nullptr;
@@ -232,7 +233,8 @@ int check_err(ill_engine* e) {
   HCK(hipStreamSynchronize(e->stream));
   if (err) {
     // An abandoned pass leaves partial sums behind (clear both accumulator banks) and tagged
-    // words of its own epoch in the published codings and the lm_head partials: the epoch
+    // words of its own epoch in the published codings, the down-projection partials and the
+    // lm_head partials: the epoch
     // moves on by two (the same bank parity), so the next pass's tags differ from them.
     uint32_t ep = 0;
     hipMemcpy(&ep, &e->ctl->epoch, 4, hipMemcpyDeviceToHost);
@@ -259,6 +261,7 @@ int count_passes(ill_engine* e, int n) {
   if (e->passes_since_clear < ILL_TAG_CLEAR_PASSES) return 0;
   HCK(hipStreamSynchronize(e->stream));
   HCK(hipMemsetAsync(e->pub, 0, (size_t)ILL_PUB_WORDS * 8, e->stream));
+  HCK(hipMemsetAsync(e->part, 0, (size_t)ILL_PART_WORDS * 16, e->stream));
   HCK(hipMemsetAsync(e->lmp, 0, (size_t)ILL_WG * 16 * 2 * 8, e->stream));
   HCK(hipStreamSynchronize(e->stream));
   e->passes_since_clear = (uint64_t)n;
@@ -682,6 +685,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
             dalloc((void**)&e->rope, (size_t)(e->maxctx + 16) * 32 * 8) && dalloc((void**)&e->kc, kvb) && dalloc((void**)&e->vt, kvb) &&
             dalloc((void**)&e->acc, e->acc_bytes) &&
             dalloc((void**)&e->lmp, (size_t)ILL_WG * 16 * 2 * 8) && dalloc((void**)&e->pub, (size_t)ILL_PUB_WORDS * 8) &&
+            dalloc((void**)&e->part, (size_t)ILL_PART_WORDS * 16) &&
             dalloc((void**)&e->logits, (size_t)16 * vocab * 4) &&
             dalloc((void**)&e->out_dev, (size_t)max_steps * 4);
   ok = ok && dalloc((void**)&e->dolayers, sizeof(OpLayerW) * layers) && dalloc((void**)&e->octx.x, (size_t)ILL_OP_MAXM * ILL_H * 4) &&
@@ -738,6 +742,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.acc = e->acc;
   a.lmp = e->lmp;
   a.pub = e->pub;
+  a.part = e->part;
   a.logits = e->logits;
   a.out_dev = e->out_dev;
   a.out_host = e->out_host;
@@ -770,7 +775,7 @@ int ill_destroy(ill_engine* e) {
   if (e->gexec) hipGraphExecDestroy(e->gexec);
   if (e->graph) hipGraphDestroy(e->graph);
   void* bufs[] = {e->dweights, e->dlayers, e->st, e->ctl, e->ptoks, e->tree, e->rope, e->kc, e->vt, e->acc,
-                  e->lmp, e->pub, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
+                  e->lmp, e->pub, e->part, e->logits, e->out_dev, e->args.trace, e->oweights, e->dolayers, e->octx.x, e->octx.xn,
                   e->octx.q, e->octx.ao, e->octx.h, e->octx.amax, e->opart, e->dtab, e->dtflg, e->dreq};
   for (void* p : bufs)
     if (p) hipFree(p);

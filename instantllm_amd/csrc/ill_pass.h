@@ -35,6 +35,8 @@
 #define ILL_R_BASE 14        // the residual-copy workgroup
 #define ILL_R_GUD0 16        // GUD WGs 16..91
 #define ILL_R_PREP0 92       // 16-row passes: PREP WGs 92..107 (one per row)
+#define ILL_R_RED0 108       // 16-row passes: REDUCE WGs 108..171 (row r / 4, column quarter r % 4)
+#define ILL_NRED 64
 
 struct IllPassArgs {
   IllWeights W;
@@ -53,6 +55,7 @@ struct IllPassArgs {
   int32_t* out_host;       // [maxsteps] pinned host memory
   uint64_t* trace;         // optional [256][ILL_TRACE_SLOTS] timestamps (nullptr = off)
   uint64_t* pub;           // 16-row passes: published row codings [2][ILL_MAXLAYERS + 1][16][ILL_PUB_W]
+  uint4* part;             // 16-row passes: down-projection partials [2][76][16][ILL_PART_ROW] checked words
   const uint4* ngram;      // optional n-gram draft table [ILL_NG_SLOTS] (nullptr: none)
   const int32_t* prompt;   // [4 + ILL_OB_MAX]: count, -, -, -, the last <= 256 prompt tokens
   int32_t* spec_host;      // pinned host [2]: passes and accepted drafts of speculative commits
@@ -841,6 +844,46 @@ __device__ __forceinline__ AttScale att_scale(float m, float m2) {
 }
 __device__ __forceinline__ float att_fold(float x, float x2, const AttScale& k) { return x * k.sa + x2 * k.sb; }
 
+// The outputs of split_gemv's multi-row form before they are added: y[k][j] is row
+// 4 kg + j, column 16 k + n of the wave's 112 (lane (kg, n)).
+template <int T>
+__device__ __forceinline__ void split_outputs(const uint8_t* so, const uint4* ahi, const uint4* alo, const float2* dsc,
+                                              int lane, float (&y)[7][4]) {
+  static_assert(T >= 4, "multi-row form");
+  const int kg = lane >> 4, n = lane & 15;
+  constexpr int RPL = 4;
+  const uint4 xh = ahi[kg * T + arow<T>(n)];
+  const uint4 xl = alo[kg * T + arow<T>(n)];
+  const v4i ah = (v4i){(int)xh.x, (int)xh.y, (int)xh.z, (int)xh.w};
+  const v4i al = (v4i){(int)xl.x, (int)xl.y, (int)xl.z, (int)xl.w};
+  const v4i z = {0, 0, 0, 0};
+  uint2 wv[7];
+  uint32_t sm[7];
+#pragma unroll
+  for (int k = 0; k < 7; k++) {
+    wv[k] = *(const uint2*)(so + k * 512 + lane * 8);
+    sm[k] = *(const uint32_t*)(so + 7 * 512 + k * 64 + n * 4);
+  }
+  float2 dx[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; j++) dx[j] = dsc[arow<T>(4 * kg + j)];
+#pragma unroll
+  for (int k = 0; k < 7; k++) {
+    const v4i bq = q4_unpack(wv[k].x, wv[k].y);
+    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
+    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
+    const float sw = h2f(sm[k] & 0xffff), mw = h2f(sm[k] >> 16);
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int Sv = (dh[j] << 8) + dl[j];
+      float v = 0.f;
+      v = fmaf(sw, dx[j].x * (float)Sv, v);
+      v = fmaf(mw, dx[j].y, v);
+      y[k][j] = v;
+    }
+  }
+}
+
 // Split-K partial of an 896-row projection over one 64-column input group (O: one head,
 // down: 64 hidden units), from this wave's 7 staged row tiles (rows 112 w .. +112, LDS
 // layout [7 x 512 B codes][7 x 64 B scales]). Each output y = s*d*S + m*X is added to
@@ -885,45 +928,133 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
     if (kg < 3) fx_add(accw + acc_col(16 * kb + n), fx_word(fx_of(yb)));
     return;
   }
-  const uint4 xh = ahi[kg * T + arow<T>(n)];
-  const uint4 xl = alo[kg * T + arow<T>(n)];
-  const v4i ah = (v4i){(int)xh.x, (int)xh.y, (int)xh.z, (int)xh.w};
-  const v4i al = (v4i){(int)xl.x, (int)xl.y, (int)xl.z, (int)xl.w};
-  const v4i z = {0, 0, 0, 0};
-  uint2 wv[7];
-  uint32_t sm[7];
-#pragma unroll
-  for (int k = 0; k < 7; k++) {
-    wv[k] = *(const uint2*)(so + k * 512 + lane * 8);
-    sm[k] = *(const uint32_t*)(so + 7 * 512 + k * 64 + n * 4);
-  }
-  float2 dx[RPL];
-#pragma unroll
-  for (int j = 0; j < RPL; j++) dx[j] = dsc[arow<T>(4 * kg + j)];
-  float y[7][RPL];
-#pragma unroll
-  for (int k = 0; k < 7; k++) {
-    const v4i bq = q4_unpack(wv[k].x, wv[k].y);
-    const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq, z, 0, 0, 0);
-    const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq, z, 0, 0, 0);
-    const float sw = h2f(sm[k] & 0xffff), mw = h2f(sm[k] >> 16);
+  if constexpr (T > 1) {
+    float y[7][4];
+    split_outputs<T>(so, ahi, alo, dsc, lane, y);
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
-      const int Sv = (dh[j] << 8) + dl[j];
-      float v = 0.f;
-      v = fmaf(sw, dx[j].x * (float)Sv, v);
-      v = fmaf(mw, dx[j].y, v);
-      y[k][j] = v;
+      const int t = 4 * kg + j;
+      if (t < nrows) {
+#pragma unroll
+        for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_ACC_ROW + acc_col(16 * k + n), fx_word(fx_of(y[k][j])));
+      }
     }
   }
-#pragma unroll
-  for (int j = 0; j < RPL; j++) {
-    const int t = 4 * kg + j;
-    if (t < nrows) {
-#pragma unroll
-      for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_ACC_ROW + acc_col(16 * k + n), fx_word(fx_of(y[k][j])));
-    }
+}
+
+// ---- down-projection partials (16-row passes) -------------------------------------------
+// GUD workgroup ub writes its partial y (rows t < nrows, 896 columns) as ILL_PART_ROW
+// checked 128-bit words per row (the publications' format: three float32 payload dwords
+// and tag ^ pub_mix): word (t, q, m), q < 4, m < 75, holds columns 224 q + 3 m + i, i < 3
+// (the third of word 74 is zero). Buffer half l & 1 serves layer l: a workgroup writes the
+// partials of layer l + 2 only after XB[l] is complete, that is after every REDUCE read of
+// layer l.
+#define ILL_PART_Q 75
+#define ILL_PART_ROW (4 * ILL_PART_Q)
+#define ILL_PART_WORDS (2 * ILL_NGU * ILL_MAXT * ILL_PART_ROW)
+__device__ __forceinline__ void part_write(const IllPassArgs& a, uint32_t epoch, int l, int ub, const float* yt, int nrows) {
+  const int tid = tid_opaque();
+  const uint32_t tag = tagof_pub(epoch, l);
+  const uint4* blk = a.part + ((size_t)((l & 1) * ILL_NGU + ub) * ILL_MAXT) * ILL_PART_ROW;
+  const __amdgpu_buffer_rsrc_t r = pub_rsrc(blk, ILL_MAXT * ILL_PART_ROW * 16);
+  for (int i = tid; i < nrows * ILL_PART_ROW; i += ILL_WG_THREADS) {
+    const int t = i / ILL_PART_ROW, rem = i - t * ILL_PART_ROW, q = rem / ILL_PART_Q, m = rem - q * ILL_PART_Q;
+    const float* src = yt + t * ILL_H + 224 * q + 3 * m;
+    const uint32_t x0 = __float_as_uint(src[0]), x1 = __float_as_uint(src[1]);
+    const uint32_t x2 = m < ILL_PART_Q - 1 ? __float_as_uint(src[2]) : 0u;
+    const ill_v4u wd = {x0, x1, x2, tag ^ pub_mix(x0, x1, x2)};
+    __builtin_amdgcn_raw_buffer_store_b128(wd, r, i * 16, 0, ILL_BUF_SC1);
   }
+}
+
+// REDUCE (16-row passes, ILL_NRED workgroups; rows t >= nrows idle): workgroup r owns row
+// t = r / 4, columns 224 q .. 224 q + 223 (q = r % 4), of the residual stream, in place of
+// the BASE workgroup of shorter passes. First it adds the embedding into XA[0]; then, layer
+// by layer, it sums the 76 partials of the down projection (their fx_of values, as the
+// atomics of shorter passes would) and the completed XA[l], makes that total XB[l] in one
+// contribution of count 77, and adds it into XA[l + 1] as the base of the next layer. The
+// integers are the ones the per-partial atomics and the BASE copies would have produced.
+// Threads (g, m), g < 6, m < 75, poll and sum word m of producers g, g + 6, ...; the six
+// sums of a word meet in LDS.
+template <int T>
+__device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H, int r, uint8_t* lds) {
+  const int t = r >> 2, q = r & 3;
+  if (t >= H.nrows) return true;
+  const int NL = a.W.layers;
+  const int tid = tid_opaque();
+  const int g = tid / ILL_PART_Q, m = tid - g * ILL_PART_Q;
+  const bool act = g < 6;
+  int64_t* red = (int64_t*)lds;   // [6][75][3]
+  constexpr int PSTRIDE = ILL_MAXT * ILL_PART_ROW * 16;   // bytes per producer
+  const int off = (t * ILL_PART_ROW + q * ILL_PART_Q + m) * 16;
+  const int col = 224 * q + tid;   // the column of threads tid < 224
+  if (tid < 224) fx_add(acc_ptr(a, H.bank, 0, 0, t) + acc_col(col), fx_word(fx_of(embed1(a.W, H.tok[t], col))));
+  for (int l = 0; l < NL; l++) {
+    trace_mark(a, ILL_TRL * l);
+    const uint32_t tag = tagof_pub(H.epoch, l);
+    const __amdgpu_buffer_rsrc_t rs = pub_rsrc(a.part + (size_t)(l & 1) * ILL_NGU * ILL_MAXT * ILL_PART_ROW, ILL_NGU * PSTRIDE);
+    int64_t s0 = 0, s1 = 0, s2 = 0;
+    const bool alive = wave_wait2([&]() {
+      return !act || pub_ok(__builtin_amdgcn_raw_buffer_load_b128(rs, opq(off + g * PSTRIDE), 0, ILL_BUF_SC1), tag);
+    }, [&]() {
+      bool ok = true;
+      s0 = s1 = s2 = 0;
+      if (act) {
+        ill_v4u wv[13];
+#pragma unroll
+        for (int i = 0; i < 13; i++) {
+          const int p = g + 6 * i;
+          wv[i] = (ill_v4u){0u, 0u, 0u, 0u};
+          if (p < ILL_NGU) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, opq(off + p * PSTRIDE), 0, ILL_BUF_SC1);
+        }
+#pragma unroll
+        for (int i = 0; i < 13; i++) {
+          if (g + 6 * i < ILL_NGU) {
+            ok &= pub_ok(wv[i], tag);
+            s0 += fx_of(__uint_as_float(wv[i][0]));
+            s1 += fx_of(__uint_as_float(wv[i][1]));
+            s2 += fx_of(__uint_as_float(wv[i][2]));
+          }
+        }
+      }
+      return ok;
+    }, a.ctl, 900 + l);
+    if (!__syncthreads_and(alive)) return false;
+    trace_mark(a, ILL_TRL * l + 1);
+    if (act) {
+      red[(g * ILL_PART_Q + m) * 3 + 0] = s0;
+      red[(g * ILL_PART_Q + m) * 3 + 1] = s1;
+      red[(g * ILL_PART_Q + m) * 3 + 2] = s2;
+    }
+    __syncthreads();
+    bool xa_ok = true;
+    if (tid < 224) {
+      const int mm = tid / 3, i = tid - 3 * (tid / 3);
+      int64_t sum = 0;
+#pragma unroll
+      for (int gg = 0; gg < 6; gg++) sum += red[(gg * ILL_PART_Q + mm) * 3 + i];
+      // XA[l] (14 heads and this workgroup's base): long complete when the partials arrive
+      const uint64_t* xa = acc_ptr(a, H.bank, l, 0, t) + acc_col(col);
+      uint64_t xw = 0;
+      xa_ok = wave_wait([&]() {
+        xw = aload64(xa);
+        return fx_count(xw) == xa_expect<T>(0);
+      }, a.ctl, 950 + l);
+      sum += fx_value(xw);
+      constexpr int64_t NB = ILL_NGU + 1;
+      fx_add(acc_ptr(a, H.bank, l, ILL_KIND_XB, t) + acc_col(col), (uint64_t)NB * FX_COUNT + (uint64_t)(sum + NB * FX_BIAS));
+      if (l + 1 < NL) fx_add(acc_ptr(a, H.bank, l + 1, 0, t) + acc_col(col), fx_word(sum));
+    }
+    if (!__syncthreads_and(xa_ok)) return false;
+    trace_mark(a, ILL_TRL * l + 10);
+    if (a.trace) {
+      wait_vm();
+      trace_mark(a, ILL_TRL * l + 12);
+    }
+    __syncthreads();   // red is rewritten by the next layer
+    trace_mark(a, ILL_TRL * l + 11);
+  }
+  return true;
 }
 
 // 16-row passes: the partial chunk c (the chunk holding pos, or the one after it) for
@@ -1418,8 +1549,26 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   }
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 5);
-  split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + acc_col(16 * 7 * w));
+  if constexpr (ill_pub<T>()) {
+    // 16-row passes: the partial leaves as plain checked words, and the REDUCE workgroups
+    // make one accumulator contribution per word out of the 76 partials (the atomics of 76
+    // workgroups x 16 rows would queue at the memory side for several microseconds)
+    float y[7][4];
+    split_outputs<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, y);
+    float* yt = (float*)stage;   // [16][896]: the gate/up stage, free after the gate/up GEMM
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int t = 4 * kg + j;
+#pragma unroll
+      for (int k = 0; k < 7; k++)
+        if (t < nrows) yt[t * ILL_H + 112 * w + 16 * k + n] = y[k][j];
+    }
+    lds_barrier();
+    part_write(a, H.epoch, l, ub, yt, nrows);
+  } else {
+    split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, G.ahi, G.alo, G.dsc, lane, nrows,
+                  acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + acc_col(16 * 7 * w));
+  }
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -1969,12 +2118,14 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       if (l + 1 < NL) gud_stage(a.L[l + 1], ub, w, lane, ill_stage);
       trace_mark(a, ILL_TRL * l + 11);
     }
-  } else if (wg == ILL_R_BASE) {
+  } else if (!ill_pub<T>() && wg == ILL_R_BASE) {   // (16-row passes: REDUCE keeps the residual)
     for (int l = 0; l < NL; l++) {
       trace_mark(a, ILL_TRL * l);
       if (!role_base<T>(a, H, l)) return;
       trace_mark(a, ILL_TRL * l + 11);
     }
+  } else if (ill_pub<T>() && wg >= ILL_R_RED0 && wg < ILL_R_RED0 + ILL_NRED) {
+    if (!role_red<T>(a, H, wg - ILL_R_RED0, ill_stage)) return;
   } else if (ill_pub<T>() && wg >= ILL_R_PREP0 && wg < ILL_R_PREP0 + ILL_MAXT) {
     const int t = wg - ILL_R_PREP0;
     if (t < H.nrows) {

@@ -37,6 +37,7 @@
 #define ILL_R_PREP0 92       // 16-row passes: PREP WGs 92..107 (one per row)
 #define ILL_R_RED0 108       // 16-row passes: REDUCE WGs 108..171 (row r / 4, column quarter r % 4)
 #define ILL_NRED 64
+#define ILL_R_ATT1 172       // 16-row passes: ATT WGs 172..185, rows 8-15 of head wg - 172
 
 struct IllPassArgs {
   IllWeights W;
@@ -895,7 +896,7 @@ __device__ __forceinline__ void split_outputs(const uint8_t* so, const uint4* ah
 // The arithmetic of each output is the same in both forms.
 template <int T>
 __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, const uint4* alo, const float2* dsc,
-                                           int lane, int nrows, uint64_t* accw) {
+                                           int lane, int nrows, uint64_t* accw, int rlo = 0) {
   const int kg = lane >> 4, n = lane & 15;
   constexpr int RPL = T >= 4 ? 4 : T;
   if constexpr (T == 1) {
@@ -934,7 +935,7 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
-      if (t < nrows) {
+      if (t >= rlo && t < nrows) {
 #pragma unroll
         for (int k = 0; k < 7; k++) fx_add(accw + (size_t)t * ILL_ACC_ROW + acc_col(16 * k + n), fx_word(fx_of(y[k][j])));
       }
@@ -1071,7 +1072,7 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
 // q < 24 (a range holding pos .. pos + 15): path row values at depths 0 .. depth(t), else 0.
 template <int T>
 __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, const uint8_t* stage, const KVFrag& f, int c,
-                                            bool cache, const v8h qa[2][2]) {
+                                            bool cache, const v8h qa[2][2], int rlo, int rhi) {
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int pos = H.pos, nrows = H.nrows, ns = pos >> 6;
@@ -1151,7 +1152,7 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
 #pragma unroll
   for (int r = 0; r < 2; r++) {
     const int t = w + ILL_WAVES * r;
-    if (t >= nrows) continue;
+    if (t < rlo || t >= rhi) continue;   // rows of this workgroup only
     const int Lt = pos + H.depth[t] + 1;
     if (Lt <= 64 * c) continue;   // wave-uniform: no position of the chunk is on the row's path
     const int j = t & 3;
@@ -1208,7 +1209,7 @@ __device__ __forceinline__ int att_pair_chunk(const PassHdr& H, int ns, int cmax
 }
 
 template <int T>
-__device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int h, uint8_t* stage) {
+__device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H, AttLds<T>& A, int l, int h, int half, uint8_t* stage) {
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int g = h / 7;
@@ -1216,6 +1217,11 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   constexpr int RPL = T >= 4 ? 4 : T;
   const int nrows = H.nrows;
   const int pos = H.pos;
+  // 16-row passes split the rows over two workgroups per head (half 0: rows 0-7, half 1:
+  // rows 8-15); both compute every row's q, k and v (the tiles are 16 rows wide anyway) and
+  // the shared chunks, and each finishes its own rows: path values, the partial chunk's
+  // P·V, the combine and the O contributions
+  const int rlo = ill_pub<T>() ? 8 * half : 0, rhi = ill_pub<T>() ? min(nrows, rlo + 8) : nrows;
   // QKV epilogue constants (independent of the input): bias and RoPE (cos, sin) per row
   const int nt = qkv_nt<T>(w), lt0 = qkv_lt0<T>(w);
   const int bw = lt0 >> 1, hf1 = nt == 1 ? (lt0 & 1) : 0;   // block; a single tile's half
@@ -1298,7 +1304,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   } else if (nt == 2) {
     const int b = att_block(h, bw);
     const int head = b >> 1;
-    const bool writer = (h % 7) == 0;   // one query head per group writes the K/V cache
+    const bool writer = (h % 7) == 0 && half == 0;   // one workgroup per group writes the K/V cache
 #pragma unroll
     for (int j = 0; j < RPL; j++) {
       const int t = 4 * kg + j;
@@ -1344,7 +1350,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     const int d0 = 8 * (pos >> 3) - pos;   // depth of q = 0 (-7 .. 0)
     static_assert(T * 32 <= ILL_WG_THREADS, "one thread per (row, dim pair)");
     const int t1 = min(tid >> 5, T - 1), dp = tid & 31;   // row t1, dims 2 dp and 2 dp + 1
-    const int dep = (tid >> 5) < nrows ? H.depth[t1] : -1;
+    const int dep = (tid >> 5) >= rlo && (tid >> 5) < rhi ? H.depth[t1] : -1;   // (rows of this workgroup)
     uint32_t e[24];   // both dims' values (low half: dim 2 dp)
 #pragma unroll
     for (int q = 0; q < 24; q++) {
@@ -1422,7 +1428,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
         kv_fetch(kbase, vbase, c, lane, f);
         fc = c;
       }
-      part_eval16<T>(H, A, stage, f, c, cache, qa);
+      part_eval16<T>(H, A, stage, f, c, cache, qa, rlo, rhi);
     }
   }
   trace_mark(a, ILL_TRL * l + 6);
@@ -1446,7 +1452,7 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   // slots against the global maximum; row t by wave t % 8, one dim per lane, then the row
   // is coded as the A operand of the O projection (one quant group: head h's columns)
   for (int t = w; t < T; t += ILL_WAVES) {
-    if (t >= nrows) {
+    if (t < rlo || t >= rhi) {   // not this workgroup's row (or not live): coded as zeros
       if (lane < 4) {
         A.ahi[lane * T + t] = make_uint4(0, 0, 0, 0);
         A.alo[lane * T + t] = make_uint4(0, 0, 0, 0);
@@ -1489,8 +1495,8 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   trace_mark(a, ILL_TRL * l + 8);
   wait_vm();   // this wave's staged O tiles
   trace_mark(a, ILL_TRL * l + 9);
-  split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, nrows,
-                acc_ptr(a, H.bank, l, h % xa_copies<T>(), 0) + acc_col(16 * 7 * w));
+  split_gemv<T>(stage + ill_st_o(T) + w * ILL_ST_SPLIT, A.ahi, A.alo, A.dsc, lane, rhi,
+                acc_ptr(a, H.bank, l, h % xa_copies<T>(), 0) + acc_col(16 * 7 * w), rlo);
   trace_mark(a, ILL_TRL * l + 10);
   if (a.trace) {   // traced runs only: when this wave's contributions have landed
     wait_vm();
@@ -2094,13 +2100,15 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   const int wg = blockIdx.x;
   const int NL = a.W.layers;
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  if (wg >= ILL_R_ATT0 && wg < ILL_R_ATT0 + ILL_NATT) {
-    const int h = wg - ILL_R_ATT0;
+  const bool att0 = wg >= ILL_R_ATT0 && wg < ILL_R_ATT0 + ILL_NATT;
+  const bool att1 = ill_pub<T>() && wg >= ILL_R_ATT1 && wg < ILL_R_ATT1 + ILL_NATT;
+  if (att0 || att1) {
+    const int h = att0 ? wg - ILL_R_ATT0 : wg - ILL_R_ATT1, half = att0 ? 0 : 1;
     att_stage_qkv<T>(a.L[0], h, w, lane, ill_stage);
     if (T == 1) att_stage_o<T>(a.L[0], h, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
       trace_mark(a, ILL_TRL * l);
-      if (!role_att<T>(a, H, S.att, l, h, ill_stage)) return;
+      if (!role_att<T>(a, H, S.att, l, h, half, ill_stage)) return;
       lds_barrier();   // every wave is done with the stage before it is refilled
       if (l + 1 < NL) {
         att_stage_qkv<T>(a.L[l + 1], h, w, lane, ill_stage);

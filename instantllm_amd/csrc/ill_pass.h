@@ -35,9 +35,10 @@
 #define ILL_R_BASE 14        // the residual-copy workgroup
 #define ILL_R_GUD0 16        // GUD WGs 16..91
 #define ILL_R_PREP0 92       // 16-row passes: PREP WGs 92..107 (one per row)
-#define ILL_R_RED0 108       // 16-row passes: REDUCE WGs 108..171 (row r / 4, column quarter r % 4)
-#define ILL_NRED 64
-#define ILL_R_ATT1 172       // 16-row passes: ATT WGs 172..185, rows 8-15 of head wg - 172
+#define ILL_RED_Q 8          // 16-row passes: REDUCE WGs per row
+#define ILL_NRED (ILL_RED_Q * ILL_MAXT)
+#define ILL_R_RED0 108       // 16-row passes: REDUCE WGs 108..235 (row r / 8, column eighth r % 8)
+#define ILL_R_ATT1 236       // 16-row passes: ATT WGs 236..249, rows 8-15 of head wg - 236
 
 struct IllPassArgs {
   IllWeights W;
@@ -946,12 +947,13 @@ __device__ __forceinline__ void split_gemv(const uint8_t* so, const uint4* ahi, 
 // ---- down-projection partials (16-row passes) -------------------------------------------
 // GUD workgroup ub writes its partial y (rows t < nrows, 896 columns) as ILL_PART_ROW
 // checked 128-bit words per row (the publications' format: three float32 payload dwords
-// and tag ^ pub_mix): word (t, q, m), q < 4, m < 75, holds columns 224 q + 3 m + i, i < 3
-// (the third of word 74 is zero). Buffer half l & 1 serves layer l: a workgroup writes the
+// and tag ^ pub_mix): word (t, q, m), q < 8, m < 38, holds columns 112 q + 3 m + i, i < 3
+// (the last two of word 37 are zero). Buffer half l & 1 serves layer l: a workgroup writes the
 // partials of layer l + 2 only after XB[l] is complete, that is after every REDUCE read of
 // layer l.
-#define ILL_PART_Q 75
-#define ILL_PART_ROW (4 * ILL_PART_Q)
+#define ILL_RED_COLS (ILL_H / ILL_RED_Q)          // columns per REDUCE workgroup (112)
+#define ILL_PART_Q ((ILL_RED_COLS + 2) / 3)      // words per (row, REDUCE workgroup)
+#define ILL_PART_ROW (ILL_RED_Q * ILL_PART_Q)
 #define ILL_PART_WORDS (2 * ILL_NGU * ILL_MAXT * ILL_PART_ROW)
 __device__ __forceinline__ void part_write(const IllPassArgs& a, uint32_t epoch, int l, int ub, const float* yt, int nrows) {
   const int tid = tid_opaque();
@@ -960,36 +962,38 @@ __device__ __forceinline__ void part_write(const IllPassArgs& a, uint32_t epoch,
   const __amdgpu_buffer_rsrc_t r = pub_rsrc(blk, ILL_MAXT * ILL_PART_ROW * 16);
   for (int i = tid; i < nrows * ILL_PART_ROW; i += ILL_WG_THREADS) {
     const int t = i / ILL_PART_ROW, rem = i - t * ILL_PART_ROW, q = rem / ILL_PART_Q, m = rem - q * ILL_PART_Q;
-    const float* src = yt + t * ILL_H + 224 * q + 3 * m;
-    const uint32_t x0 = __float_as_uint(src[0]), x1 = __float_as_uint(src[1]);
-    const uint32_t x2 = m < ILL_PART_Q - 1 ? __float_as_uint(src[2]) : 0u;
+    const float* src = yt + t * ILL_H + ILL_RED_COLS * q + 3 * m;
+    const uint32_t x0 = __float_as_uint(src[0]);
+    const uint32_t x1 = 3 * m + 1 < ILL_RED_COLS ? __float_as_uint(src[1]) : 0u;
+    const uint32_t x2 = 3 * m + 2 < ILL_RED_COLS ? __float_as_uint(src[2]) : 0u;
     const ill_v4u wd = {x0, x1, x2, tag ^ pub_mix(x0, x1, x2)};
     __builtin_amdgcn_raw_buffer_store_b128(wd, r, i * 16, 0, ILL_BUF_SC1);
   }
 }
 
 // REDUCE (16-row passes, ILL_NRED workgroups; rows t >= nrows idle): workgroup r owns row
-// t = r / 4, columns 224 q .. 224 q + 223 (q = r % 4), of the residual stream, in place of
+// t = r / 8, columns 112 q .. 112 q + 111 (q = r % 8), of the residual stream, in place of
 // the BASE workgroup of shorter passes. First it adds the embedding into XA[0]; then, layer
 // by layer, it sums the 76 partials of the down projection (their fx_of values, as the
 // atomics of shorter passes would) and the completed XA[l], makes that total XB[l] in one
 // contribution of count 77, and adds it into XA[l + 1] as the base of the next layer. The
 // integers are the ones the per-partial atomics and the BASE copies would have produced.
-// Threads (g, m), g < 6, m < 75, poll and sum word m of producers g, g + 6, ...; the six
+// Threads (g, m), g < 13, m < 38, poll and sum word m of producers g, g + 13, ...; the 13
 // sums of a word meet in LDS.
 template <int T>
 __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H, int r, uint8_t* lds) {
-  const int t = r >> 2, q = r & 3;
+  constexpr int NG = ILL_WG_THREADS / ILL_PART_Q, PER = (ILL_NGU + NG - 1) / NG;   // 13 groups of 6 producers
+  const int t = r / ILL_RED_Q, q = r % ILL_RED_Q;
   if (t >= H.nrows) return true;
   const int NL = a.W.layers;
   const int tid = tid_opaque();
   const int g = tid / ILL_PART_Q, m = tid - g * ILL_PART_Q;
-  const bool act = g < 6;
-  int64_t* red = (int64_t*)lds;   // [6][75][3]
+  const bool act = g < NG;
+  int64_t* red = (int64_t*)lds;   // [NG][ILL_PART_Q][3]
   constexpr int PSTRIDE = ILL_MAXT * ILL_PART_ROW * 16;   // bytes per producer
   const int off = (t * ILL_PART_ROW + q * ILL_PART_Q + m) * 16;
-  const int col = 224 * q + tid;   // the column of threads tid < 224
-  if (tid < 224) fx_add(acc_ptr(a, H.bank, 0, 0, t) + acc_col(col), fx_word(fx_of(embed1(a.W, H.tok[t], col))));
+  const int col = ILL_RED_COLS * q + tid;   // the column of threads tid < ILL_RED_COLS
+  if (tid < ILL_RED_COLS) fx_add(acc_ptr(a, H.bank, 0, 0, t) + acc_col(col), fx_word(fx_of(embed1(a.W, H.tok[t], col))));
   for (int l = 0; l < NL; l++) {
     trace_mark(a, ILL_TRL * l);
     const uint32_t tag = tagof_pub(H.epoch, l);
@@ -1001,16 +1005,16 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
       bool ok = true;
       s0 = s1 = s2 = 0;
       if (act) {
-        ill_v4u wv[13];
+        ill_v4u wv[PER];
 #pragma unroll
-        for (int i = 0; i < 13; i++) {
-          const int p = g + 6 * i;
+        for (int i = 0; i < PER; i++) {
+          const int p = g + NG * i;
           wv[i] = (ill_v4u){0u, 0u, 0u, 0u};
           if (p < ILL_NGU) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, opq(off + p * PSTRIDE), 0, ILL_BUF_SC1);
         }
 #pragma unroll
-        for (int i = 0; i < 13; i++) {
-          if (g + 6 * i < ILL_NGU) {
+        for (int i = 0; i < PER; i++) {
+          if (g + NG * i < ILL_NGU) {
             ok &= pub_ok(wv[i], tag);
             s0 += fx_of(__uint_as_float(wv[i][0]));
             s1 += fx_of(__uint_as_float(wv[i][1]));
@@ -1029,11 +1033,11 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
     }
     __syncthreads();
     bool xa_ok = true;
-    if (tid < 224) {
+    if (tid < ILL_RED_COLS) {
       const int mm = tid / 3, i = tid - 3 * (tid / 3);
       int64_t sum = 0;
 #pragma unroll
-      for (int gg = 0; gg < 6; gg++) sum += red[(gg * ILL_PART_Q + mm) * 3 + i];
+      for (int gg = 0; gg < NG; gg++) sum += red[(gg * ILL_PART_Q + mm) * 3 + i];
       // XA[l] (14 heads and this workgroup's base): long complete when the partials arrive
       const uint64_t* xa = acc_ptr(a, H.bank, l, 0, t) + acc_col(col);
       uint64_t xw = 0;

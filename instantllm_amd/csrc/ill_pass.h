@@ -1070,8 +1070,9 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
 // at that row's position, and the softmax runs in the same lane layout, so a row's maximum
 // and sum match that pass bit for bit. The value operand differs per row, so each row's
 // P x V runs on its own operand (the cached values below pos, the table of path values vq
-// above it), with the 1-row pass's instruction sequence. Wave w finishes rows w and w + 8:
-// their statistics and outputs go to A.pm / A.pl / A.po[c - ns].
+// above it), with the 1-row pass's instruction sequence. Wave w finishes the one row of
+// rows w and w + 8 that belongs to its workgroup (rows rlo .. rhi - 1): its statistics and
+// output go to A.pm / A.pl / A.po[c - ns].
 // vq (stage + ILL_ST_VPT): [row t][dim][24] f16, the values at positions 8 (pos / 8) + q,
 // q < 24 (a range holding pos .. pos + 15): path row values at depths 0 .. depth(t), else 0.
 template <int T>
@@ -1092,13 +1093,18 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
     sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][0], k1, sp, 0, 0, 0);
     sp = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], k1, sp, 0, 0, 0);
   }
-  int Lr[4];   // L(t) of this lane's rows (0: no row)
+  // The one row this wave finishes (rows w and w + 8 that belong to this workgroup: at
+  // most one), and its place j0 = t0 % 4 in the lanes' row blocks. The softmax runs for
+  // rows 4 kg + j0 only (t0 among them); the other rows' P stays unwritten, and their P.V
+  // outputs are not used.
+  int t0 = -1;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int t = 4 * kg + j;
-    Lr[j] = t < nrows ? pos + H.depth[t] + 1 : 0;
-  }
-  float sc[4][4];
+  for (int r = 0; r < 2; r++)
+    if (w + ILL_WAVES * r >= rlo && w + ILL_WAVES * r < rhi) t0 = w + ILL_WAVES * r;
+  if (t0 < 0) return;
+  const int j0 = t0 & 3, tr = 4 * kg + j0;
+  const int Lr = tr < nrows ? pos + H.depth[tr] + 1 : 0;   // L of this lane's row (0: no row)
+  float sc[4];
 #pragma unroll
   for (int b = 0; b < 4; b++) {
     const int vp = 64 * c + 16 * b + n;
@@ -1110,35 +1116,26 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
       s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[1][1], u4_to_v8h(f.k[b][1]), s, 0, 0, 0);
     }
     const int dd = min(max(vp - pos, 0), 15);   // depth of a pass position
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int src = (lane & 48) | H.prow[4 * kg + j][dd];
-      const float g = __shfl(sp[j], src, 64);
-      sc[b][j] = vp < pos ? s[j] : (vp < Lr[j] ? g : -INFINITY);
-    }
+    const int src = (lane & 48) | H.prow[tr][dd];
+    const float g = __shfl(j0 == 0 ? sp[0] : j0 == 1 ? sp[1] : j0 == 2 ? sp[2] : sp[3], src, 64);
+    const float sv = j0 == 0 ? s[0] : j0 == 1 ? s[1] : j0 == 2 ? s[2] : s[3];
+    sc[b] = vp < pos ? sv : (vp < Lr ? g : -INFINITY);
   }
-  float mx[4], ls[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const float m = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
-    mx[j] = gmax<16>(m);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
+  float mx, ls;
+  {
+    const float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = gmax<16>(m);
     float sum = 0.f;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-      sc[b][j] = att_exp(sc[b][j] - mx[j]);
-      sum += sc[b][j];
+      sc[b] = att_exp(sc[b] - mx);
+      sum += sc[b];
     }
-    ls[j] = gsum<16>(sum);
+    ls = gsum<16>(sum);
   }
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-#pragma unroll
-    for (int b = 0; b < 4; b++)
-      if (4 * kg + j < T) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
-  }
+  for (int b = 0; b < 4; b++)
+    if (tr < T) pb[tr * 64 + 16 * b + n] = sc[b];
   wave_lds_sync();
   v8h ph[2], pl[2];
 #pragma unroll
@@ -1153,16 +1150,13 @@ __device__ __forceinline__ void part_eval16(const PassHdr& H, AttLds<T>& A, cons
   }
   wave_lds_sync();
   const uint4* vq = (const uint4*)(stage + ILL_ST_VPT);
-#pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int t = w + ILL_WAVES * r;
-    if (t < rlo || t >= rhi) continue;   // rows of this workgroup only
+  {
+    const int t = t0, j = j0;
     const int Lt = pos + H.depth[t] + 1;
-    if (Lt <= 64 * c) continue;   // wave-uniform: no position of the chunk is on the row's path
-    const int j = t & 3;
+    if (Lt <= 64 * c) return;   // wave-uniform: no position of the chunk is on the row's path
     if (kg == (t >> 2) && n == 0) {
-      A.pm[c - ns][t] = j == 0 ? mx[0] : j == 1 ? mx[1] : j == 2 ? mx[2] : mx[3];
-      A.pl[c - ns][t] = j == 0 ? ls[0] : j == 1 ? ls[1] : j == 2 ? ls[2] : ls[3];
+      A.pm[c - ns][t] = mx;
+      A.pl[c - ns][t] = ls;
     }
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {

@@ -132,8 +132,8 @@ int ill_capture_spec(ill_engine* e, int npasses);
  * launch per pass otherwise), while polling out_tokens. adaptive != 0 chooses each launch's
  * shape from the accepted drafts per pass (Engine.nextPassShape, :888-898, with thresholds
  * from this engine's pass costs, which grow with the kernel's row count): the configured
- * shape while at least 3.4 are accepted, 4-row chains while at least 1.4 are (back to the
- * configured shape at 2.5), else one-row passes with a 4-row probe every 16 passes.
+ * shape while at least 2.4 are accepted, 4-row chains while at least 1.6 are (back to the
+ * configured shape at 2.2), else one-row passes with a 4-row probe every 16 passes.
  * out / n_out as for ill_generate; stats (optional, [2]) receives the passes and accepted
  * drafts of the request. */
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,

@@ -1335,13 +1335,14 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   if ((rc = ill_prefill(e, toks + common, ntok - common, 0))) return rc;
   const bool graphs = e->fmt == 2;
   // Pass shapes (Engine.nextPassShape, Engine.swift:888-898, with thresholds from this
-  // engine's pass costs, which grow with the kernel's row count: about 345 us for 1 row,
-  // 830 us for 4 and 1.24 ms for 16, plus the drafting): a pass of 1 + r tokens beats plain
-  // decoding when r >= 1.4 accepted drafts (4 rows) or r >= 3.4 (16 rows with drafting).
-  // Level 0 is the configured shape, kept while r >= 3.4 over the last few passes at that
-  // level; level 1 a 4-row chain (3 drafts), back to level 0 at r >= 2.5, kept at r >= 1.4;
-  // level 2 one-row passes without drafts (a decode step's cost), left for a 4-row probe
-  // after 16 passes. Passes at a level only count toward its own rate.
+  // engine's pass costs, which grow with the kernel's row count: about 340 us for 1 row,
+  // 800 us for 4 and 860 us for 16, plus the drafting, up to 250 us for a learned tree): a
+  // pass of 1 + r tokens beats plain decoding when r >= 1.6 accepted drafts (4 rows) or
+  // r >= 2.3 (16 rows with a drafted tree). Level 0 is the configured shape, kept while
+  // r >= 2.4 over the last few passes at that level; level 1 a 4-row chain (3 drafts), back
+  // to level 0 at r >= 2.2, kept at r >= 1.6; level 2 one-row passes without drafts (a
+  // decode step's cost), left for a 4-row probe after 16 passes. Passes at a level only
+  // count toward its own rate.
   int level = 0, level_p0 = 0;
   std::vector<std::pair<int, int>> hist;
   auto shape_of = [&](int lv) -> std::pair<int, int> {
@@ -1358,8 +1359,8 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     const auto& first = hist[hist.size() >= 4 ? hist.size() - 4 : 0];
     if (p - first.first < 2) return level;
     const double rate = (double)(a - first.second) / (double)(p - first.first);
-    if (level == 0) return rate >= 3.4 ? 0 : (rows > 4 ? 1 : (rate >= 1.4 ? 0 : 2));
-    return rate >= 2.5 ? 0 : (rate >= 1.4 ? 1 : 2);
+    if (level == 0) return rate >= 2.4 ? 0 : (rows > 4 ? 1 : (rate >= 1.6 ? 0 : 2));
+    return rate >= 2.2 ? 0 : (rate >= 1.6 ? 1 : 2);
   };
   int cur_rows = rows;
   int drafted_rows = rows;   // the most rows a pending pass can hold (the prompt's commit drafted it)

@@ -195,10 +195,10 @@ def _decode_vs_chain(e, prompt, nsteps=15):
     return steps, graph_last, rows
 
 
-@pytest.mark.parametrize("nsteps", [15, 4, 3])
+@pytest.mark.parametrize("nsteps", [15, 4, 3, 2])
 def test_decode_steps_equal_chain_pass_rows_small(nsteps):
     """Small q4 model, prompt of 58 (the steps cross the 64-position chunk boundary); chains
-    of 15 rows (the 16-row kernel) and of 4 and 3 rows (the 4-row kernel)."""
+    of 15, 4 and 3 rows (the 16-row kernel) and of 2 rows (the 4-row kernel)."""
     from instantllm_amd.engine import Engine
     import tempfile
     import os

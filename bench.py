@@ -45,12 +45,12 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
 # a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (167,577.06 x 2 + 16,358.19) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 359_948_608
+# (163,477.6 x 2 + 16,358.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 351_552_922
 # MFMA utilisation of the 16-row verify pass and of the prefill GEMMs, from rocprofv3
 # SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
 MFMA_COUNTERS = {
-    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0062, "int8_TOPs": 27.7},
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0105, "int8_TOPs": 45.4},
     "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0104, "int8_TOPs": 48.1},
     "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.143, "f16_TFLOPs": 360.3},
     "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.109, "f16_TFLOPs": 275.1},
@@ -264,6 +264,45 @@ def speculative(path: str, n_new: int = 96) -> dict:
     return out
 
 
+def speculative_single(path: str, n_new: int = 96) -> dict:
+    """The learned drafter's passes of `speculative` launched one at a time (every verify
+    pass and every drafting kernel a dispatch of its own), for kernel traces: the profiler
+    does not survive a hipGraph launch here. Tree (15 drafts) and chain (7) requests."""
+    import tempfile
+    from instantllm_amd import ildraft as DW, illfile as F
+    from instantllm_amd.engine import Engine
+    e = Engine(path, max_context=1024, max_pass=16, max_steps=n_new + 32)
+    rng = np.random.default_rng(11)
+    words = ["w%d" % i for i in range(300)]
+    seen = [([int(t) for t in rng.integers(100, F.VOCAB, 24)], " ".join(rng.choice(words, 6))) for _ in range(8)]
+    recs = [{"prompt": t, "pids": p, "y": e.generate(p, max_new=n_new, chunk=8)} for p, t in seen]
+    with tempfile.TemporaryDirectory() as td:
+        tp = os.path.join(td, "t.bin")
+        DW.save(tp, recs, DW.DraftConfig(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
+        e.load_ildraft(tp)
+    out = {}
+    for label, tree in (("learned_tree16", 15), ("learned_chain8", 0)):
+        passes = acc = 0
+        for p, t in seen[:3]:
+            e.truncate_cache(0)
+            e.set_learned(True, 8, tree)
+            e.set_draft_context(p, t, None)
+            e.reset_out_tokens()
+            e.set_prompt(p)
+            e.set_state(pos=0, n=len(p), maxsteps=n_new, tspec=tree + 1 if tree else 8, learned=1)
+            e.prefill(p)
+            for _ in range(n_new):
+                if e.get_state()["done"]:
+                    break
+                e.spec_pass()
+            st = e.get_state()
+            passes += st["passes"]
+            acc += st["accepted"]
+        out[label] = {"passes": passes, "accepted": acc}
+    e.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +319,8 @@ def main() -> int:
                          "step is its own launch, timed with HIP events around its kernel, and prompts "
                          "are prefilled through 16-row passes (for profilers that do not follow graph "
                          "launches)")
+    ap.add_argument("--spec-single", action="store_true",
+                    help="only run the learned drafter's passes one launch at a time (for kernel traces)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (the reference dispatch "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -288,6 +329,10 @@ def main() -> int:
         print("bench.py: this build runs on one GPU only (the decode step does not shard); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.spec_single:
+        from instantllm_amd import synth, illfile as F
+        print(json.dumps({"spec_single": speculative_single(synth.cached_model(F.FMT_Q4, 2))}), flush=True)
+        return 0
     if args.calib_copy_mib > 0:
         import torch
         n = args.calib_copy_mib << 20

@@ -333,14 +333,14 @@ __device__ __forceinline__ const uint4* t1_abase(const PrepLds<T>& P, int lane) 
 
 // Accumulate 16-row tiles over K = 896: acc[i][j] (rows t = 4*kg + j of the pass, weight
 // row n of tile i) += sum_G s*d*S + m*X. The per-value operation sequence is independent
-// of T. `fetch(i, cb, w, s)` supplies tile i's block cb: 16 weight bytes and the (scale,
-// min) pairs for this lane. The body has no branches, so the compiler can issue every
-// operand read before the first MFMA; rows >= nrows produce values that callers ignore.
-// With NT > 1 (T = 1 only) the tiles share each group's A-operand read and their MFMA
-// chains interleave.
+// of T and of NT. `fetch(i, cb, w, s)` supplies tile i's block cb: 16 weight bytes and the
+// (scale, min) pairs for this lane. The body has no branches, so the compiler can issue
+// every operand read before the first MFMA; rows >= nrows produce values that callers
+// ignore. With NT > 1 the tiles share each group's A-operand and (d, X) reads (LDS reads,
+// not MFMAs, bound these tiles) and their MFMA chains interleave.
 template <int T, int NT, class Fetch>
 __device__ __forceinline__ void q4_tiles896f(Fetch fetch, const PrepLds<T>& P, int lane_, float (*acc)[4]) {
-  static_assert(T == 1 || NT == 1, "interleaved tiles at T = 1 only");
+  static_assert(NT == 1 || NT == 2, "one or two interleaved tiles");
   const int lane = opq(lane_);
   const int kg = lane >> 4, m = arow<T>(lane & 15);
   constexpr int RPL = T >= 4 ? 4 : T;
@@ -380,28 +380,36 @@ __device__ __forceinline__ void q4_tiles896f(Fetch fetch, const PrepLds<T>& P, i
         acc[i][0] = fmaf(mw, dx.y, acc[i][0]);
       }
     } else {
-      const v4i b = gi == 0 ? q4_unpack(wv[0][cb].x, wv[0][cb].y) : q4_unpack(wv[0][cb].z, wv[0][cb].w);
       const uint4 h = P.ahi[(G * 4 + kg) * T + m];
       const uint4 l = P.alo[(G * 4 + kg) * T + m];
       const v4i ah = (v4i){(int)h.x, (int)h.y, (int)h.z, (int)h.w};
       const v4i al = (v4i){(int)l.x, (int)l.y, (int)l.z, (int)l.w};
-      const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
-      const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
-      const uint32_t sm = gi == 0 ? sv[0][cb].x : sv[0][cb].y;
-      const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+      float2 dx[RPL];
 #pragma unroll
-      for (int j = 0; j < RPL; j++) {
-        const float2 dx = P.sc[G * T + arow<T>(4 * kg + j)];
-        const int S = (dh[j] << 8) + dl[j];
-        const float t1 = dx.x * (float)S;
-        acc[0][j] = fmaf(sw, t1, acc[0][j]);
-        acc[0][j] = fmaf(mw, dx.y, acc[0][j]);
+      for (int j = 0; j < RPL; j++) dx[j] = P.sc[G * T + arow<T>(4 * kg + j)];
+#pragma unroll
+      for (int i = 0; i < NT; i++) {
+        const v4i b = gi == 0 ? q4_unpack(wv[i][cb].x, wv[i][cb].y) : q4_unpack(wv[i][cb].z, wv[i][cb].w);
+        const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, b, z, 0, 0, 0);
+        const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, b, z, 0, 0, 0);
+        const uint32_t sm = gi == 0 ? sv[i][cb].x : sv[i][cb].y;
+        const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
+#pragma unroll
+        for (int j = 0; j < RPL; j++) {
+          const int S = (dh[j] << 8) + dl[j];
+          const float t1 = dx[j].x * (float)S;
+          acc[i][j] = fmaf(sw, t1, acc[i][j]);
+          acc[i][j] = fmaf(mw, dx[j].y, acc[i][j]);
+        }
       }
       // At T > 1 each group needs 4 rows of (d, X): pin each group's epilogue to its group
       // and bound the scheduler's read-ahead to two groups, so the operands and MFMA
       // results of a whole tile are not held in registers at once.
 #pragma unroll
-      for (int j = 0; j < RPL; j++) asm volatile("" : "+v"(acc[0][j]));
+      for (int i = 0; i < NT; i++) {
+#pragma unroll
+        for (int j = 0; j < RPL; j++) asm volatile("" : "+v"(acc[i][j]));
+      }
       if (G & 1) __builtin_amdgcn_sched_barrier(0);
     }
   }

@@ -469,22 +469,32 @@ __device__ __forceinline__ bool pub_read(const uint64_t* src, uint32_t tag, int 
   const int rbase = t * (ILL_PUB_Q * 16) + l32 * 16;
   uint32_t v[15];
   // light poll: the word of the row scale, the same address for the half-wave. (Offsets
-  // pass through opq, so every poll issues its loads afresh.)
+  // pass through opq, so every poll issues its loads afresh.) The first full read goes
+  // through the L2 (no sc1): the consumers on one XCD then share one fetch of each line.
+  // A line the L2 held from before the write fails the check (its words carry another
+  // tag, or miss part of it), and every later read is at device scope.
+  bool cached = true;
   const bool alive = wave_wait2([&]() {
     if (!live) return true;
     return pub_ok(__builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(t * (ILL_PUB_Q * 16) + ILL_PUB_LIGHT * 16), 0, ILL_BUF_SC1), tag);
   }, [&]() {
     bool ok = true;
+    ill_v4u q[5];
 #pragma unroll
     for (int j = 0; j < 5; j++) {
-      ill_v4u q = {0u, 0u, 0u, 0u};
+      q[j] = (ill_v4u){0u, 0u, 0u, 0u};
       if (live) {
-        q = __builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(rbase + j * 512), 0, ILL_BUF_SC1);
-        ok &= pub_ok(q, tag);
+        if (cached) q[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(rbase + j * 512), 0, 0);
+        else q[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, opq(rbase + j * 512), 0, ILL_BUF_SC1);
       }
-      v[3 * j] = q[0];
-      v[3 * j + 1] = q[1];
-      v[3 * j + 2] = q[2];
+    }
+    cached = false;
+#pragma unroll
+    for (int j = 0; j < 5; j++) {
+      if (live) ok &= pub_ok(q[j], tag);
+      v[3 * j] = q[j][0];
+      v[3 * j + 1] = q[j][1];
+      v[3 * j + 2] = q[j][2];
     }
     return ok;
   }, ctl, code);
@@ -605,17 +615,17 @@ union PassLds {
 // att_block gives the block of the fused matrix) and every wave 7 row tiles of O's head-h
 // columns. Row tile lt = 2 bw + hf is half hf of block bw (dims d, or d + 32, of the head,
 // d = 16 (block & 1) + n). Wave w computes qkv_nt(w) tiles from qkv_lt0(w):
-//   T = 1: waves 0-3 both halves of blocks 0-3 (q and k: a RoPE pair stays in one lane),
-//          waves 4-7 one half of a v block each, so each SIMD (waves w, w + 4) runs 3 tiles;
-//   T > 1: waves 0-5 both halves of block w.
+// waves 0-3 both halves of blocks 0-3 (q and k: a RoPE pair stays in one lane), waves 4-7
+// one half of a v block each, so each SIMD (waves w, w + 4) runs 3 tiles. (At T > 1 the
+// tiles are bound by their per-group epilogue arithmetic, which this spreads evenly.)
 __device__ __forceinline__ int att_block(int h, int bw) {
   const int g = h / 7;
   return bw < 2 ? 2 * h + bw : (bw < 4 ? 28 + 2 * g + (bw - 2) : 32 + 2 * g + (bw - 4));
 }
 template <int T>
-__device__ __forceinline__ int qkv_nt(int w) { return T == 1 ? (w < 4 ? 2 : 1) : (w < 6 ? 2 : 0); }
+__device__ __forceinline__ int qkv_nt(int w) { return w < 4 ? 2 : 1; }
 template <int T>
-__device__ __forceinline__ int qkv_lt0(int w) { return T == 1 && w >= 4 ? w + 4 : 2 * w; }
+__device__ __forceinline__ int qkv_lt0(int w) { return w >= 4 ? w + 4 : 2 * w; }
 
 template <int T>
 __device__ __forceinline__ void att_stage_qkv(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
@@ -630,11 +640,10 @@ __device__ __forceinline__ void att_stage_qkv(const IllLayerW& L, int h, int w, 
 }
 
 // Attention work is dealt out by slot: slot j holds the shared chunks c = j (mod 8) and the
-// partial pairs numbered j - ns (mod 8). At T = 1 slot j runs on wave (j + 4) % 8, so the
-// shared chunks go first to the waves with one QKV tile; at T > 1 on wave (j + 6) % 8, the
-// waves without QKV tiles first. (The mapping is its own inverse at T = 1.)
+// partial pairs numbered j - ns (mod 8). Slot j runs on wave (j + 4) % 8, so the shared
+// chunks go first to the waves with one QKV tile. (The mapping is its own inverse.)
 template <int T>
-__device__ __forceinline__ int att_slot(int w) { return (w + (T == 1 ? 4 : 2)) & 7; }
+__device__ __forceinline__ int att_slot(int w) { return (w + 4) & 7; }
 
 template <int T>
 __device__ __forceinline__ void att_stage_o(const IllLayerW& L, int h, int w, int lane, uint8_t* stage) {
@@ -1283,20 +1292,32 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
     acc0[0] = accs[0][0];
     acc1[0] = accs[1][0];
     trace_mark(a, ILL_TRL * l + 3);
-  } else if (nt > 0) {
+  } else if (nt == 2) {   // two tiles sharing each group's activation reads
+    float accs[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    q4_tiles896_lds<T, 2>(st, ILL_ST_TILE, A.u.prep, lane, accs);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc0[j] = accs[0][j];
+      acc1[j] = accs[1][j];
+    }
+    trace_mark(a, ILL_TRL * l + 3);
+  } else {
     q4_tile896_lds<T>(st, st + ILL_KST * 1024, A.u.prep, lane, acc0);
-    q4_tile896_lds<T>(st + ILL_ST_TILE, st + ILL_ST_TILE + ILL_KST * 1024, A.u.prep, lane, acc1);
     trace_mark(a, ILL_TRL * l + 3);
   }
-  if (nt == 1) {   // T = 1, one half of a v block: no RoPE
+  if (nt == 1) {   // one half of a v block: no RoPE
     const int dim = d + 32 * hf1;
-    const bool writer = (h % 7) == 0;
-    if (kg == 0) {
-      const uint32_t h0 = f2h_sat(acc0[0] * rs[0] + bias0);
-      A.v[0][dim] = (uint16_t)h0;
+    const bool writer = (h % 7) == 0 && half == 0;   // one workgroup per group writes the V cache
+#pragma unroll
+    for (int j = 0; j < RPL; j++) {
+      const int t = 4 * kg + j;
+      if (t >= nrows) continue;
+      const uint32_t h0 = f2h_sat(acc0[j] * rs[j] + bias0);
+      A.v[t][dim] = (uint16_t)h0;
       if (writer) {
-        uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + pos / 64) * 64 * 64;
-        gst(vb + dim * 64 + (pos & 63), (uint16_t)h0);
+        const int slot = pos + t;
+        uint16_t* vb = a.vt + (((size_t)l * ILL_NKV + g) * (a.maxctx / 64) + slot / 64) * 64 * 64;
+        gst(vb + dim * 64 + (slot & 63), (uint16_t)h0);
       }
     }
   } else if (nt == 2) {

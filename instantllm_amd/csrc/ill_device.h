@@ -361,21 +361,34 @@ __device__ __forceinline__ void q4_tiles896f(Fetch fetch, const PrepLds<T>& P, i
     for (int G = 0; G < 2 * ILL_KST; G++) xa[G] = a1[G * 4 + kg];
     __builtin_amdgcn_sched_barrier(0);
   }
+  // T = 1: every group's MFMA is issued before the group epilogues (which run in group
+  // order), so the products stream through the matrix pipe instead of each one's latency
+  // being waited for in the accumulation chain
+  int S1[T == 1 ? NT : 1][T == 1 ? 2 * ILL_KST : 1];
+  if (T == 1) {
 #pragma unroll
-  for (int G = 0; G < 2 * ILL_KST; G++) {
-    const int cb = G >> 1, gi = G & 1;
-    if (T == 1) {
+    for (int G = 0; G < 2 * ILL_KST; G++) {
+      const int cb = G >> 1, gi = G & 1;
       const uint4 x = xa[G];
       const v4i ax = (v4i){(int)x.x, (int)x.y, (int)x.z, (int)x.w};
-      const float2 dx = P.sc[G];
 #pragma unroll
       for (int i = 0; i < NT; i++) {
         const v4i b = gi == 0 ? q4_unpack(wv[i][cb].x, wv[i][cb].y) : q4_unpack(wv[i][cb].z, wv[i][cb].w);
         const v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, b, z, 0, 0, 0);
+        S1[i][G] = (dd[0] << 8) + dd[1];
+      }
+    }
+  }
+#pragma unroll
+  for (int G = 0; G < 2 * ILL_KST; G++) {
+    const int cb = G >> 1, gi = G & 1;
+    if (T == 1) {
+      const float2 dx = P.sc[G];
+#pragma unroll
+      for (int i = 0; i < NT; i++) {
         const uint32_t sm = gi == 0 ? sv[i][cb].x : sv[i][cb].y;
         const float sw = h2f(sm & 0xffff), mw = h2f(sm >> 16);
-        const int S = (dd[0] << 8) + dd[1];
-        const float t1 = dx.x * (float)S;
+        const float t1 = dx.x * (float)S1[i][G];
         acc[i][0] = fmaf(sw, t1, acc[i][0]);
         acc[i][0] = fmaf(mw, dx.y, acc[i][0]);
       }

@@ -45,13 +45,13 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
 # a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (163,477.6 x 2 + 16,358.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 351_552_922
+# (163,474.2 x 2 + 16,358.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 351_545_920
 # MFMA utilisation of the 16-row verify pass and of the prefill GEMMs, from rocprofv3
 # SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
 MFMA_COUNTERS = {
-    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0105, "int8_TOPs": 45.4},
-    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0104, "int8_TOPs": 48.1},
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0110, "int8_TOPs": 47.4},
+    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0106, "int8_TOPs": 48.9},
     "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.143, "f16_TFLOPs": 360.3},
     "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.109, "f16_TFLOPs": 275.1},
     "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.042, "f16_TFLOPs": 105.3},

@@ -1344,9 +1344,13 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   // r >= 2.3 (16 rows with a drafted tree). Level 0 is the configured shape, kept while
   // r >= 2.4 over the last few passes at that level; level 1 a 4-row chain (3 drafts), back
   // to level 0 at r >= 2.2, kept at r >= 1.6; level 2 one-row passes without drafts (a
-  // decode step's cost), left for a 4-row probe after 16 passes. Passes at a level only
-  // count toward its own rate.
-  int level = 0, level_p0 = 0;
+  // decode step's cost), left for a 4-row probe after `probe_gap` passes. Passes at a level
+  // only count toward its own rate. A level is judged after two of its passes, or after one
+  // when it accepted no draft at all, and the configured shape falls straight to one-row
+  // passes when fewer than one draft per pass is accepted; every probe that fails doubles
+  // the gap to the next (16 .. 128 passes), a probe that pays resets it.
+  int level = 0, level_p0 = 0, probe_gap = 16;
+  bool probing = false;
   std::vector<std::pair<int, int>> hist;
   auto shape_of = [&](int lv) -> std::pair<int, int> {
     if (lv == 0) return std::pair<int, int>(rows, treeb);
@@ -1357,12 +1361,14 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     if (!adaptive) return 0;
     const int p = ((volatile int32_t*)e->spec_host)[0], a = ((volatile int32_t*)e->spec_host)[1];
     if (hist.empty() || hist.back().first != p) hist.emplace_back(p, a);
-    if (level == 2) return p - level_p0 >= 16 ? 1 : 2;
-    if (hist.size() < 3) return level;
-    const auto& first = hist[hist.size() >= 4 ? hist.size() - 4 : 0];
-    if (p - first.first < 2) return level;
-    const double rate = (double)(a - first.second) / (double)(p - first.first);
-    if (level == 0) return rate >= 2.4 ? 0 : (rows > 4 ? 1 : (rate >= 1.6 ? 0 : 2));
+    if (level == 2) return p - level_p0 >= probe_gap ? 1 : 2;
+    if (hist.size() < 2) return level;
+    const auto& first = hist[hist.size() >= 5 ? hist.size() - 5 : 0];
+    const int np = p - first.first;
+    if (np < 1) return level;
+    const double rate = (double)(a - first.second) / (double)np;
+    if (np < 2 && rate > 0.0) return level;
+    if (level == 0) return rate >= 2.4 ? 0 : (rows > 4 && rate >= 1.0 ? 1 : (rate >= 1.6 ? 0 : 2));
     return rate >= 2.2 ? 0 : (rate >= 1.6 ? 1 : 2);
   };
   int cur_rows = rows;
@@ -1377,6 +1383,11 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
     if (encoded < max_new && (!graphs || encoded - (sp[0] - 1) <= chunk)) {
       const int lv = next_level();
       if (lv != level) {
+        if (level == 2 && lv == 1) probing = true;
+        else if (probing) {   // the probe's verdict
+          probe_gap = lv == 2 ? std::min(2 * probe_gap, 128) : 16;
+          probing = false;
+        }
         level = lv;
         level_p0 = sp[0];
         hist.clear();

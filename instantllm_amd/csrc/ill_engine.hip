@@ -1045,6 +1045,17 @@ int launch_spec_graph(ill_engine* e, int T, int npasses) {
   HCK(hipGraphLaunch(g.x, e->stream));
   return 0;
 }
+
+// one pass of generate_spec on the T-row instantiation and its drafting, launched directly
+// (a pass after a change of shape, or one of a shape not yet judged)
+int launch_spec_one(ill_engine* e, int T) {
+  if (int rc = set_wlog(e, 0)) return rc;
+  if (int rc = count_passes(e, 1)) return rc;
+  enqueue_pass(e, T);
+  enqueue_draft(e);
+  HCK(hipGetLastError());
+  return 0;
+}
 }  // namespace
 
 int ill_capture_steps(ill_engine* e, int nsteps) {
@@ -1342,46 +1353,57 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   // 800 us for 4 and 860 us for 16, plus the drafting, up to 250 us for a learned tree): a
   // pass of 1 + r tokens beats plain decoding when r >= 1.6 accepted drafts (4 rows) or
   // r >= 2.3 (16 rows with a drafted tree). Level 0 is the configured shape, kept while
-  // r >= 2.4 over the last few passes at that level; level 1 a 4-row chain (3 drafts), back
+  // r >= 2.4 over the last four passes of that shape; level 1 a 4-row chain (3 drafts), back
   // to level 0 at r >= 2.2, kept at r >= 1.6; level 2 one-row passes without drafts (a
-  // decode step's cost), left for a 4-row probe after `probe_gap` passes. Passes at a level
-  // only count toward its own rate. A level is judged after two of its passes, or after one
-  // when it accepted no draft at all, and the configured shape falls straight to one-row
-  // passes when fewer than one draft per pass is accepted; every probe that fails doubles
-  // the gap to the next (16 .. 128 passes), a probe that pays resets it.
-  int level = 0, level_p0 = 0, probe_gap = 16;
+  // decode step's cost), left for a 4-row probe after `probe_gap` passes. A level is judged
+  // on the passes that hold rows drafted at its shape: after two of them, or after one that
+  // accepted no draft, and at most two of them are in flight before that verdict. The
+  // configured shape falls straight to one-row passes when fewer than one draft per pass is
+  // accepted; every probe that fails doubles the gap to the next (16 .. 128 passes), a probe
+  // that pays resets it. A pass holds the rows drafted after the pass before it, so the pass
+  // after a change of shape runs on the instantiation of the previous shape, the rest on
+  // their own.
+  int level = 0, probe_gap = 16;
   bool probing = false;
-  std::vector<std::pair<int, int>> hist;
-  auto shape_of = [&](int lv) -> std::pair<int, int> {
-    if (lv == 0) return std::pair<int, int>(rows, treeb);
-    if (lv == 1) return std::pair<int, int>(std::min(rows, 4), 0);
-    return std::pair<int, int>(1, 0);
+  int lv_first = 0;         // the first pass holding rows drafted at this level's shape
+  std::vector<int> samp;    // samp[d]: accepted drafts once d passes after the prefill committed
+  int encoded = 0;          // passes enqueued after the prefill
+  volatile const int32_t* ot = e->out_host;
+  volatile const int32_t* sp = e->spec_host;
+  // passes committed after the prefill (-1 before the prompt's commit), with the accepted
+  // count read first: the commit stores it after the pass count, so a pairing is at worst
+  // stale, and refreshed by the next read while the pass count stands
+  auto observe = [&]() -> int {
+    const int acc = sp[1];
+    const int d = sp[0] - 1;
+    if (d < 0) return -1;
+    if ((int)samp.size() <= d) samp.resize(d + 1, acc);
+    samp[d] = acc;
+    return d;
   };
-  auto next_level = [&]() -> int {
+  // the level for the next pass and whether its shape has been judged
+  auto next_level = [&](int done, bool& judged) -> int {
+    judged = true;
     if (!adaptive) return 0;
-    const int p = ((volatile int32_t*)e->spec_host)[0], a = ((volatile int32_t*)e->spec_host)[1];
-    if (hist.empty() || hist.back().first != p) hist.emplace_back(p, a);
-    if (level == 2) return p - level_p0 >= probe_gap ? 1 : 2;
-    if (hist.size() < 2) return level;
-    const auto& first = hist[hist.size() >= 5 ? hist.size() - 5 : 0];
-    const int np = p - first.first;
-    if (np < 1) return level;
-    const double rate = (double)(a - first.second) / (double)np;
-    if (np < 2 && rate > 0.0) return level;
+    if (level == 2) return encoded - lv_first >= probe_gap ? 1 : 2;
+    const int n = done - lv_first;
+    judged = n >= 2 || (n == 1 && samp[done] == samp[lv_first]);
+    if (!judged) return level;
+    const int d0 = std::max(lv_first, done - 4);
+    const double rate = (double)(samp[done] - samp[d0]) / (double)(done - d0);
     if (level == 0) return rate >= 2.4 ? 0 : (rows > 4 && rate >= 1.0 ? 1 : (rate >= 1.6 ? 0 : 2));
     return rate >= 2.2 ? 0 : (rate >= 1.6 ? 1 : 2);
   };
   int cur_rows = rows;
-  int drafted_rows = rows;   // the most rows a pending pass can hold (the prompt's commit drafted it)
-  volatile const int32_t* ot = e->out_host;
-  volatile const int32_t* sp = e->spec_host;
-  int got = 0, encoded = 0;   // tokens read, passes enqueued after the prefill
-  bool stopped = false;
-  while (!stopped && got < max_new) {
+  int drafted_rows = rows;   // the most rows the next pass can hold (the prompt's commit drafted it)
+  int got = 0;   // tokens read
+  while (got < max_new) {
+    const int done = observe();
     // keep at most one chunk of passes ahead of the committed ones (Engine.swift:991-1008);
     // every pass commits at least one token, so max_new passes always suffice
-    if (encoded < max_new && (!graphs || encoded - (sp[0] - 1) <= chunk)) {
-      const int lv = next_level();
+    if (encoded < max_new && encoded - done <= chunk) {
+      bool judged;
+      const int lv = next_level(done, judged);
       if (lv != level) {
         if (level == 2 && lv == 1) probing = true;
         else if (probing) {   // the probe's verdict
@@ -1389,32 +1411,37 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
           probing = false;
         }
         level = lv;
-        level_p0 = sp[0];
-        hist.clear();
+        lv_first = encoded + 1;
+        judged = level == 2;
+        const int want_rows = level == 0 ? rows : (level == 1 ? std::min(rows, 4) : 1);
+        const int want_tree = level == 0 ? treeb : 0;
+        if (want_rows != cur_rows || want_tree != cur_tree) {   // ordered after the passes before it
+          cur_rows = want_rows;
+          cur_tree = want_tree;
+          HCK(hipMemcpyAsync(&e->st->tspec, &cur_rows, 4, hipMemcpyHostToDevice, e->stream));
+          HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
+        }
       }
-      const std::pair<int, int> want = shape_of(level);
-      if (want.first != cur_rows || want.second != cur_tree) {   // ordered after the passes before it
-        cur_rows = want.first;
-        cur_tree = want.second;
-        HCK(hipMemcpyAsync(&e->st->tspec, &cur_rows, 4, hipMemcpyHostToDevice, e->stream));
-        HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
-      }
-      if (graphs) {
-        // the first pass of this launch holds what the previous launch drafted (under the
-        // rows then in effect); its later passes hold cur_rows
-        const int T = pass_T(std::max(drafted_rows, cur_rows));
+      // an unjudged shape has at most two of its passes in flight
+      if (judged || encoded < lv_first + 2) {
+        if (!graphs) {
+          if ((rc = ill_spec_pass(e, 0))) return rc;   // host-sized pass (layer-by-layer path)
+          encoded++;
+        } else if (pass_T(drafted_rows) != pass_T(cur_rows) || !judged) {
+          if ((rc = launch_spec_one(e, pass_T(drafted_rows)))) return rc;
+          encoded++;
+        } else {
+          if ((rc = launch_spec_graph(e, pass_T(cur_rows), chunk))) return rc;
+          encoded += chunk;
+        }
         drafted_rows = cur_rows;
-        if ((rc = launch_spec_graph(e, T, chunk))) return rc;
-        encoded += chunk;
         continue;
       }
-      if ((rc = ill_spec_pass(e, 0))) return rc;   // host-sized pass (layer-by-layer path)
-      encoded++;
     }
     const int t = ot[got];
     if (t < 0) {
       // an idle stream with no new token: the device stopped (or every pass is spent)
-      if (hipStreamQuery(e->stream) == hipSuccess && ot[got] < 0) {
+      if (hipStreamQuery(e->stream) == hipSuccess && ot[got] < 0 && observe() == done) {
         IllState st;
         if ((rc = check_err(e)) || (rc = read_state(e, &st))) return rc;
         if (st.done || encoded >= max_new) break;

@@ -234,6 +234,36 @@ __device__ __forceinline__ uint32_t ild_fkey(float s) {
 __device__ __forceinline__ float ild_logf(float x) { return (float)log((double)x); }
 __device__ __forceinline__ float ild_expf(float x) { return (float)exp((double)x); }
 
+// The next pass's rows, tree and control block from the drafted rows (one thread).
+__device__ __forceinline__ void ild_next_pass(const IllPassArgs& a, const IldLds& S, int treeB) {
+  IllCtl* c = a.ctl;
+  int rows;
+  if (treeB > 0) {
+    rows = S.rows;
+    a.tree[0] = rows;
+    for (int i = 0; i < rows; ++i) {
+      a.tree[ILL_TR_DEPTH + i] = S.tr_dep[i];
+      a.tree[ILL_TR_PARENT + i] = i == 0 ? -1 : S.tr_par[i];
+      a.tree[ILL_TR_TOK + i] = S.tr_tok[i];
+      a.tree[ILL_TR_ANC + i] = (int)S.tr_anc[i];
+      a.ptoks[i] = S.tr_tok[i];
+    }
+    c->mode = ILL_MODE_TREE;
+  } else {
+    rows = 1 + S.nd;
+    for (int i = 0; i < rows; ++i) a.ptoks[i] = S.next_rows[i];
+    c->mode = ILL_MODE_ROWS;
+  }
+  a.st->n = rows;
+  a.st->nver = rows;
+  a.st->tree = treeB > 0 ? 1 : 0;
+  c->nrows = rows;
+  c->lmh_row0 = 0;
+  c->lmh_rows = rows;
+  c->commit = 2;
+  c->draft = 0;
+}
+
 __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a, IllDraftArgs d) {
   __shared__ IldLds S;
   __shared__ int go0, have, w0, base, T, K, treeB, first_out, last, eos0, eos1;
@@ -256,6 +286,19 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
   }
   __syncthreads();
   if (!go0) return;
+  if (K == 0) {   // nothing to draft: the next pass is the one row `last` (nothing to stage)
+    if (tid == 0) {
+      S.rows = 1;
+      S.nd = 0;
+      S.tr_par[0] = -1;
+      S.tr_tok[0] = last;
+      S.tr_dep[0] = 0;
+      S.tr_anc[0] = 1u;
+      S.next_rows[0] = last;
+      ild_next_pass(a, S, treeB);
+    }
+    return;
+  }
   // stage the request and the scorer
   {
     const int4* src = (const int4*)d.req;
@@ -777,33 +820,5 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     }
   }
   __syncthreads();
-  // ---- the next pass: rows, tree and control block ----
-  if (tid == 0) {
-    IllCtl* c = a.ctl;
-    int rows;
-    if (treeB > 0) {
-      rows = S.rows;
-      a.tree[0] = rows;
-      for (int i = 0; i < rows; ++i) {
-        a.tree[ILL_TR_DEPTH + i] = S.tr_dep[i];
-        a.tree[ILL_TR_PARENT + i] = i == 0 ? -1 : S.tr_par[i];
-        a.tree[ILL_TR_TOK + i] = S.tr_tok[i];
-        a.tree[ILL_TR_ANC + i] = (int)S.tr_anc[i];
-        a.ptoks[i] = S.tr_tok[i];
-      }
-      c->mode = ILL_MODE_TREE;
-    } else {
-      rows = 1 + S.nd;
-      for (int i = 0; i < rows; ++i) a.ptoks[i] = S.next_rows[i];
-      c->mode = ILL_MODE_ROWS;
-    }
-    a.st->n = rows;
-    a.st->nver = rows;
-    a.st->tree = treeB > 0 ? 1 : 0;
-    c->nrows = rows;
-    c->lmh_row0 = 0;
-    c->lmh_rows = rows;
-    c->commit = 2;
-    c->draft = 0;
-  }
+  if (tid == 0) ild_next_pass(a, S, treeB);
 }

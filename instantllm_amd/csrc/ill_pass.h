@@ -1882,18 +1882,20 @@ __device__ __forceinline__ uint32_t wg_max_u32(uint32_t v, uint32_t* slots) {
 __device__ __forceinline__ void spec_draft(const IllPassArgs& a, int have, int last, int tspec, int nodraft, int eos0, int eos1,
                                            DraftLds& D) {
   const int i = threadIdx.x;
-  const int w0 = have > ILL_OB_MAX ? have - ILL_OB_MAX : 0;
-  for (int k = w0 + i; k < have; k += ILL_WG_THREADS) D.ob[k - w0] = gld(a.out_dev + k);
-  const int np = a.prompt ? min(max(gld(a.prompt), 0), ILL_OB_MAX) : 0;
-  if (i == 0) {
-    D.L = have - w0;
-    D.len = 0;
-    for (int k = ILL_NG_MAXN; k >= 1; k--) D.hist[D.len++] = have - k >= 0 ? gld(a.out_dev + have - k) : -1;
-    D.nd = 0;
-  }
-  __syncthreads();
   const int T = min(max(tspec, 1), ILL_MAXT);
   const int maxd = nodraft ? 0 : T - 1;
+  if (i == 0) D.nd = 0;
+  const int w0 = have > ILL_OB_MAX ? have - ILL_OB_MAX : 0;
+  const int np = a.prompt && maxd > 0 ? min(max(gld(a.prompt), 0), ILL_OB_MAX) : 0;
+  if (maxd > 0) {   // the window and the n-gram history (nothing to stage for a 1-row pass)
+    for (int k = w0 + i; k < have; k += ILL_WG_THREADS) D.ob[k - w0] = gld(a.out_dev + k);
+    if (i == 0) {
+      D.L = have - w0;
+      D.len = 0;
+      for (int k = ILL_NG_MAXN; k >= 1; k--) D.hist[D.len++] = have - k >= 0 ? gld(a.out_dev + have - k) : -1;
+    }
+    __syncthreads();
+  }
   for (int nd = 0; nd < maxd; nd++) {
     const int L = D.L;
     // 1. self-repetition: position j (1 <= j <= L - 1) continues a match of m >= 3 tokens

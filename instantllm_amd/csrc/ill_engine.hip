@@ -1362,7 +1362,7 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   // accepted; every probe that fails doubles the gap to the next (16 .. 128 passes), a probe
   // that pays resets it. A pass holds the rows drafted after the pass before it, so the pass
   // after a change of shape runs on the instantiation of the previous shape, the rest on
-  // their own.
+  // their own; a change to one-row passes cuts that pass to its first row instead.
   int level = 0, probe_gap = 16;
   bool probing = false;
   int lv_first = 0;         // the first pass holding rows drafted at this level's shape
@@ -1420,6 +1420,11 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
           cur_tree = want_tree;
           HCK(hipMemcpyAsync(&e->st->tspec, &cur_rows, 4, hipMemcpyHostToDevice, e->stream));
           HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
+        }
+        if (level == 2 && drafted_rows > 1) {   // the pending pass, cut to its first row
+          hipLaunchKernelGGL(ill_trunc_kernel, dim3(1), dim3(64), 0, e->stream, e->args);
+          HCK(hipGetLastError());
+          drafted_rows = 1;
         }
       }
       // an unjudged shape has at most two of its passes in flight

@@ -1999,6 +1999,25 @@ __global__ __launch_bounds__(ILL_WG_THREADS) void ill_draft_kernel(IllPassArgs a
   spec_draft(a, have, last, tspec, nodraft, eos0, eos1, D);
 }
 
+// Cuts the drafted pass pending after a speculative commit to its first row, the last
+// committed token (never a draft), so that the pass commits one token, as greedy decoding
+// would, on the 1-row instantiation. A stopped request, or one whose drafting is still to
+// run, is left as it is.
+__global__ __launch_bounds__(64) void ill_trunc_kernel(IllPassArgs a) {
+  if (threadIdx.x != 0) return;
+  IllCtl* c = a.ctl;
+  IllState* st = a.st;
+  if (c->commit != 2 || c->draft || st->done) return;
+  a.ptoks[0] = c->last_tok;
+  st->n = 1;
+  st->nver = 1;
+  st->tree = 0;
+  c->mode = ILL_MODE_ROWS;
+  c->nrows = 1;
+  c->lmh_row0 = 0;
+  c->lmh_rows = 1;
+}
+
 // Commit of the pass's argmaxes C.g[t] (rows lmh0 ..): token record, State advance, stop
 // test, chain / tree accept walk and KV compaction (Shaders.swift:192-244, :246-418). The
 // pass kernel also advances the epoch and its accumulator-bank bookkeeping. The State is

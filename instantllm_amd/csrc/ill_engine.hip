@@ -1357,7 +1357,7 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   // to level 0 at r >= 2.2, kept at r >= 1.6; level 2 one-row passes without drafts (a
   // decode step's cost), left for a 4-row probe after `probe_gap` passes. A level is judged
   // on the passes that hold rows drafted at its shape: after two of them, or after one that
-  // accepted no draft, and at most two of them are in flight before that verdict. The
+  // accepted no draft, and at most one of them is in flight before that verdict. The
   // configured shape falls straight to one-row passes when fewer than one draft per pass is
   // accepted; every probe that fails doubles the gap to the next (16 .. 128 passes), a probe
   // that pays resets it. A pass holds the rows drafted after the pass before it, so the pass
@@ -1427,8 +1427,9 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
           drafted_rows = 1;
         }
       }
-      // an unjudged shape has at most two of its passes in flight
-      if (judged || encoded < lv_first + 2) {
+      // an unjudged shape has at most one of its passes in flight (the host sees a commit
+      // while its drafting still runs, and launches the next pass behind it)
+      if (judged || encoded <= std::max(done, lv_first)) {
         if (!graphs) {
           if ((rc = ill_spec_pass(e, 0))) return rc;   // host-sized pass (layer-by-layer path)
           encoded++;

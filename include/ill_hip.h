@@ -129,11 +129,15 @@ int ill_capture_spec(ill_engine* e, int npasses);
 
 /* Engine.generate with speculation on (Engine.swift:922-1038): prefill, then verify passes
  * of up to `rows` (2..16) rows, in captured graphs of `chunk` passes for q4 models (one
- * launch per pass otherwise), while polling out_tokens. adaptive != 0 chooses each launch's
+ * launch per pass otherwise), while polling out_tokens. adaptive != 0 chooses each pass's
  * shape from the accepted drafts per pass (Engine.nextPassShape, :888-898, with thresholds
  * from this engine's pass costs, which grow with the kernel's row count): the configured
  * shape while at least 2.4 are accepted, 4-row chains while at least 1.6 are (back to the
- * configured shape at 2.2), else one-row passes with a 4-row probe every 16 passes.
+ * configured shape at 2.2), else one-row passes with a 4-row probe after 16 passes (the
+ * gap doubles, up to 128, after each probe that fails). A shape is judged on its own
+ * passes, after two of them (one that accepted nothing), with one of them in flight at a
+ * time until then; a change to one-row passes cuts the pending drafted pass to its first
+ * row. The tokens are those of greedy decoding in every case.
  * out / n_out as for ill_generate; stats (optional, [2]) receives the passes and accepted
  * drafts of the request. */
 int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new, int rows, int chunk, int adaptive,
@@ -171,8 +175,8 @@ int ill_set_draft_context(ill_engine* e, const int32_t* prompt, int n, const cha
 /* Engine.useLearned / learnedT / learnedTree (Engine.swift:871-880): use != 0 lets a
  * prepared context switch ill_generate_spec to the learned drafter; its passes are chains
  * of chain_rows (2..16) rows, or with tree_budget > 0 trees of min(tree_budget, 15) drafts
- * (passes of that + 1 rows; adaptive generation falls back to 8-row chains while fewer than
- * 1.5 drafts per pass are accepted). Defaults 1, 8, 15. */
+ * (passes of that + 1 rows; with ill_generate_spec's `adaptive` these are its configured
+ * shape). Defaults 1, 8, 15. */
 int ill_set_learned(ill_engine* e, int use, int chain_rows, int tree_budget);
 
 /* The pass the last speculative commit set up (no reference counterpart: inspection for

@@ -111,9 +111,12 @@ __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
   H.accepted = st->accepted;
   H.tspec = st->tspec;
   H.nodraft = st->nodraft;
-  H.epoch = c->epoch;
-  H.bank = c->epoch & 1;
-  H.zrows = c->bank_rows[(c->epoch & 1) ^ 1];
+  // every load's address is known before any value arrives (one round trip): both
+  // banks' row counts, all 16 row tokens and tree entries are loaded and then selected
+  const int ep = c->epoch, br0 = c->bank_rows[0], br1 = c->bank_rows[1];
+  H.epoch = ep;
+  H.bank = ep & 1;
+  H.zrows = (ep & 1) ? br0 : br1;
   H.mode = c->mode;
   H.nrows = c->nrows;
   H.pos = st->pos;
@@ -121,11 +124,19 @@ __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
   H.lmhn = c->lmh_rows;
   H.wlog = c->write_logits;
   H.commit = c->commit;
+  int pt[16], td[16], tp[16];   // ptoks holds 16 rows, tree ILL_TR_INTS entries
+#pragma unroll
   for (int t = 0; t < 16; t++) {
-    H.tok[t] = t < H.nrows ? a.ptoks[t] : 0;
+    pt[t] = a.ptoks[t];
+    td[t] = a.tree[ILL_TR_DEPTH + t];
+    tp[t] = a.tree[ILL_TR_PARENT + t];
+  }
+#pragma unroll
+  for (int t = 0; t < 16; t++) {
+    H.tok[t] = t < H.nrows ? pt[t] : 0;
     if (H.mode == ILL_MODE_TREE) {
-      H.depth[t] = t < H.nrows ? a.tree[ILL_TR_DEPTH + t] : 0;
-      H.parent[t] = t < H.nrows ? a.tree[ILL_TR_PARENT + t] : 0;
+      H.depth[t] = t < H.nrows ? td[t] : 0;
+      H.parent[t] = t < H.nrows ? tp[t] : 0;
     } else {
       H.depth[t] = t;
       H.parent[t] = t > 0 ? t - 1 : 0;

@@ -222,7 +222,7 @@ def speculative(path: str, n_new: int = 96) -> dict:
                    "tok/s from the host clock over whole generate calls"}
     with tempfile.TemporaryDirectory() as td:
         tp = os.path.join(td, "t.bin")
-        DW.save(tp, recs, DW.DraftConfig(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
+        DW.save(tp, recs, DW.TableSpec(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
         e.load_ildraft(tp)
 
     def timed(fn):
@@ -278,7 +278,7 @@ def speculative_single(path: str, n_new: int = 96) -> dict:
     recs = [{"prompt": t, "pids": p, "y": e.generate(p, max_new=n_new, chunk=8)} for p, t in seen]
     with tempfile.TemporaryDirectory() as td:
         tp = os.path.join(td, "t.bin")
-        DW.save(tp, recs, DW.DraftConfig(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
+        DW.save(tp, recs, DW.TableSpec(), DW.random_scorer(16, seed=5, emphasis={1: 3.0, 2: 1.5, 17: 2.0, 20: 1.0, 23: 1.5}), {})
         e.load_ildraft(tp)
     out = {}
     for label, tree in (("learned_tree16", 15), ("learned_chain8", 0)):

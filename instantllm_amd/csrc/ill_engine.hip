@@ -123,6 +123,7 @@ struct ill_engine {
   int32_t* out_dev = nullptr;
   int32_t* out_host = nullptr;
   int32_t* spec_host = nullptr;   // pinned [2]: passes, accepted drafts (written by spec commits)
+  int32_t* stop_host = nullptr;   // pinned, host-coherent: the stop request read by each commit
   int32_t* prompt = nullptr;      // [4 + 256]: prompt-lookup context of the drafter
   uint8_t* ngram = nullptr;       // n-gram draft table (ILL_NG_SLOTS x 16 B), optional
   // learned drafter (ILDraft.swift): host table, device copies, per-request context
@@ -699,9 +700,11 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   if (hipMemcpy(e->dolayers, e->holayers.data(), sizeof(OpLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "layer table upload failed"));
   if (hipHostMalloc((void**)&e->out_host, (size_t)max_steps * 4, hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&e->spec_host, 2 * 4, hipHostMallocDefault) != hipSuccess)
+      hipHostMalloc((void**)&e->spec_host, 2 * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&e->stop_host, 4, hipHostMallocCoherent) != hipSuccess)
     return cleanup(fail(ILL_E_HIP, "pinned token buffer allocation failed"));
   e->spec_host[0] = e->spec_host[1] = 0;
+  *(volatile int32_t*)e->stop_host = 0;
   if (!dalloc((void**)&e->prompt, (4 + ILL_OB_MAX) * 4)) return cleanup(fail(ILL_E_HIP, "prompt buffer allocation failed"));
   for (int i = 0; i < max_steps; i++) e->out_host[i] = -1;
   if (hipMemcpy(e->dlayers, e->hlayers.data(), sizeof(IllLayerW) * layers, hipMemcpyHostToDevice) != hipSuccess)
@@ -750,6 +753,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   a.out_dev = e->out_dev;
   a.out_host = e->out_host;
   a.spec_host = e->spec_host;
+  a.stop_host = e->stop_host;
   a.prompt = e->prompt;
   a.ngram = nullptr;
   a.maxctx = e->maxctx;
@@ -784,6 +788,7 @@ int ill_destroy(ill_engine* e) {
     if (p) hipFree(p);
   if (e->out_host) hipHostFree(e->out_host);
   if (e->spec_host) hipHostFree(e->spec_host);
+  if (e->stop_host) hipHostFree(e->stop_host);
   if (e->prompt) hipFree(e->prompt);
   if (e->ngram) hipFree(e->ngram);
   delete e->ild;
@@ -818,8 +823,16 @@ int ill_set_state(ill_engine* e, const int32_t state[16]) {
   const int32_t tb = s.learned && e->learned_tree > 0 ? std::min(e->learned_tree, ILL_MAXT - 1) : 0;
   HCK(hipMemcpyAsync(&e->ctl->tree_b, &tb, 4, hipMemcpyHostToDevice, e->stream));
   HCK(hipStreamSynchronize(e->stream));
+  // a new State starts a new request: the device is idle, so no commit reads the word now
+  __atomic_store_n(e->stop_host, 0, __ATOMIC_SEQ_CST);
   e->pos_hint = s.pos;
   e->learned_active = s.learned != 0;
+  return ILL_OK;
+}
+
+int ill_stop(ill_engine* e) {
+  if (!e) return fail(ILL_E_ARG, "null engine");
+  __atomic_store_n(e->stop_host, 1, __ATOMIC_SEQ_CST);
   return ILL_OK;
 }
 
@@ -947,6 +960,14 @@ int ill_load_ngram(ill_engine* e, const void* table, int64_t bytes) {
     e->ngram = nullptr;
   } else {
     if (bytes != (int64_t)ILL_NG_SLOTS * 16) return fail(ILL_E_ARG, "n-gram table of %lld bytes (expected %d)", (long long)bytes, ILL_NG_SLOTS * 16);
+    // every occupied slot {u64 key, i32 next, u16 count, u16 total} must name a token of
+    // this model's vocabulary: the drafter embeds it in the next pass
+    const uint32_t* sl = (const uint32_t*)table;
+    for (int i = 0; i < ILL_NG_SLOTS; i++) {
+      const uint32_t* q = sl + 4 * i;
+      if ((q[0] | q[1]) && (int32_t)q[2] >= 0 && (int32_t)q[2] < e->vocab) continue;
+      if (q[0] | q[1]) return fail(ILL_E_ARG, "n-gram slot %d: next token %d outside the vocabulary", i, (int32_t)q[2]);
+    }
     if (!e->ngram) HCK(hipMalloc((void**)&e->ngram, (size_t)bytes));
     HCK(hipMemcpy(e->ngram, table, (size_t)bytes, hipMemcpyHostToDevice));
   }
@@ -959,6 +980,8 @@ int ill_set_prompt(ill_engine* e, const int32_t* toks, int n) {
   if (!e || (n > 0 && !toks) || n < 0) return fail(ILL_E_ARG, "bad prompt");
   int32_t buf[4 + ILL_OB_MAX] = {0};
   const int np = n < ILL_OB_MAX ? n : ILL_OB_MAX;
+  for (int i = n - np; i < n; i++)   // the drafter proposes these tokens
+    if (toks[i] < 0 || toks[i] >= e->vocab) return fail(ILL_E_ARG, "prompt token %d out of range", toks[i]);
   buf[0] = np;
   for (int i = 0; i < np; i++) buf[4 + i] = toks[n - np + i];
   HCK(hipMemcpyAsync(e->prompt, buf, sizeof buf, hipMemcpyHostToDevice, e->stream));
@@ -1261,6 +1284,11 @@ int ill_load_prefix(ill_engine* e, const char* path, int32_t* toks, int max_toks
 }
 
 int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk, int32_t* out, int* n_out, float* logits_out) {
+  return ill_generate_cb(e, toks, ntok, max_new, chunk, out, n_out, logits_out, nullptr, nullptr);
+}
+
+int ill_generate_cb(ill_engine* e, const int32_t* toks, int ntok, int max_new, int chunk, int32_t* out, int* n_out,
+                    float* logits_out, ill_token_fn on_token, void* user) {
   if (!e || !toks || ntok < 1 || max_new < 1 || !out || !n_out) return fail(ILL_E_ARG, "bad generate arguments");
   if (max_new > e->maxsteps) return fail(ILL_E_ARG, "max_new %d > max_steps %d", max_new, e->maxsteps);
   // Engine.swift:934 (tokens + maxNew <= maxContext), with the 16-slot margin of a pass
@@ -1306,6 +1334,12 @@ int ill_generate(ill_engine* e, const int32_t* toks, int ntok, int max_new, int 
     got++;
     if (t == 151645 || t == 151643) break;
     out[(*n_out)++] = t;
+    if (on_token && !on_token(t, user)) {
+      // Engine.swift:1021-1036: the caller stopped the request; steps still queued leave
+      // at once (the next commit reads the stop word and sets the State's done flag)
+      stopped = true;
+      if (got < encoded) ill_stop(e);
+    }
   }
   HCK(hipStreamSynchronize(e->stream));
   if ((rc = check_err(e))) return rc;
@@ -1512,20 +1546,32 @@ int ill_load_ildraft(ill_engine* e, const char* path) {
     delete t;
     return fail(ILL_E_FILE, "%s", err.c_str());
   }
-  HCK(hipStreamSynchronize(e->stream));
-  if (e->dtab) HCK(hipFree(e->dtab));
+  // the new table goes into buffers of its own first: on any failure the engine keeps no
+  // drafter (never a pointer to freed memory) and the new table is released
+  uint8_t* tab = nullptr;
+  int rc = ILL_OK;
+  if (hipStreamSynchronize(e->stream) != hipSuccess || hipMalloc((void**)&tab, t->blob.size()) != hipSuccess ||
+      hipMemcpy(tab, t->blob.data(), t->blob.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      (!e->dtflg && hipMalloc((void**)&e->dtflg, ILD_VOCAB) != hipSuccess) ||
+      hipMemcpy(e->dtflg, t->tflg.data(), ILD_VOCAB, hipMemcpyHostToDevice) != hipSuccess ||
+      (!e->dreq && hipMalloc((void**)&e->dreq, sizeof(IllDraftReq)) != hipSuccess) ||
+      hipMemset(e->dreq, 0, sizeof(IllDraftReq)) != hipSuccess)
+    rc = fail(ILL_E_HIP, "learned drafter table upload failed");
+  drop_graph(e);   // captured drafting kernels hold the old table's pointers
+  if (e->dtab) (void)hipFree(e->dtab);
   e->dtab = nullptr;
-  HCK(hipMalloc((void**)&e->dtab, t->blob.size()));
-  HCK(hipMemcpy(e->dtab, t->blob.data(), t->blob.size(), hipMemcpyHostToDevice));
-  if (!e->dtflg) HCK(hipMalloc((void**)&e->dtflg, ILD_VOCAB));
-  HCK(hipMemcpy(e->dtflg, t->tflg.data(), ILD_VOCAB, hipMemcpyHostToDevice));
-  if (!e->dreq) HCK(hipMalloc((void**)&e->dreq, sizeof(IllDraftReq)));
-  HCK(hipMemset(e->dreq, 0, sizeof(IllDraftReq)));
   delete e->ild;
+  e->ild = nullptr;
+  e->dargs = IllDraftArgs{};
+  e->draft_ctx_ready = false;
+  if (rc != ILL_OK) {
+    if (tab) (void)hipFree(tab);
+    delete t;
+    return rc;
+  }
+  e->dtab = tab;
   e->ild = t;
   e->dargs = illd::device_args(*t, e->dtab, e->dtflg, e->dreq);
-  e->draft_ctx_ready = false;
-  drop_graph(e);   // captured drafting kernels hold the old table's pointers
   return ILL_OK;
 }
 

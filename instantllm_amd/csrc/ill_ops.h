@@ -1253,6 +1253,8 @@ __global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a
   __syncthreads();
   if (H.done) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  int stopreq = 0;   // the host's stop word (see ill_pass_kernel), waited for at the commit
+  if (tid == 0 && a.stop_host) stopreq = __hip_atomic_load((const GAS int32_t*)a.stop_host, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   for (int t = H.lmh0; t < H.lmh0 + H.lmhn; t++) {
     uint64_t k = 0;
     for (int i = tid; i < ntiles; i += ILL_WG_THREADS) {
@@ -1272,5 +1274,5 @@ __global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a
     }
     __syncthreads();
   }
-  commit_apply(a, H, C, false);
+  commit_apply(a, H, C, false, stopreq);
 }

@@ -61,6 +61,7 @@ struct IllPassArgs {
   const uint4* ngram;      // optional n-gram draft table [ILL_NG_SLOTS] (nullptr: none)
   const int32_t* prompt;   // [4 + ILL_OB_MAX]: count, -, -, -, the last <= 256 prompt tokens
   int32_t* spec_host;      // pinned host [2]: passes and accepted drafts of speculative commits
+  const int32_t* stop_host;   // pinned host word: nonzero once the host asked queued passes to stop
   int maxctx;
   int maxsteps;
 };
@@ -1799,8 +1800,8 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 }
 
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel);
-__device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C) {
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq);
+__device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C, int stopreq) {
   const uint32_t tag = tagof_lmh(H.epoch);
   const int i = tid_opaque();
   // every workgroup's partials for the rows in use (row 0 when the pass has no lm_head rows):
@@ -1847,7 +1848,7 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
     C.g[H.lmh0 + i] = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFu));
   }
   __syncthreads();
-  commit_apply(a, H, C, true);
+  commit_apply(a, H, C, true, stopreq);
 }
 
 // ---- drafting (k_commit_spec, Shaders.swift:367-412) ----------------------------------------
@@ -1943,7 +1944,7 @@ __device__ __forceinline__ void spec_draft(const IllPassArgs& a, int have, int l
           for (int pr = 0; pr < 16; pr++) {
             const int v = D.ng[ILL_NG_MAXN - n][pr];
             if (v == 1) break;
-            if (v >= 2) { got = v - 2; break; }
+            if (v >= 2) { got = (unsigned)(v - 2) < (unsigned)a.W.vocab ? v - 2 : -1; break; }
           }
         D.d = got;
       }
@@ -1962,6 +1963,7 @@ __device__ __forceinline__ void spec_draft(const IllPassArgs& a, int have, int l
       }
       pk = wg_max_u32(pk, D.best);
       d = pk ? gld(a.prompt + 4 + (pk & 0xffff)) : -1;
+      if ((unsigned)d >= (unsigned)a.W.vocab) d = -1;   // a token outside the vocabulary is no guess
     }
     if (d < 0) break;   // uniform: every thread holds the same d
     if (i == 0) {
@@ -2034,13 +2036,18 @@ __global__ __launch_bounds__(64) void ill_trunc_kernel(IllPassArgs a) {
 // pass kernel also advances the epoch and its accumulator-bank bookkeeping. The State is
 // read from the header (the snapshot taken at the start of the pass: only the commit
 // writes it during a pass), so the commit issues stores only.
-__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel) {
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq) {
   const int i = tid_opaque();
   IllState* st = a.st;
   if (i == 0) {
     C.npath = 0;
     C.pos0 = H.pos;
-    if (H.commit == 0) {
+    if (stopreq) {
+      // the host stopped the request (Engine.swift:1032-1036 sets the State's done flag):
+      // this pass commits nothing, and every pass queued behind it leaves at its header
+      st->done = 1;
+      a.ctl->draft = 0;
+    } else if (H.commit == 0) {
       st->pos = H.pos + H.nrows;
     } else if (H.commit == 1) {
       const int tok = C.g[H.lmh0];
@@ -2143,6 +2150,11 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   if (threadIdx.x == 0) load_hdr(a, H);
   __syncthreads();
   if (H.done) return;
+  // the host's stop word, for the commit: issued now and used at the end of the pass, so
+  // its round trip to host memory stays off the pass's critical path
+  int stopreq = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0 && a.stop_host)
+    stopreq = __hip_atomic_load((const GAS int32_t*)a.stop_host, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   // a pass must fit this instantiation: every workgroup reads the same header and leaves
   if (H.nrows < 1 || H.nrows > T || H.lmhn < 0 || H.lmh0 < 0 || H.lmh0 + H.lmhn > T) {
     if (blockIdx.x == 0 && threadIdx.x == 0) set_err(a.ctl, ILL_ERR_SHAPE);
@@ -2198,7 +2210,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   trace_mark(a, ILL_TR_TAIL + 2);
   if (wg == 0) {   // the commit first: the bank is next used by the following launch
     __syncthreads();
-    commit(a, H, S.cm);
+    commit(a, H, S.cm, stopreq);
     trace_mark(a, ILL_TR_TAIL + 5);
     zero_other_bank(a, H);
   }

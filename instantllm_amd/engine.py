@@ -26,6 +26,8 @@ _lib = None
 # int encode(void* user, const char* text, int32_t* ids, int cap): the tokenizer callback of
 # the learned drafter's request context
 ENCODE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.POINTER(C.c_int32), C.c_int)
+# ill_token_fn: int (*)(int32_t token, void* user)
+TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_void_p)
 
 # The learned drafter's request context as the device reads it (IllDraftReq, ill_ildraft.h)
 DRAFT_REQ = np.dtype([("np", "<i4"), ("ncopy", "<i4"), ("nnb", "<i4"), ("nas", "<i4"),
@@ -90,6 +92,8 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_kv_copy_out": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16)]),
         "ill_kv_copy_in": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16)]),
         "ill_generate": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), C.POINTER(F32)]),
+        "ill_generate_cb": (C.c_int, [P, ip, C.c_int, C.c_int, C.c_int, ip, C.POINTER(C.c_int), C.POINTER(F32), TOKEN_FN, P]),
+        "ill_stop": (C.c_int, [P]),
         "ill_time_graph": (C.c_int, [P, C.c_int, C.POINTER(F32)]),
         "ill_load_ngram": (C.c_int, [P, C.c_void_p, C.c_int64]),
         "ill_prefix_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
@@ -230,17 +234,28 @@ class Engine:
         npos = k.shape[2]
         self._check(self.lib.ill_kv_copy_in(self.h, npos, _ptr(k, C.c_uint16), _ptr(v, C.c_uint16)))
 
-    def generate(self, tokens, max_new: int, chunk: int = 8, want_logits: bool = False):
-        """Engine.generate (Engine.swift:922-1038) without drafting."""
+    def generate(self, tokens, max_new: int, chunk: int = 8, want_logits: bool = False, on_token=None):
+        """Engine.generate (Engine.swift:922-1038) without drafting. `on_token(tok) -> bool`
+        (optional) sees each token as it is delivered; returning False stops the request."""
         a = _i32(tokens)
         out = np.zeros(max_new, np.int32)
         n = C.c_int(0)
         lg = np.empty(self.vocab, np.float32) if want_logits else None
-        self._check(self.lib.ill_generate(self.h, _ptr(a, C.c_int32), len(a), max_new, chunk,
-                                          _ptr(out, C.c_int32), C.byref(n),
-                                          _ptr(lg, C.c_float) if lg is not None else None))
+        lgp = _ptr(lg, C.c_float) if lg is not None else None
+        if on_token is None:
+            self._check(self.lib.ill_generate(self.h, _ptr(a, C.c_int32), len(a), max_new, chunk,
+                                              _ptr(out, C.c_int32), C.byref(n), lgp))
+        else:
+            cb = TOKEN_FN(lambda t, _user: 1 if on_token(int(t)) else 0)
+            self._check(self.lib.ill_generate_cb(self.h, _ptr(a, C.c_int32), len(a), max_new, chunk,
+                                                 _ptr(out, C.c_int32), C.byref(n), lgp, cb, None))
         toks = out[: n.value].tolist()
         return (toks, lg) if want_logits else toks
+
+    def stop(self):
+        """Stop the passes already launched (Engine.swift:1032-1036): the next commit to read
+        the stop word commits nothing and sets the State's done flag."""
+        self._check(self.lib.ill_stop(self.h))
 
     # ---- prefix reuse (Engine.swift:788-838, :929-933) ---------------------------------
     def prefix_info(self) -> tuple[int, int]:

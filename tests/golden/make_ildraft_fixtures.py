@@ -43,8 +43,8 @@ def make_table():
     """(table bytes, requests to draft for): 8 of the table's own requests, 8 new ones."""
     c = Corpus(seed=0)
     recs = c.records(300)
-    cfg = W.DraftConfig(cc2_min=2)
-    blob = W.build(recs, cfg, W.random_scorer(cfg.H, seed=5, emphasis=SCORER_EMPHASIS), c.flags)
+    spec = W.TableSpec(pair_min_count=2)
+    blob = W.build(recs, spec, W.random_scorer(spec.hidden, seed=5, emphasis=SCORER_EMPHASIS), c.flags)
     return blob, recs[:8] + [c.request(f) for f in range(8)]
 
 

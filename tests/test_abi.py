@@ -33,6 +33,21 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_library_exports_only_the_declared_abi():
+    """Kernel stubs and internal helpers stay local (hidden visibility plus the version
+    script instantllm_amd/csrc/exports.map): the header's functions are the whole ABI."""
+    import shutil
+    import subprocess
+    lib_path = ROOT / "instantllm_amd" / "libillhip.so"
+    if not lib_path.exists():
+        pytest.skip("libillhip.so not built")
+    if not shutil.which("nm"):
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib_path)], capture_output=True, text=True, check=True).stdout
+    exported = sorted({line.split()[-1] for line in out.splitlines() if line.strip() and line.split()[-2] in "TtWDdBbRrVv"})
+    assert exported == declared_functions()
+
+
 def test_last_error_and_bad_path_without_gpu():
     """ill_create validates the file before touching the GPU."""
     from instantllm_amd.engine import load_library

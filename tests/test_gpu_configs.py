@@ -6,8 +6,8 @@
 * config 1: the four stand-alone q4 GEMV shapes (QKV, gate/up, down, and the lm_head
   151936 x 896 with its argmax epilogue on the one-slice kernel) against the float64
   dequantization;
-* config 4's long context: a 4032-token prefill, then decode steps up to 4096 attended
-  positions against the oracle, and a 16-row tree pass near 4096 whose rows equal the
+* config 4's long context (q8, f16 and q4): a 4032-token prefill, then decode steps up
+  to 4096 attended positions against the oracle, and a 16-row tree pass near 4096 whose rows equal the
   1-row steps along their paths bit for bit (the attention split over four workgroups per
   (row, head) and their combine);
 * the decode-step invariant: the logits of N 1-row decode steps (single launches and a
@@ -111,7 +111,7 @@ def test_config1_gemv_shapes(name, rows, K, norm, amax, kernel_slices):
 
 # ---- config 4 at 4096 positions ----------------------------------------------------------
 
-@pytest.mark.parametrize("fmt", [F.FMT_Q8, F.FMT_Q4], ids=["q8", "q4"])
+@pytest.mark.parametrize("fmt", [F.FMT_Q8, F.FMT_F16, F.FMT_Q4], ids=["q8", "f16", "q4"])
 def test_config4_context_4096(tmp_path, fmt):
     """4032-token prefill, decode steps up to 4096 attended positions with the oracle's
     logits at every step, then a 16-row tree pass at 4064 whose rows equal 1-row steps

@@ -295,3 +295,36 @@ def test_stop_token_and_maxsteps(engine):
     engine.decode_step()
     st = engine.get_state()
     assert st["done"] == 1 and st["step"] == 1
+
+
+def test_host_stop_ends_queued_steps(engine):
+    """Engine.generate's onToken stop (Engine.swift:1021-1036): the callback stops the
+    request after the 5th token of a 32-step graph; the steps still queued leave at once.
+    The device advanced by no more than the steps that were already running, and the cached
+    prefix is the prompt plus the delivered tokens (a follow-up request over them reuses
+    it and continues exactly as a cold greedy run)."""
+    e = engine
+    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 4096, size=20)]
+    e.truncate_cache(0)
+    ref = e.generate(prompt, max_new=40, chunk=8)
+    seen = []
+    e.truncate_cache(0)
+    got = e.generate(prompt, max_new=32, chunk=32, on_token=lambda t: (seen.append(t), len(seen) < 5)[1])
+    assert got == ref[:5] and seen == ref[:5]
+    st = e.get_state()
+    # prefill commits token 0 at pos len(prompt); step k commits token k: at most the step in
+    # flight when the host stopped, and the one whose commit found the stop word, ran
+    assert st["done"] == 1
+    assert st["pos"] <= len(prompt) + 4 + 2, st
+    assert st["step"] <= 5 + 1, st
+    cached, _ = e.prefix_info()
+    assert cached == len(prompt) + 4
+    # a follow-up over the delivered tokens prefills only the last one and continues greedily
+    follow = e.generate(prompt + got, max_new=8, chunk=8)
+    _, last = e.prefix_info()
+    assert last == 1
+    assert follow == ref[5:13]
+    # ill_stop before a request does not leak into it: set_state clears the word
+    e.stop()
+    e.truncate_cache(0)
+    assert e.generate(prompt, max_new=12, chunk=4) == ref[:12]

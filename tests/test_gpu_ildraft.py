@@ -59,7 +59,7 @@ def setup(tmp_path_factory):
         y = e.generate(pids, max_new=60, chunk=8)
         recs.append({"prompt": text, "pids": pids, "y": y})
     tpath = str(d / "ildraft.bin")
-    W.save(tpath, recs, W.DraftConfig(cc2_min=1), W.random_scorer(16, seed=5, emphasis=EMPH), Corpus(seed=1).flags)
+    W.save(tpath, recs, W.TableSpec(pair_min_count=1), W.random_scorer(16, seed=5, emphasis=EMPH), Corpus(seed=1).flags)
     e.load_ildraft(tpath)
     tab = O.Table.load(tpath)
     yield e, tab, reqs
@@ -177,7 +177,7 @@ def test_learned_fullsize_q4():
             recs.append({"prompt": text, "pids": pids, "y": e.generate(pids, max_new=48, chunk=8)})
         with tempfile.TemporaryDirectory() as td:
             tp = str(Path(td) / "t.bin")
-            W.save(tp, recs, W.DraftConfig(), W.random_scorer(16, seed=5, emphasis=EMPH), {})
+            W.save(tp, recs, W.TableSpec(), W.random_scorer(16, seed=5, emphasis=EMPH), {})
             e.load_ildraft(tp)
             tab = O.Table.load(tp)
         pids, text = reqs[2]

@@ -259,3 +259,33 @@ def test_pass_wider_than_the_kernel_is_refused(q4_engine):
     finally:
         e.load_ngram(None)
     assert e.generate(prompt, max_new=24, chunk=8) == gx[:24]
+
+
+def test_out_of_vocabulary_draft_sources_are_refused(q4_engine, tmp_path):
+    """The drafter embeds what the n-gram table and the prompt propose in the next pass, so
+    tokens outside the model's vocabulary are refused when the table or prompt is handed
+    over; a drafter table that fails to load leaves the engine with no learned drafter (it
+    then drafts with the commit's own drafter and keeps working)."""
+    from instantllm_amd.engine import IllError
+    e = q4_engine
+    prompt = _prompt(43)
+    e.truncate_cache(0)
+    gx = e.generate(prompt, max_new=24, chunk=8)
+    t = ngram.build([gx])
+    slot = int(np.flatnonzero(t["key"] != 0)[0])
+    t["next"][slot] = VOCAB            # one past the last token
+    with pytest.raises(IllError, match="outside the vocabulary"):
+        e.load_ngram(t)
+    t["next"][slot] = -3
+    with pytest.raises(IllError, match="outside the vocabulary"):
+        e.load_ngram(t)
+    with pytest.raises(IllError, match="out of range"):
+        e.set_prompt(prompt[:5] + [VOCAB + 7] + prompt[5:])
+    bad = tmp_path / "bad.ildraft"
+    bad.write_bytes(b"not a table")
+    with pytest.raises(IllError):
+        e.load_ildraft(str(bad))
+    e.load_ngram(None)
+    e.truncate_cache(0)
+    toks, _, _ = e.generate_spec(prompt, 16, rows=4, chunk=4)
+    assert toks == gx[:16]

@@ -210,9 +210,38 @@ __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>(
 // A residual accumulator: the sum of its copies (16 rows apart), complete when every copy
 // has its contributions. XB = false: the post-attention residual XA[l] (kinds 0 ..), true:
 // the post-MLP residual XB[l] (kinds ILL_KIND_XB ..).
+// How a consumer polls an accumulator input (prep896): 0 the wave's light word (one column
+// of each row) until it is complete, then the whole input; 1 the whole input every time;
+// 2 the light word until it lacks at most ILL_SLACK_XA / ILL_SLACK_XB contributions, then
+// the whole input (until complete).
+// The slack is per accumulator (XA: 15 contributions at 16 rows, 8 / 7 per copy at one row;
+// XB: 77, or 39 / 38): the full read is issued while the last contributions land, so it
+// returns about when they are complete (one row, config 2: 333 -> 327.6 us per step with
+// slack 4 / 8 against the plain two-stage poll; the full input every time: 339 us).
+#ifndef ILL_POLL
+#define ILL_POLL 2
+#endif
+#ifndef ILL_SLACK_XA
+#define ILL_SLACK_XA 4
+#endif
+#ifndef ILL_SLACK_XB
+#define ILL_SLACK_XB 8
+#endif
 template <int T, bool XB>
 struct SrcRes {
+  static constexpr int kSlack = XB ? ILL_SLACK_XB : ILL_SLACK_XA;
   const uint64_t* base;   // copy 0, row 0
+  // every copy of column c of row t lacks at most `slack` contributions
+  __device__ __forceinline__ bool near1(int t, int c, int slack) const {
+    constexpr int NC = XB ? xb_copies<T>() : xa_copies<T>();
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+      const uint64_t w = aload64(base + ((size_t)k * 16 + t) * ILL_ACC_ROW + acc_col(c));
+      ok &= fx_count(w) + slack >= (XB ? xb_expect<T>(k) : xa_expect<T>(k));
+    }
+    return ok;
+  }
   __device__ __forceinline__ bool load1(int t, int c, float& v) const {
     constexpr int NC = XB ? xb_copies<T>() : xa_copies<T>();
     bool ok = true;
@@ -256,12 +285,14 @@ __device__ __forceinline__ float embed1(const IllWeights& W, int tok, int c) {
 }
 
 struct SrcEmbed {
+  static constexpr int kSlack = 0;
   IllWeights W;
   const int* toks;   // LDS copy of the row tokens
   __device__ __forceinline__ bool load1(int t, int c, float& v) const {
     v = embed1(W, toks[t], c);
     return true;
   }
+  __device__ __forceinline__ bool near1(int, int, int) const { return true; }
 };
 
 __device__ __forceinline__ int q4perm_inv(int c) { return (c & 8) | ((c & 1) << 2) | ((c >> 1) & 3); }
@@ -328,7 +359,10 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
     float x;
 #pragma unroll
     for (int t = 0; t < T; t++)
-      if (t < nrows) ok &= src.load1(t, cl, x);
+      if (t < nrows) {
+        if constexpr (ILL_POLL == 0) ok &= src.load1(t, cl, x);
+        else if constexpr (ILL_POLL == 2) ok &= src.near1(t, cl, Src::kSlack);
+      }
     return ok;
   }, [&]() {
     bool ok = true;
@@ -429,6 +463,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
 #define ILL_PUB_LIGHT 156                   // the word holding the row scale (k = 476)
 #define ILL_PUB_WORDS (2 * (ILL_MAXLAYERS + 1) * ILL_MAXT * ILL_PUB_W)
 #define ILL_BUF_SC1 16   // buffer access cache policy: device scope (sc1)
+#define ILL_BUF_SYS 17   // system scope (sc0 sc1): memory the host writes
 typedef uint32_t ill_v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint32_t tagof_pub(uint32_t epoch, int slot) { return epoch * 32u + (uint32_t)slot + 1u; }
 __device__ __forceinline__ uint64_t* pub_ptr(const IllPassArgs& a, int kind, int slot, int t) {
@@ -1801,7 +1836,9 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq);
-__device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C, int stopreq) {
+// stop_word: the LDS copy of the host's stop word, loaded asynchronously by thread 0 when the
+// pass started (complete once thread 0 has waited for its first poll below).
+__device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C, const int& stop_word) {
   const uint32_t tag = tagof_lmh(H.epoch);
   const int i = tid_opaque();
   // every workgroup's partials for the rows in use (row 0 when the pass has no lm_head rows):
@@ -1848,7 +1885,7 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
     C.g[H.lmh0 + i] = (int)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFu));
   }
   __syncthreads();
-  commit_apply(a, H, C, true, stopreq);
+  commit_apply(a, H, C, true, i == 0 ? stop_word : 0);
 }
 
 // ---- drafting (k_commit_spec, Shaders.swift:367-412) ----------------------------------------
@@ -2150,11 +2187,17 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   if (threadIdx.x == 0) load_hdr(a, H);
   __syncthreads();
   if (H.done) return;
-  // the host's stop word, for the commit: issued now and used at the end of the pass, so
-  // its round trip to host memory stays off the pass's critical path
-  int stopreq = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0 && a.stop_host)
-    stopreq = __hip_atomic_load((const GAS int32_t*)a.stop_host, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // The host's stop word, for the commit (workgroup 0): copied into LDS by an asynchronous
+  // load issued now and used at the end of the pass, so its round trip to host memory stays
+  // off the critical path and no register holds it meanwhile.
+  __shared__ int stop_lds;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (a.stop_host)
+      __builtin_amdgcn_global_load_lds((const void*)a.stop_host, (__attribute__((address_space(3))) void*)&stop_lds, 4, 0,
+                                       ILL_BUF_SYS);
+    else
+      stop_lds = 0;
+  }
   // a pass must fit this instantiation: every workgroup reads the same header and leaves
   if (H.nrows < 1 || H.nrows > T || H.lmhn < 0 || H.lmh0 < 0 || H.lmh0 + H.lmhn > T) {
     if (blockIdx.x == 0 && threadIdx.x == 0) set_err(a.ctl, ILL_ERR_SHAPE);
@@ -2210,7 +2253,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   trace_mark(a, ILL_TR_TAIL + 2);
   if (wg == 0) {   // the commit first: the bank is next used by the following launch
     __syncthreads();
-    commit(a, H, S.cm, stopreq);
+    commit(a, H, S.cm, stop_lds);
     trace_mark(a, ILL_TR_TAIL + 5);
     zero_other_bank(a, H);
   }

@@ -43,15 +43,16 @@ F32_NORM_BIAS_BYTES = 286_208     # f32 norms + QKV biases as stored in .ill v1
 EMBED_ROW_BYTES = 504             # one q4 embedding row (448 B codes + 56 B scales)
 KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
-# WRITE_SIZE (one counter per run, median over dispatches), each scaled by the reading of
-# a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (163,474.2 x 2 + 16,358.2) KiB. Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 351_545_920
-# MFMA utilisation of the 16-row verify pass and of the prefill GEMMs, from rocprofv3
-# SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
+# WRITE_SIZE (one counter per run, median over single dispatches), each scaled by the
+# reading of a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
+# (163,424.9 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 45d366b.
+# Source and commands: profiles/pass_kernel_q4_decode_config2.md
+TRAFFIC_BYTES_PER_STEP = 351_444_992
+# MFMA utilisation of the pass kernels (commit 45d366b) and of the prefill GEMMs, from
+# rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
 MFMA_COUNTERS = {
-    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0110, "int8_TOPs": 47.4},
-    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0106, "int8_TOPs": 48.9},
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0109, "int8_TOPs": 47.3},
+    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0109, "int8_TOPs": 50.2},
     "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.143, "f16_TFLOPs": 360.3},
     "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.109, "f16_TFLOPs": 275.1},
     "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.042, "f16_TFLOPs": 105.3},
@@ -303,6 +304,69 @@ def speculative_single(path: str, n_new: int = 96) -> dict:
     return out
 
 
+# Trace slots of the pass kernel's per-workgroup timeline (ill_trace_enable): per layer
+# ILL_TRL = 16 slots, then the lm_head / commit tail. The 1-row roles mark these stages:
+TRACE_TRL, TRACE_TAIL = 16, 16 * 30
+ATT_STAGES = (("input coded", 1), ("QKV tiles", 3), ("QKV epilogue", 4), ("attention (wave 0)", 6),
+              ("slot states", 14), ("combine", 7), ("O issued", 10))
+GUD_STAGES = (("input coded", 1), ("gate/up tile", 3), ("SiLU barrier", 4), ("down coding", 5),
+              ("down issued", 10))
+
+
+def layer_trace(e, prompt: list[int], steps: int) -> dict:
+    """The benchmarked configuration with the in-kernel trace on: `steps` decode steps after
+    the prefix, captured in one hipGraph and replayed; the trace holds the last step's
+    per-workgroup timestamps (100 MHz device clock). Per layer (medians over layers 2-21,
+    us from the attention workgroup 0's layer start): the stages of the ATT (workgroups
+    0-13) and GUD (16-91) roles; the tail (final norm, lm_head, commit) from the last
+    layer's start; the step's in-kernel span against the graph's per-step time, with and
+    without the trace."""
+    no_eos = (-5, -5)
+
+    def replay(trace: bool) -> float:
+        e.trace_enable(False)
+        if trace:
+            e.trace_enable(True)
+        e.reset_out_tokens()
+        e.set_state(pos=0, n=len(prompt), maxsteps=steps + 64, eos=no_eos)
+        e.prefill(prompt)
+        e.capture_steps(steps)
+        e.sync()
+        return e.time_graph(1) * 1e3 / steps
+
+    plain_us = replay(False)
+    traced_us = replay(True)
+    tr = e.trace_read().astype(np.int64)
+    e.trace_enable(False)
+    t0 = tr[tr > 0].min()
+    rel = np.where(tr > 0, (tr - t0) / 100.0, np.nan)   # us from the step's first mark
+    a0 = rel[0, 0::TRACE_TRL][:24]
+    layers = range(2, 22)
+
+    def med(wgs, slot):
+        v = [rel[w, TRACE_TRL * l + slot] - a0[l] for w in wgs for l in layers]
+        return round(float(np.nanmedian(v)), 2)
+
+    att, gud = range(0, 14), range(16, 92)
+    tail = {name: round(float(np.nanmedian(rel[:, TRACE_TAIL + k] - a0[23])), 2)
+            for name, k in (("final norm coded (median workgroup)", 1), ("lm_head done (median workgroup)", 2))}
+    tail["lm_head done (last workgroup)"] = round(float(np.nanmax(rel[:, TRACE_TAIL + 2]) - a0[23]), 2)
+    tail["partials seen by the commit"] = round(float(rel[0, TRACE_TAIL + 4] - a0[23]), 2)
+    tail["commit done"] = round(float(rel[0, TRACE_TAIL + 5] - a0[23]), 2)
+    span = float(np.nanmax(rel))
+    return {
+        "prefix": len(prompt), "steps": steps,
+        "graph_us_per_step": round(plain_us, 2), "graph_us_per_step_traced": round(traced_us, 2),
+        "in_kernel_span_us_traced": round(span, 2),
+        "layer_period_us": round(float((a0[21] - a0[2]) / 19), 3),
+        "att_stages_us": {n: med(att, k) for n, k in ATT_STAGES},
+        "gud_stages_us": {n: med(gud, k) for n, k in GUD_STAGES},
+        "next_layer_att_input_us": round(float(np.nanmedian([a0[l + 1] - a0[l] + rel[0, TRACE_TRL * (l + 1) + 1] - a0[l + 1]
+                                                              for l in layers])), 2),
+        "tail_from_last_layer_start_us": tail,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -321,6 +385,9 @@ def main() -> int:
                          "launches)")
     ap.add_argument("--spec-single", action="store_true",
                     help="only run the learned drafter's passes one launch at a time (for kernel traces)")
+    ap.add_argument("--layer-trace", action="store_true",
+                    help="only run the benchmarked configuration with the in-kernel trace on (graph "
+                         "replay, no profiler) and print its per-layer breakdown")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (the reference dispatch "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -383,6 +450,10 @@ def main() -> int:
         t1 = time.perf_counter()
         return (t1 - t0) * 1e3, ms_dev, e.get_state()["pos"]
 
+    if args.layer_trace:
+        print(json.dumps({"layer_trace": layer_trace(e, prompt, K)}), flush=True)
+        e.close()
+        return 0
     if W > 0:
         run(W)
     wall_ms, dev_ms, pos_end = run(K)

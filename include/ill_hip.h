@@ -146,14 +146,17 @@ ILL_API int ill_set_prompt(ill_engine* e, const int32_t* toks, int n);
  * encodeWidePass + k_commit_spec, Engine.swift:524-579), launched and waited for. */
 ILL_API int ill_spec_pass(ill_engine* e, int write_logits);
 
-/* Record `npasses` such passes into one hipGraph (q4 models): each pass takes its rows from
- * the commit before it, so the graph chains verify passes without the host; passes after
- * the stop flag early-exit. ill_launch_graph replays it. */
+/* Record `npasses` such passes into one hipGraph (Engine.swift:991-1013 encodes them the
+ * same way for every format): each pass takes its rows from the commit before it, so the
+ * graph chains verify passes without the host; passes after the stop flag early-exit. q4
+ * passes run on the pass-kernel instantiation of the State's tspec rows; q8 and f16 passes
+ * on the layer-by-layer kernels launched for as many rows, of which the rows a pass does
+ * not hold are computed and never committed. ill_launch_graph replays it. */
 ILL_API int ill_capture_spec(ill_engine* e, int npasses);
 
 /* Engine.generate with speculation on (Engine.swift:922-1038): prefill, then verify passes
- * of up to `rows` (2..16) rows, in captured graphs of `chunk` passes for q4 models (one
- * launch per pass otherwise), while polling out_tokens. adaptive != 0 chooses each pass's
+ * of up to `rows` (2..16) rows, in captured graphs of `chunk` passes (every format), while
+ * polling out_tokens. adaptive != 0 chooses each pass's
  * shape from the accepted drafts per pass (Engine.nextPassShape, :888-898, with thresholds
  * from this engine's pass costs, which grow with the kernel's row count): the configured
  * shape while at least 2.4 are accepted, 4-row chains while at least 1.6 are (back to the

@@ -200,8 +200,16 @@ int count_passes(ill_engine* e, int n);
 // against 804 us at 4 rows, 742 against 759 at 3; 722 against 710 at 2).
 int pass_T(int rows) { return rows <= 1 ? 1 : (rows <= 2 ? 4 : 16); }
 
+void op_seq_fmt(ill_engine* e, int M, int lm_rows);
+
+// One pass of up to T rows whose rows, mode and commit come from the device (the control
+// block the previous commit or the host wrote): q4 on the T-row pass kernel; q8 and f16 on
+// the layer-by-layer kernels launched for T rows, of which the rows beyond the pass's own
+// are computed and never committed (row t's K/V slot is pos + t, so they touch no live
+// slot, and every row's arithmetic is independent of the others).
 void enqueue_pass(ill_engine* e, int T) {
-  if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
+  if (e->fmt != 2) op_seq_fmt(e, T, T);
+  else if (T == 1) hipLaunchKernelGGL(ill_pass_kernel<1>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(1), e->stream, e->args);
   else if (T == 4) hipLaunchKernelGGL(ill_pass_kernel<4>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(4), e->stream, e->args);
   else hipLaunchKernelGGL(ill_pass_kernel<16>, dim3(ILL_WG), dim3(ILL_WG_THREADS), ill_stage_bytes(16), e->stream, e->args);
 }
@@ -1021,7 +1029,6 @@ int ill_spec_pass(ill_engine* e, int write_logits) {
 
 int ill_capture_spec(ill_engine* e, int npasses) {
   if (!e || npasses < 1) return fail(ILL_E_ARG, "bad pass count");
-  if (e->fmt != 2) return fail(ILL_E_FORMAT, "chained speculative passes need the q4 pass kernel (format %d passes size their launches on the host)", e->fmt);
   drop_graph(e);
   // every pass has at most the State's tspec rows: the smallest instantiation that holds them
   IllState s;
@@ -1381,7 +1388,6 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
   int cur_tree = treeb;
   HCK(hipMemcpyAsync(&e->ctl->tree_b, &cur_tree, 4, hipMemcpyHostToDevice, e->stream));
   if ((rc = ill_prefill(e, toks + common, ntok - common, 0))) return rc;
-  const bool graphs = e->fmt == 2;
   // Pass shapes (Engine.nextPassShape, Engine.swift:888-898, with thresholds from this
   // engine's pass costs, which grow with the kernel's row count: about 340 us for 1 row,
   // 800 us for 4 and 860 us for 16, plus the drafting, up to 250 us for a learned tree): a
@@ -1464,10 +1470,7 @@ int ill_generate_spec(ill_engine* e, const int32_t* toks, int ntok, int max_new,
       // an unjudged shape has at most one of its passes in flight (the host sees a commit
       // while its drafting still runs, and launches the next pass behind it)
       if (judged || encoded <= std::max(done, lv_first)) {
-        if (!graphs) {
-          if ((rc = ill_spec_pass(e, 0))) return rc;   // host-sized pass (layer-by-layer path)
-          encoded++;
-        } else if (pass_T(drafted_rows) != pass_T(cur_rows) || !judged) {
+        if (pass_T(drafted_rows) != pass_T(cur_rows) || !judged) {
           if ((rc = launch_spec_one(e, pass_T(drafted_rows)))) return rc;
           encoded++;
         } else {

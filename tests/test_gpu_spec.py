@@ -132,25 +132,52 @@ def test_adaptive_shapes_keep_the_output(q4_engine):
     assert toks == g
 
 
-def test_spec_q8_layer_by_layer_path(tmp_path):
-    """q8 passes are sized on the host: one launch per pass, the same tokens and counts."""
+@pytest.mark.parametrize("fmt", [F.FMT_Q8, F.FMT_F16], ids=["q8g32", "f16"])
+def test_spec_layer_by_layer_formats_chain_on_the_device(tmp_path, fmt):
+    """q8 and f16 speculative passes chained in hipGraphs (Engine.swift:991-1013 encodes
+    every format's passes ahead): the tokens are greedy's and the pass and accept counts the
+    oracle's simulation; the same passes launched one by one give the same tokens and counts;
+    a captured graph of passes equals them too (adaptive shapes included)."""
     from instantllm_amd.engine import Engine
-    path = str(tmp_path / "q8.ill")
-    synth.build_model(path, F.FMT_Q8, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB), q8_group=32)
+    path = str(tmp_path / "m.ill")
+    synth.build_model(path, fmt, seed=4, shape=synth.ModelShape(layers=3, vocab=VOCAB), q8_group=32)
     e = Engine(path, max_context=1024, max_pass=16, max_steps=128)
     try:
         prompt = _prompt(11)
         e.truncate_cache(0)   # compare cold runs
-        gx = e.generate(prompt, max_new=32 + 8, chunk=8)
+        gx = e.generate(prompt, max_new=32 + 16, chunk=8)
         g = gx[:32]
-        table = ngram.build([g])
+        table = ngram.build([g[:20]])   # drafts right for the first part, then on their own
         e.load_ngram(table)
         e.truncate_cache(0)   # compare cold runs
         toks, passes, acc = e.generate_spec(prompt, 32, rows=8, chunk=4)
+        assert toks == g
+        assert (passes, acc) == D.simulate(prompt, gx, 32, 8, table=table)[1:]
+        e.truncate_cache(0)
+        toks_a, _, _ = e.generate_spec(prompt, 32, rows=16, chunk=3, adaptive=True)
+        assert toks_a == g
+        # single passes, then one captured graph of the same passes
+        for graph in (False, True):
+            e.truncate_cache(0)
+            e.reset_out_tokens()
+            e.set_prompt(prompt)
+            e.set_state(pos=0, n=len(prompt), maxsteps=32, tspec=8)
+            e.prefill(prompt)
+            if graph:
+                e.capture_spec(passes)
+                e.launch_graph()
+                e.sync()
+            else:
+                for _ in range(passes):
+                    if e.get_state()["done"]:
+                        break
+                    e.spec_pass()
+            st = e.get_state()
+            assert [int(t) for t in e.out_tokens()[:32]] == g, graph
+            assert (st["passes"], st["accepted"]) == (passes, acc), graph
     finally:
+        e.load_ngram(None)
         e.close()
-    assert toks == g
-    assert (passes, acc) == D.simulate(prompt, gx, 32, 8, table=table)[1:]
 
 
 def test_spec_fullsize_q4():

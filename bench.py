@@ -354,6 +354,14 @@ def layer_trace(e, prompt: list[int], steps: int) -> dict:
     tail["partials seen by the commit"] = round(float(rel[0, TRACE_TAIL + 4] - a0[23]), 2)
     tail["commit done"] = round(float(rel[0, TRACE_TAIL + 5] - a0[23]), 2)
     span = float(np.nanmax(rel))
+    entry = rel[:, TRACE_TAIL + 8]
+    edges = {"first workgroup entered": 0.0,
+             "last workgroup entered": round(float(np.nanmax(entry)), 2),
+             "header loaded (median workgroup)": round(float(np.nanmedian(rel[:, TRACE_TAIL + 9])), 2),
+             "first layer start (attention workgroup 0)": round(float(a0[0]), 2),
+             "commit done": round(float(rel[0, TRACE_TAIL + 5]), 2),
+             "workgroup 0 exits": round(float(rel[0, TRACE_TAIL + 10]), 2),
+             "last workgroup exits": round(float(np.nanmax(rel[:, TRACE_TAIL + 10])), 2)}
     return {
         "prefix": len(prompt), "steps": steps,
         "graph_us_per_step": round(plain_us, 2), "graph_us_per_step_traced": round(traced_us, 2),
@@ -364,6 +372,7 @@ def layer_trace(e, prompt: list[int], steps: int) -> dict:
         "next_layer_att_input_us": round(float(np.nanmedian([a0[l + 1] - a0[l] + rel[0, TRACE_TRL * (l + 1) + 1] - a0[l + 1]
                                                               for l in layers])), 2),
         "tail_from_last_layer_start_us": tail,
+        "kernel_edges_us": edges,
     }
 
 

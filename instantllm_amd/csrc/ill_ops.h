@@ -1249,8 +1249,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a
   __shared__ PassHdr H;
   __shared__ CommitLds C;
   __shared__ uint64_t best[ILL_WAVES];
-  if (threadIdx.x == 0) load_hdr(a, H);
-  __syncthreads();
+  load_hdr(a, H);
   if (H.done) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   int stopreq = 0;   // the host's stop word (see ill_pass_kernel), waited for at the commit

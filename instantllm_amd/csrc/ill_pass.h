@@ -67,7 +67,8 @@ struct IllPassArgs {
 };
 
 // Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10 and
-// 12-15 role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail.
+// 12-15 role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail
+// (tail + 8: the workgroup entered the kernel, + 9: header loaded, + 10: it leaves).
 #define ILL_TRL 16
 #define ILL_TR_TAIL (ILL_TRL * ILL_MAXLAYERS)
 #define ILL_TRACE_SLOTS (ILL_TR_TAIL + 12)
@@ -99,58 +100,74 @@ __device__ __forceinline__ int tid_opaque() {
 // its outstanding global loads, stores, atomics or LDS DMA (which __syncthreads would).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// The pass header: State, control block and row metadata, read once by thread 0.
+// The pass header: State, control block and row metadata. Called by every thread of the
+// workgroup (it holds two barriers). Wave 0's lanes load one word each (lanes 0-15 the
+// State, 16-31 the control block, 32-47 the row tokens, 48-63 the tree's depths and
+// parents), so the whole header is one round trip to memory; threads 0-15 then fill one
+// row each of the path table. (Thread 0 loading field by field into LDS took about 40
+// round trips, 8.7 us at the start of every pass: the stores to LDS kept the compiler from
+// issuing the loads together.)
 __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
-  const IllState* st = a.st;
-  const IllCtl* c = a.ctl;
-  H.done = st->done;
-  H.step = st->step;
-  H.maxsteps = st->maxsteps;
-  H.eos0 = st->eos0;
-  H.eos1 = st->eos1;
-  H.passes = st->passes;
-  H.accepted = st->accepted;
-  H.tspec = st->tspec;
-  H.nodraft = st->nodraft;
-  // every load's address is known before any value arrives (one round trip): both
-  // banks' row counts, all 16 row tokens and tree entries are loaded and then selected
-  const int ep = c->epoch, br0 = c->bank_rows[0], br1 = c->bank_rows[1];
-  H.epoch = ep;
-  H.bank = ep & 1;
-  H.zrows = (ep & 1) ? br0 : br1;
-  H.mode = c->mode;
-  H.nrows = c->nrows;
-  H.pos = st->pos;
-  H.lmh0 = c->lmh_row0;
-  H.lmhn = c->lmh_rows;
-  H.wlog = c->write_logits;
-  H.commit = c->commit;
-  int pt[16], td[16], tp[16];   // ptoks holds 16 rows, tree ILL_TR_INTS entries
-#pragma unroll
-  for (int t = 0; t < 16; t++) {
-    pt[t] = a.ptoks[t];
-    td[t] = a.tree[ILL_TR_DEPTH + t];
-    tp[t] = a.tree[ILL_TR_PARENT + t];
-  }
-#pragma unroll
-  for (int t = 0; t < 16; t++) {
-    H.tok[t] = t < H.nrows ? pt[t] : 0;
-    if (H.mode == ILL_MODE_TREE) {
-      H.depth[t] = t < H.nrows ? td[t] : 0;
-      H.parent[t] = t < H.nrows ? tp[t] : 0;
-    } else {
-      H.depth[t] = t;
-      H.parent[t] = t > 0 ? t - 1 : 0;
+  __shared__ int raw[80];
+  const int t = threadIdx.x;
+  if (t < 64) {
+    int v0, v1 = 0;
+    if (t < 16) v0 = gld((const int32_t*)a.st + t);
+    else if (t < 32) v0 = gld((const int32_t*)a.ctl + (t - 16));
+    else if (t < 48) v0 = gld(a.ptoks + (t - 32));
+    else {
+      v0 = gld(a.tree + ILL_TR_DEPTH + (t - 48));
+      v1 = gld(a.tree + ILL_TR_PARENT + (t - 48));
     }
+    raw[t] = v0;
+    if (t >= 48) raw[t + 16] = v1;
   }
-  for (int t = 0; t < 16; t++) {
-    for (int d = 0; d < 16; d++) H.prow[t][d] = 0;
+  lds_barrier();
+  const IllState& st = *(const IllState*)&raw[0];
+  const IllCtl& c = *(const IllCtl*)&raw[16];
+  const int mode = c.mode, nrows = c.nrows;
+  static_assert(sizeof(IllState) == 64 && sizeof(IllCtl) == 64, "one word per lane");
+  if (t == 0) {
+    H.done = st.done;
+    H.step = st.step;
+    H.maxsteps = st.maxsteps;
+    H.eos0 = st.eos0;
+    H.eos1 = st.eos1;
+    H.passes = st.passes;
+    H.accepted = st.accepted;
+    H.tspec = st.tspec;
+    H.nodraft = st.nodraft;
+    H.pos = st.pos;
+    const uint32_t ep = c.epoch;
+    H.epoch = ep;
+    H.bank = ep & 1;
+    H.zrows = (ep & 1) ? c.bank_rows[0] : c.bank_rows[1];
+    H.mode = mode;
+    H.nrows = nrows;
+    H.lmh0 = c.lmh_row0;
+    H.lmhn = c.lmh_rows;
+    H.wlog = c.write_logits;
+    H.commit = c.commit;
+  }
+  if (t < 16) {
+    // row r's depth and parent: the tree's entries in tree passes, a chain otherwise
+    auto depth = [&](int r) { return mode == ILL_MODE_TREE ? (r < nrows ? raw[48 + r] : 0) : r; };
+    auto parent = [&](int r) { return mode == ILL_MODE_TREE ? (r < nrows ? raw[64 + r] : 0) : (r > 0 ? r - 1 : 0); };
+    H.tok[t] = t < nrows ? raw[32 + t] : 0;
+    H.depth[t] = depth(t);
+    H.parent[t] = parent(t);
+    int row[16];
+#pragma unroll
+    for (int d = 0; d < 16; d++) row[d] = 0;
     int r = t;
-    for (int d = H.depth[t]; d >= 0; --d) {
-      H.prow[t][d] = r;
-      r = r > 0 ? H.parent[r] : 0;
+    for (int d = depth(t); d >= 0; --d) {
+      if (d < 16) row[d] = r;
+      r = r > 0 ? parent(r) : 0;
     }
+#pragma unroll
+    for (int d = 0; d < 16; d++) H.prow[t][d] = row[d];
   }
+  lds_barrier();
 }
 
 // ---- residual fixed point --------------------------------------------------------------
@@ -2184,8 +2201,9 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   __shared__ PassLds<T> S;
   extern __shared__ __attribute__((aligned(16))) uint8_t ill_stage[];   // ILL_STAGE_BYTES (dynamic)
   __shared__ PassHdr H;
-  if (threadIdx.x == 0) load_hdr(a, H);
-  __syncthreads();
+  trace_mark(a, ILL_TR_TAIL + 8);
+  load_hdr(a, H);
+  trace_mark(a, ILL_TR_TAIL + 9);
   if (H.done) return;
   // The host's stop word, for the commit (workgroup 0): copied into LDS by an asynchronous
   // load issued now and used at the end of the pass, so its round trip to host memory stays
@@ -2257,4 +2275,5 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
     trace_mark(a, ILL_TR_TAIL + 5);
     zero_other_bank(a, H);
   }
+  trace_mark(a, ILL_TR_TAIL + 10);
 }

@@ -746,6 +746,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   IllPassArgs& a = e->args;
   a.W = e->W;
   a.L = e->dlayers;
+  a.L0 = e->hlayers[0];
   a.st = e->st;
   a.ctl = e->ctl;
   a.ptoks = e->ptoks;

@@ -64,6 +64,8 @@ struct IllPassArgs {
   const int32_t* stop_host;   // pinned host word: nonzero once the host asked queued passes to stop
   int maxctx;
   int maxsteps;
+  IllLayerW L0;            // L[0] again: the pass's first weight stage reads these pointers from
+                           // the kernel arguments (scalar loads), not with a round trip each
 };
 
 // Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10 and
@@ -2228,8 +2230,8 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   const bool att1 = ill_pub<T>() && wg >= ILL_R_ATT1 && wg < ILL_R_ATT1 + ILL_NATT;
   if (att0 || att1) {
     const int h = att0 ? wg - ILL_R_ATT0 : wg - ILL_R_ATT1, half = att0 ? 0 : 1;
-    att_stage_qkv<T>(a.L[0], h, w, lane, ill_stage);
-    if (T == 1) att_stage_o<T>(a.L[0], h, w, lane, ill_stage);
+    att_stage_qkv<T>(a.L0, h, w, lane, ill_stage);
+    if (T == 1) att_stage_o<T>(a.L0, h, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
       trace_mark(a, ILL_TRL * l);
       if (!role_att<T>(a, H, S.att, l, h, half, ill_stage)) return;
@@ -2242,7 +2244,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
     }
   } else if (wg >= ILL_R_GUD0 && wg < ILL_R_GUD0 + ILL_NGU) {
     const int ub = wg - ILL_R_GUD0;
-    gud_stage(a.L[0], ub, w, lane, ill_stage);
+    gud_stage(a.L0, ub, w, lane, ill_stage);
     for (int l = 0; l < NL; l++) {
       trace_mark(a, ILL_TRL * l);
       if (!role_gud<T>(a, H, S.gud, l, ub, ill_stage)) return;

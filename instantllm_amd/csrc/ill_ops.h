@@ -281,8 +281,8 @@ __device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float 
 // row (used when that is the row's position).
 template <int BM, int EPI>
 __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHdr& hd, const v4f (&acc)[BM / 16][2], int m0,
-                                                 int n0, int w, int kg, int n, uint64_t (&red)[4][16], int cs_base = -1,
-                                                 const float2* cs = nullptr) {
+                                                 int n0, int kz, int w, int kg, int n, uint64_t (&red)[4][16],
+                                                 int cs_base = -1, const float2* cs = nullptr) {
   constexpr int TM = BM / 16;
   if (hd.done) return;
   const OpCtx& c = a.c;
@@ -295,7 +295,7 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int m = m0 + 16 * i + 4 * kg + r, col = n0 + 32 * w + 16 * j + n;
-          if (m < a.M) a.part[((size_t)blockIdx.z * a.M + m) * a.W.N + col] = acc[i][j][r];
+          if (m < a.M) a.part[((size_t)kz * a.M + m) * a.W.N + col] = acc[i][j][r];
         }
     return;
   }
@@ -374,9 +374,28 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
 // buffer, two barriers per k-step, half the LDS and fewer registers: more workgroups per
 // CU, which is what the many-tile prefill gate/up GEMM needs (25.6 vs 40.7 us at 512 rows,
 // f16), while the ring wins where the tiles are few (O and down: 14.6 vs 17.0 us).
-template <int FMT, int BM, int EPI, int DEPTH>
+// Tile of a prefill GEMM workgroup (grid: column tiles x row tiles x K slices). Workgroups
+// are dealt to the 8 XCDs round-robin (workgroup id mod 8), and each XCD has its own L2, so
+// the tiles are renumbered: the order (K slice, column tile, row tile) is cut into 8
+// contiguous runs, run c going to the workgroups on XCD c in dispatch order. The row tiles
+// of a weight slab (column tile, K slice) then share one XCD's L2 instead of fetching the
+// slab from HBM once per XCD (512-row down projection, f16: 19.3 -> 16.5 us; QKV and O
+// 2-7% faster). A permutation of tiles: the results do not change.
+struct OpTile {
+  int x, y, z;
+};
+__device__ __forceinline__ OpTile op_tile_xcd() {
+  const int nx = gridDim.x, ny = gridDim.y;
+  const int T = nx * ny * gridDim.z;
+  const int id = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  const int c = id & 7, k = id >> 3;
+  const int u = c * (T >> 3) + min(c, T & 7) + k;   // XCD c holds ceil((T - c) / 8) workgroups
+  const int y = u % ny, sl = u / ny;
+  return {sl % nx, y, sl / nx};
+}
+
+template <int FMT, int BM, int EPI, int DEPTH, int NB = (DEPTH > 1 ? 2 : 1)>
 __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
-  constexpr int NB = DEPTH > 1 ? 2 : 1;
   const OpHdr hd = op_hdr(a.c);
   __shared__ __attribute__((aligned(16))) _Float16 As[NB][BM * OP_LDK];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[NB][OP_BN * OP_LDK];
@@ -384,9 +403,11 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   constexpr int TM = BM / 16;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
-  const int n0 = blockIdx.x * OP_BN, m0 = blockIdx.y * BM;
+  // (the gate/up GEMM keeps the dispatch order: renumbered it ran 1.5-10% slower, measured)
+  const OpTile tl = BM == 64 && EPI != OP_SILU ? op_tile_xcd() : OpTile{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int n0 = tl.x * OP_BN, m0 = tl.y * BM;
   const int K = a.W.K;
-  const int kb = blockIdx.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
+  const int kb = tl.z * a.ksteps * OP_BK, ke = min(K, kb + a.ksteps * OP_BK);
   const int ns = (ke - kb) / OP_BK;
   v4f acc[TM][2];
 #pragma unroll
@@ -421,7 +442,7 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
       }
       __syncthreads();
     }
-    op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, w, kg, n, red);
+    op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, tl.z, w, kg, n, red);
     return;
   }
   constexpr int OP_DEPTH = DEPTH;
@@ -441,6 +462,7 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   auto kstep = [&](int d, int st, bool refetch) {
     _Float16* as = As[(d & 1) % NB];
     _Float16* bs = Bs[(d & 1) % NB];
+    if constexpr (NB == 1) lds_barrier();   // one buffer: every wave is done with the last step
     op_store_a<BM>(ar[d], as, tid);
     op_store_w<FMT>(wr[d], bs, tid);
     lds_barrier();   // LDS only: the ring's HBM loads stay in flight
@@ -475,7 +497,7 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
 #pragma unroll
   for (int d = 0; d < OP_DEPTH - 1; d++)
     if (s0 + d < ns) kstep(d, s0 + d, false);
-  op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, w, kg, n, red);
+  op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, tl.z, w, kg, n, red);
 }
 
 // ---- GEMM of passes of up to 16 rows --------------------------------------------------
@@ -656,9 +678,9 @@ __global__ __launch_bounds__(64 * NWV) void op_gemv_kernel(OpGemmArgs a) {
       for (int jj = 0; jj < 2; jj++)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[0][jj][r] = acc[0][jj][r] + kacc[ww][jj][lane][r];
-    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, 0, kg, n, red, a.pos_hint, cs);
+    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, (int)blockIdx.z, 0, kg, n, red, a.pos_hint, cs);
   } else {
-    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, w, kg, n, red, a.pos_hint, cs);
+    op_gemm_epilogue<16, EPI>(a, hd, acc, 0, n0, (int)blockIdx.z, w, kg, n, red, a.pos_hint, cs);
   }
 }
 

@@ -135,3 +135,64 @@ def test_oracle_q8_bound_and_ulp_rule():
     assert np.all(sf * 127 >= amax)                      # every code fits
     lower = (s.view(np.uint16) - 1).view(np.float16).astype(np.float32)
     assert np.all((lower * 127 < amax) | (sf == 0) | (s.view(np.uint16) == np.float16(amax / 127).view(np.uint16)))
+
+
+CLIP_FIXTURE = ROOT / "tests" / "golden" / "q4_clip_groups.json"
+
+
+def _clip_groups():
+    import json
+    doc = json.loads(CLIP_FIXTURE.read_text())
+    groups = list(doc["groups"]) + ([doc["refit"]] if doc["refit"] else [])
+    w = np.array([g["w"] for g in groups], np.float32)
+    return doc, groups, w
+
+
+def _answers(q, s, b):
+    return [(tuple(int(v) for v in q[i]), int(s.view(np.uint16)[i]), int(b.view(np.uint16)[i]))
+            for i in range(len(s))]
+
+
+def _want(groups):
+    return [(tuple(g["codes"]), g["scale_f16_bits"], g["bias_f16_bits"]) for g in groups]
+
+
+def test_oracle_q4_clip_search_known_answers():
+    """Hand-evaluated groups (tests/golden/make_q4_clip_fixtures.py: every candidate of
+    Convert.swift:319-366 in float64), one won by each clip pair with a margin, and one whose
+    least-squares refit moves (scale, bias) off the clipped fit: the oracle returns each
+    group's (codes, f16 scale, f16 bias)."""
+    doc, groups, w = _clip_groups()
+    clips = (0.0, 0.03, 0.06, 0.1, 0.15)
+    assert doc["refit"] is not None and len(doc["groups"]) == 25
+    assert {tuple(g["pair"]) for g in doc["groups"]} == {(a, c) for a in clips for c in clips}
+    assert (doc["refit"]["scale_f16_bits"], doc["refit"]["bias_f16_bits"]) != \
+        (doc["refit"]["unrefit_scale_f16_bits"], doc["refit"]["unrefit_bias_f16_bits"])
+    q, s, b = OQ.q4_groups(w)
+    assert _answers(q, s, b) == _want(groups)
+
+
+@pytest.mark.parametrize("change", ["drop", "nudge"])
+def test_clip_fixtures_catch_a_wrong_clip_constant(monkeypatch, change):
+    """A planted mistake in the oracle's clip set (one constant dropped, or moved by 0.01)
+    changes the answer of at least one fixture group, for every constant: the fixtures pin
+    all five."""
+    _, groups, w = _clip_groups()
+    want = _want(groups)
+    clips = [float(c) for c in OQ.CLIPS]
+    for i in range(len(clips)):
+        wrong = clips[:i] + clips[i + 1:] if change == "drop" else clips[:i] + [clips[i] + 0.01] + clips[i + 1:]
+        monkeypatch.setattr(OQ, "CLIPS", np.array(wrong, np.float32))
+        assert _answers(*OQ.q4_groups(w)) != want, (change, clips[i])
+
+
+@needs_lib
+def test_q4_library_clip_search_known_answers():
+    """The library's quantizer on the same groups, one group per row."""
+    from instantllm_amd.engine import quantize_q4
+    _, groups, w = _clip_groups()
+    packed, sb = quantize_q4(w, threads=2)
+    q = np.empty((w.shape[0], 64), np.int64)
+    q[:, 0::2] = packed & 0xF
+    q[:, 1::2] = packed >> 4
+    assert _answers(q, sb[:, 0, 0], sb[:, 0, 1]) == _want(groups)

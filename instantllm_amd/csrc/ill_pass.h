@@ -39,6 +39,8 @@
 #define ILL_NRED (ILL_RED_Q * ILL_MAXT)
 #define ILL_R_RED0 108       // 16-row passes: REDUCE WGs 108..235 (row r / 8, column eighth r % 8)
 #define ILL_R_ATT1 236       // 16-row passes: ATT WGs 236..249, rows 8-15 of head wg - 236
+#define ILL_R_IDLE0 92       // 1-row passes: WGs 92..255 have no layer role; each stages
+#define ILL_LMH_PRE 16       // ILL_LMH_PRE lm_head tiles (two per wave) in its LDS meanwhile
 
 struct IllPassArgs {
   IllWeights W;
@@ -106,9 +108,10 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // workgroup (it holds two barriers). Wave 0's lanes load one word each (lanes 0-15 the
 // State, 16-31 the control block, 32-47 the row tokens, 48-63 the tree's depths and
 // parents), so the whole header is one round trip to memory; threads 0-15 then fill one
-// row each of the path table. (Thread 0 loading field by field into LDS took about 40
-// round trips, 8.7 us at the start of every pass: the stores to LDS kept the compiler from
-// issuing the loads together.)
+// row each of the path table. (Thread 0 filling it alone took 8.7 us at the start of every
+// pass: its header reads became scalar loads, which share the lgkmcnt counter with LDS
+// stores, so the waits for its ~150 LDS stores also waited for loads in flight, and the
+// reads went out in six dependent rounds.)
 __device__ __forceinline__ void load_hdr(const IllPassArgs& a, PassHdr& H) {
   __shared__ int raw[80];
   const int t = threadIdx.x;
@@ -1763,8 +1766,14 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
 
+// The lm_head over the final RMSNorm (tied embedding rows, 16-row tiles), with the per-row
+// argmax partials published for the commit. In 1-row passes the workgroups with no layer
+// role (ILL_R_IDLE0..255) copy ILL_LMH_PRE tiles each into their free LDS stage while they
+// wait for the last layer, and those tiles come off the stream the other workgroups share
+// after the last edge (the argmax and the logits do not depend on which workgroup holds a
+// tile; the products run the same code on either source).
 template <int T>
-__device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, LmhLds<T>& Lm) {
+__device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H, LmhLds<T>& Lm, uint8_t* stage) {
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int NL = a.W.layers;
@@ -1775,8 +1784,21 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
   int bi[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) { bv[j] = -INFINITY; bi[j] = 0x7fffffff; }
+  static_assert(ILL_LMH_PRE == 2 * ILL_WAVES && ILL_LMH_PRE * ILL_ST_TILE <= ill_stage_bytes(1), "two tiles per wave");
+  const bool pre = T == 1 && wg >= ILL_R_IDLE0;
+  const int npre = T == 1 ? (ILL_WG - ILL_R_IDLE0) * ILL_LMH_PRE : 0;   // tiles 0 .. npre-1 staged
+  const int p0 = (wg - ILL_R_IDLE0) * ILL_LMH_PRE + 2 * w;              // this wave's staged pair
   if (H.lmhn > 0) {
-    int tile = wg + ILL_WG * w;
+    if (pre) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        if (p0 + i >= ntiles) continue;
+        uint8_t* d = stage + (2 * w + i) * ILL_ST_TILE;
+        wave_copy_to_lds(a.W.wemb + (size_t)(p0 + i) * ILL_KST * 1024, d, ILL_KST * 1024, lane);
+        wave_copy_to_lds((const uint8_t*)(a.W.semb + (size_t)(p0 + i) * ILL_KST * 32), d + ILL_KST * 1024, ILL_KST * 128, lane);
+      }
+    }
+    int tile = npre + wg + ILL_WG * w;
     Q4Tile cur;
     if (tile < ntiles) q4_load(cur, a.W.wemb + (size_t)tile * ILL_KST * 1024, a.W.semb + (size_t)tile * ILL_KST * 32, lane);
     float rs[4];   // final-norm scale of this lane's rows
@@ -1786,6 +1808,26 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
     if (!ok) return false;
     trace_mark(a, ILL_TR_TAIL + 1);
     constexpr int RPL = T >= 4 ? 4 : T;
+    if (pre) {
+      wait_vm();   // the staged tiles (copied long before; also the first streamed tile)
+      float acc2[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      q4_tiles896_lds<T, 2>(stage + 2 * w * ILL_ST_TILE, ILL_ST_TILE, Lm.prep, lane, acc2);
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        if (p0 + i >= ntiles) continue;
+        const int idx = 16 * (p0 + i) + n;
+#pragma unroll
+        for (int j = 0; j < RPL; j++) acc2[i][j] *= rs[j];
+#pragma unroll
+        for (int j = 0; j < RPL; j++) {
+          const int t = 4 * kg + j;
+          if (t >= H.lmh0 && t < H.lmh0 + H.lmhn) {
+            if (H.wlog) gst(a.logits + (size_t)t * V + idx, acc2[i][j]);
+            amax_merge(bv[j], bi[j], acc2[i][j], idx);
+          }
+        }
+      }
+    }
     while (tile < ntiles) {
       const int nxt = tile + ILL_WG * ILL_WAVES;
       Q4Tile nx;
@@ -2268,7 +2310,7 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
     }
   }
   trace_mark(a, ILL_TR_TAIL);
-  if (!role_lmh<T>(a, H, S.lmh)) return;
+  if (!role_lmh<T>(a, H, S.lmh, ill_stage)) return;
   if (wg != 0) zero_other_bank(a, H);
   trace_mark(a, ILL_TR_TAIL + 2);
   if (wg == 0) {   // the commit first: the bank is next used by the following launch

@@ -70,6 +70,23 @@ struct IllPassArgs {
                            // the kernel arguments (scalar loads), not with a round trip each
 };
 
+// Layer l's weight pointers read with scalar loads (the table is written by the host only,
+// so the constant address space is exact). Passes of 4 and 16 rows use them: a vector load
+// of a pointer is waited for with vmcnt, which also waits for every weight stage the wave
+// issued before it (16-row verify 4 us faster). The 1-row kernel keeps the generic loads:
+// there the pointers' SGPRs spill into VGPR lanes in the role loops (10 us slower).
+__device__ __forceinline__ IllLayerW layer_ptrs(const IllLayerW* L, int l) {
+  static_assert(sizeof(IllLayerW) % 8 == 0, "pointer fields");
+  typedef const __attribute__((address_space(4))) uint64_t* CP;
+  const CP p = (CP)(L + l);
+  uint64_t v[sizeof(IllLayerW) / 8];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(IllLayerW) / 8); i++) v[i] = p[i];
+  IllLayerW r;
+  __builtin_memcpy(&r, v, sizeof r);
+  return r;
+}
+
 // Trace slots per workgroup: ILL_TRL per layer (0 role start, 1 input ready, 2-10 and
 // 12-15 role-specific intermediate points, 11 done) and 12 for the lm_head / commit tail
 // (tail + 8: the workgroup entered the kernel, + 9: header loaded, + 10: it leaves).
@@ -1289,7 +1306,8 @@ __device__ __forceinline__ bool role_att(const IllPassArgs& a, const PassHdr& H,
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
   const int g = h / 7;
-  const IllLayerW& L = a.L[l];
+  const IllLayerW Lc = layer_ptrs(a.L, l);
+  const IllLayerW& L = T == 1 ? a.L[l] : Lc;
   constexpr int RPL = T >= 4 ? 4 : T;
   const int nrows = H.nrows;
   const int pos = H.pos;
@@ -1606,7 +1624,8 @@ template <int T>
 __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H, GudLds<T>& G, int l, int ub, uint8_t* stage) {
   const int tid = tid_opaque(), w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
-  const IllLayerW& L = a.L[l];
+  const IllLayerW Lc = layer_ptrs(a.L, l);
+  const IllLayerW& L = T == 1 ? a.L[l] : Lc;
   const int nrows = H.nrows;
   constexpr int RPL = T >= 4 ? 4 : T;
   float rs[4];   // RMSNorm scale of this lane's rows
@@ -2279,8 +2298,10 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       if (!role_att<T>(a, H, S.att, l, h, half, ill_stage)) return;
       lds_barrier();   // every wave is done with the stage before it is refilled
       if (l + 1 < NL) {
-        att_stage_qkv<T>(a.L[l + 1], h, w, lane, ill_stage);
-        if (T == 1) att_stage_o<T>(a.L[l + 1], h, w, lane, ill_stage);
+        const IllLayerW Ln = layer_ptrs(a.L, l + 1);
+        const IllLayerW& L1 = T == 1 ? a.L[l + 1] : Ln;
+        att_stage_qkv<T>(L1, h, w, lane, ill_stage);
+        if (T == 1) att_stage_o<T>(L1, h, w, lane, ill_stage);
       }
       trace_mark(a, ILL_TRL * l + 11);
     }
@@ -2291,7 +2312,10 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
       trace_mark(a, ILL_TRL * l);
       if (!role_gud<T>(a, H, S.gud, l, ub, ill_stage)) return;
       lds_barrier();
-      if (l + 1 < NL) gud_stage(a.L[l + 1], ub, w, lane, ill_stage);
+      if (l + 1 < NL) {
+        const IllLayerW Ln = layer_ptrs(a.L, l + 1);
+        gud_stage(T == 1 ? a.L[l + 1] : Ln, ub, w, lane, ill_stage);
+      }
       trace_mark(a, ILL_TRL * l + 11);
     }
   } else if (!ill_pub<T>() && wg == ILL_R_BASE) {   // (16-row passes: REDUCE keeps the residual)

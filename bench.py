@@ -45,18 +45,18 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over single dispatches), each scaled by the
 # reading of a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (163,424.9 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 45d366b.
+# (163,349.8 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 4bcea3b.
 # Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 351_444_992
-# MFMA utilisation of the pass kernels (commit 45d366b) and of the prefill GEMMs, from
+TRAFFIC_BYTES_PER_STEP = 351_291_187
+# MFMA utilisation of the pass kernels and of the prefill kernels (commit 4bcea3b), from
 # rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
 MFMA_COUNTERS = {
-    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0109, "int8_TOPs": 47.3},
-    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0109, "int8_TOPs": 50.2},
-    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.143, "f16_TFLOPs": 360.3},
-    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.109, "f16_TFLOPs": 275.1},
-    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.042, "f16_TFLOPs": 105.3},
-    "prefill attention (512 rows)": {"mfma_busy": 0.060, "f16_TFLOPs": 150.5},
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 47.8},
+    "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0112, "int8_TOPs": 51.8},
+    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.141, "f16_TFLOPs": 354.1},
+    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.085, "f16_TFLOPs": 213.3},
+    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.031, "f16_TFLOPs": 77.4},
+    "prefill attention (512-row chunks)": {"mfma_busy": 0.070, "f16_TFLOPs": 176.4},
 }
 
 

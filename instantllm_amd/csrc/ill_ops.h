@@ -1125,8 +1125,12 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_combine_kernel(OpCtx c
 // the rule of the other attention kernels, and O += P V with P split the same way. A wave's
 // next chunk's keys and values stream in while one is evaluated.
 #define OP_RW 4
+// P round trip through LDS: rows of 68 floats, so that the row-strided writes (4 kg + j)
+// and the per-lane row reads (n) spread over the 64 banks (rows of 64 put a wave's 16 row
+// reads, and its 4 kg groups' writes, on the same banks)
+#define OP_PLD 68
 __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int layer, int M) {
-  __shared__ float pbw[OP_RW][16 * 64];
+  __shared__ __attribute__((aligned(16))) float pbw[OP_RW][16 * OP_PLD];
   __shared__ float sm_[OP_RW][16], sl_[OP_RW][16], so_[OP_RW][16][64];
   const OpHdr hd = op_hdr(c);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4, n = lane & 15;
@@ -1195,7 +1199,7 @@ __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int l
       }
       ls[j] = gsum<16>(sum);
 #pragma unroll
-      for (int b = 0; b < 4; b++) pb[(4 * kg + j) * 64 + 16 * b + n] = sc[b][j];
+      for (int b = 0; b < 4; b++) pb[(4 * kg + j) * OP_PLD + 16 * b + n] = sc[b][j];
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -1204,7 +1208,7 @@ __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int l
     for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const float p = pb[n * 64 + 32 * ks + 8 * kg + i];
+        const float p = pb[n * OP_PLD + 32 * ks + 8 * kg + i];
         const _Float16 hi = (_Float16)p;
         ph[ks][i] = hi;
         pl[ks][i] = (_Float16)(p - (float)hi);

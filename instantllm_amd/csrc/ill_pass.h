@@ -1868,8 +1868,9 @@ __device__ __forceinline__ bool role_lmh(const IllPassArgs& a, const PassHdr& H,
       tile = nxt;
     }
   }
+  constexpr int RPL = T >= 4 ? 4 : T;   // rows per lane: at T = 1 only j = 0 holds a row
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+  for (int j = 0; j < RPL; j++) {
     for (int o = 8; o >= 1; o >>= 1) {
       const float ov = __shfl_xor(bv[j], o, 64);
       const int oi = __shfl_xor(bi[j], o, 64);
@@ -1949,8 +1950,10 @@ __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, C
   // global argmax per row: reduced in each of the 4 waves that hold a row's partials, then
   // across them
   const int lane = i & 63, wv = i >> 6;
+  const int mmax = (nr + 1) >> 1;   // key[m] holds rows (i >> 8) + 2 m: only m < mmax are used
 #pragma unroll
   for (int m = 0; m < 8; m++) {
+    if (m >= mmax) break;   // (uniform; each 64-bit shuffle reduction is a chain of 12 ds_bpermutes)
     uint64_t k = key[m];
     for (int o = 32; o >= 1; o >>= 1) {
       const uint64_t ok2 = __shfl_xor(k, o, 64);

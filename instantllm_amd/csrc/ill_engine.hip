@@ -1561,8 +1561,11 @@ int ill_load_ildraft(ill_engine* e, const char* path) {
   // drafter (never a pointer to freed memory) and the new table is released
   uint8_t* tab = nullptr;
   int rc = ILL_OK;
-  if (hipStreamSynchronize(e->stream) != hipSuccess || hipMalloc((void**)&tab, t->blob.size()) != hipSuccess ||
+  const illd::HashIndex hx = illd::build_index(*t);
+  const size_t hoff = (t->blob.size() + 255) & ~(size_t)255;   // the indexes after the table
+  if (hipStreamSynchronize(e->stream) != hipSuccess || hipMalloc((void**)&tab, hoff + hx.bytes.size()) != hipSuccess ||
       hipMemcpy(tab, t->blob.data(), t->blob.size(), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(tab + hoff, hx.bytes.data(), hx.bytes.size(), hipMemcpyHostToDevice) != hipSuccess ||
       (!e->dtflg && hipMalloc((void**)&e->dtflg, ILD_VOCAB) != hipSuccess) ||
       hipMemcpy(e->dtflg, t->tflg.data(), ILD_VOCAB, hipMemcpyHostToDevice) != hipSuccess ||
       (!e->dreq && hipMalloc((void**)&e->dreq, sizeof(IllDraftReq)) != hipSuccess) ||
@@ -1582,7 +1585,7 @@ int ill_load_ildraft(ill_engine* e, const char* path) {
   }
   e->dtab = tab;
   e->ild = t;
-  e->dargs = illd::device_args(*t, e->dtab, e->dtflg, e->dreq);
+  e->dargs = illd::device_args(*t, e->dtab, e->dtflg, e->dreq, hx, e->dtab + hoff);
   return ILL_OK;
 }
 

@@ -9,8 +9,9 @@
 // candidates with 53 features and a small MLP.
 //
 // GPU shape: one workgroup of 1024 threads (16 waves). Per drafted token the waves split
-// the sources (wave 0 the six n-gram orders as a cooperative 11-ary search over the sorted
-// keys, 1 self-repetition, 2 prompt lookup, 3 the copy context, 4-11 two neighbours each),
+// the sources (wave 0 the six n-gram orders, ten lanes each, through a hash index of the
+// table's sorted keys built at load, 1 self-repetition, 2 prompt lookup, 3 the copy
+// context through the same kind of index, 4-11 two neighbours each),
 // then two threads per distinct candidate (in waves 0-7 and 8-15) write its 53 features to
 // LDS, and the scorer runs with one lane per hidden unit (16 or 32 lanes per candidate),
 // the hidden unit's and the linear term's sums advancing together. The candidate
@@ -65,6 +66,13 @@ struct IllDraftArgs {
   uint64_t ngky, ngvl, ngnx, cpc1, cpc2, mlp;   // byte offsets of the sections
   int32_t n_ngky, n_cpc1, n_cpc2;
   int32_t N, M, MAXM, H;
+  // Hash indexes of NGKY, CPC1 and CPC2 built when the table loads (ild_hfind): 2^bits
+  // slots of 32 B each, a slot holding the key and the entry's values, so a lookup is one
+  // round trip to memory instead of the sorted sections' search
+  const uint4* hng;
+  const uint4* hc1;
+  const uint4* hc2;
+  uint32_t bng, bc1, bc2;
 };
 
 __device__ __forceinline__ int ild_tail(int i) {
@@ -174,55 +182,24 @@ __device__ __forceinline__ uint64_t ild_max64(uint64_t v, int width) {
   return v;
 }
 
-// Wave-cooperative exact search of ascending keys: lanes in groups of G (group g = lanes
-// g*G .. g*G+G-1; lanes past the last full group idle) each search their own table
-// (per-lane base / stride / count / key; `wide` = 64-bit keys, else 32-bit). Each round the
-// G lanes probe G evenly spaced entries of the range [lo, hi) that holds the key if
-// present, and the ballot of (entry < key) cuts the range G + 1 ways; an equal entry ends
-// the search. Every lane of a group returns the key's index or -1. Call from all 64 lanes.
-__device__ int ild_wave_find(const uint8_t* base, int stride, int n, uint64_t key, bool wide, int G, bool active) {
-  const int lane = threadIdx.x & 63;
-  const int g = lane / G, gl = lane - g * G;
-  const bool in = active && (g + 1) * G <= 64;
-  const uint64_t gmask = in ? (((G >= 64) ? ~0ull : ((1ull << G) - 1)) << (g * G)) : 0ull;
-  int lo = 0, hi = in ? n : 0;
-  int found = -1;
-  for (int round = 0; round < 32; round++) {
-    const bool more = in && found < 0 && hi - lo > G;
-    if (!__any(more)) break;
-    bool less = false, eq = false;
-    int p = 0;
-    if (more) {
-      p = lo + (int)((int64_t)(hi - lo) * (gl + 1) / (G + 1));
-      const uint8_t* q = base + (size_t)p * stride;
-      const uint64_t v = wide ? *(const uint64_t*)q : (uint64_t)*(const uint32_t*)q;
-      less = v < key;
-      eq = v == key;
+// Open-addressing lookup in an index of 2^bits slots {key (u64), used, v0, v1, -, -, -}
+// built by illd::build_index (multiplicative hash, linear probing; the lowest entry of a key
+// when a section repeats it, as a lower-bound search finds). True with the entry's values.
+__device__ __forceinline__ uint64_t ild_hslot(uint64_t key, uint32_t bits) { return (key * 0x9E3779B97F4A7C15ull) >> (64 - bits); }
+__device__ bool ild_hfind(const uint4* slots, uint32_t bits, uint64_t key, uint32_t& v0, uint32_t& v1) {
+  const uint32_t mask = (1u << bits) - 1u;
+  uint32_t h = (uint32_t)ild_hslot(key, bits);
+  for (uint32_t probe = 0; probe <= mask; probe++) {
+    const uint4 a = slots[2 * h], b = slots[2 * h + 1];
+    if (a.z == 0u) return false;
+    if ((((uint64_t)a.y << 32) | a.x) == key) {
+      v0 = a.w;
+      v1 = b.x;
+      return true;
     }
-    const uint64_t bl = __ballot(less) & gmask, be = __ballot(eq) & gmask;
-    if (more) {
-      const int span = hi - lo;
-      if (be) {
-        const int j = __builtin_ctzll(be >> (g * G));
-        found = lo + (int)((int64_t)span * (j + 1) / (G + 1));
-      } else {
-        const int c = __popcll(bl);
-        const int nlo = c > 0 ? lo + (int)((int64_t)span * c / (G + 1)) + 1 : lo;
-        const int nhi = c < G ? lo + (int)((int64_t)span * (c + 1) / (G + 1)) : hi;
-        lo = nlo;
-        hi = nhi;
-      }
-    }
+    h = (h + 1u) & mask;
   }
-  bool hit = false;
-  if (in && found < 0 && gl < hi - lo) {
-    const uint8_t* q = base + (size_t)(lo + gl) * stride;
-    const uint64_t v = wide ? *(const uint64_t*)q : (uint64_t)*(const uint32_t*)q;
-    hit = v == key;
-  }
-  const uint64_t hb = __ballot(hit) & gmask;
-  if (found >= 0) return found;
-  return hb ? lo + __builtin_ctzll(hb >> (g * G)) : -1;
+  return false;
 }
 
 // float -> uint32 preserving order (so 64-bit keys (score, ~token) compare by score desc, token asc)
@@ -380,14 +357,14 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
         }
         key = h;
       }
-      const int idx = ild_wave_find(d.tab + d.ngky, 8, d.n_ngky, key, true, 10, act);
+      uint32_t vx = 0, vy = 0;
+      const bool hit = act && ild_hfind(d.hng, d.bng, key, vx, vy);   // NGVL's entry of the key
       int tot = -1, cnt = 0, etok = 0, ecnt = 0;
-      if (act && idx >= 0) {
-        const uint2 v = *(const uint2*)(d.tab + d.ngvl + (size_t)idx * 8);
-        tot = (int)v.x;
-        cnt = (int)(v.y & 7);
+      if (hit) {
+        tot = (int)vx;
+        cnt = (int)(vy & 7);
         if (gl < cnt) {
-          const uint2 e = *(const uint2*)(d.tab + d.ngnx + (size_t)((v.y >> 3) + gl) * 8);
+          const uint2 e = *(const uint2*)(d.tab + d.ngnx + (size_t)((vy >> 3) + gl) * 8);
           etok = (int)e.x;
           ecnt = (int)e.y;
           S.top_tok[n][gl] = etok;
@@ -481,11 +458,9 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     } else if (w == 3) {
       // copy context: rates after the last token (CPC1) and the last two (CPC2)
       const uint32_t c_1 = (uint32_t)ctx(L - 1), c_2 = (uint32_t)ctx(L - 2);
-      const bool lo32 = lane < 32;
-      const int idx = ild_wave_find(d.tab + (lo32 ? d.cpc1 : d.cpc2), lo32 ? 8 : 16, lo32 ? d.n_cpc1 : d.n_cpc2,
-                                    lo32 ? (uint64_t)c_1 : (((uint64_t)c_2 << 32) | c_1), !lo32, 32, true);
-      if (lane == 0) S.c1 = idx >= 0 ? *(const float*)(d.tab + d.cpc1 + (size_t)idx * 8 + 4) : 0.1f;
-      if (lane == 32) S.c2 = idx >= 0 ? *(const float*)(d.tab + d.cpc2 + (size_t)idx * 16 + 8) : 0.1f;
+      uint32_t rate = 0, unused = 0;
+      if (lane == 0) S.c1 = ild_hfind(d.hc1, d.bc1, (uint64_t)c_1, rate, unused) ? __uint_as_float(rate) : 0.1f;
+      if (lane == 32) S.c2 = ild_hfind(d.hc2, d.bc2, ((uint64_t)c_2 << 32) | c_1, rate, unused) ? __uint_as_float(rate) : 0.1f;
       // the first prompt token not in the window whose copy rate exceeds 0.3
       uint32_t fu = 0xffffffffu;
       for (int i = lane; i < S.R.np; i += 64)

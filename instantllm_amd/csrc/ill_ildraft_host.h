@@ -320,8 +320,67 @@ inline void prepare(Table& t, const int32_t* prompt, int n, const char* text, En
   r.nas = na;
 }
 
-// The device view of a table uploaded to `dtab` (DraftMeta, ILDraft.swift:73-80).
-inline IllDraftArgs device_args(const Table& t, const uint8_t* dtab, const uint8_t* dtflg, const IllDraftReq* dreq) {
+// Hash indexes of the three searched sections (the drafting kernel's ild_hfind): for each, a
+// power of two of 32-byte slots, at least twice the section's entries, each used slot
+// {key lo, key hi, 1, v0, v1, 0, 0, 0}: NGKY keys with their NGVL entry (total, count and
+// first continuation), CPC1 / CPC2 keys with their rate. Entries are inserted in section
+// order and a repeated key keeps its first entry. Offsets (bytes into `out`, 32-aligned) and
+// the bit counts are returned in the order NGKY, CPC1, CPC2.
+struct HashIndex {
+  std::vector<uint8_t> bytes;
+  uint64_t off[3];
+  uint32_t bits[3];
+};
+inline uint32_t hash_slot(uint64_t key, uint32_t bits) { return (uint32_t)((key * 0x9E3779B97F4A7C15ull) >> (64 - bits)); }
+inline HashIndex build_index(const Table& t) {
+  HashIndex hx;
+  const char* tags[3] = {"NGKY", "CPC1", "CPC2"};
+  for (int k = 0; k < 3; k++) {
+    const Section& x = t.s(tags[k]);
+    uint32_t bits = 4;
+    while ((1ull << bits) < 2ull * x.cnt) bits++;
+    const uint64_t nslot = 1ull << bits;
+    hx.off[k] = hx.bytes.size();
+    hx.bits[k] = bits;
+    hx.bytes.resize(hx.bytes.size() + 32 * nslot, 0);
+    uint32_t* sl = (uint32_t*)(hx.bytes.data() + hx.off[k]);
+    for (uint64_t i = 0; i < x.cnt; i++) {
+      uint64_t key;
+      uint32_t v0, v1 = 0;
+      if (k == 0) {
+        key = t.at<uint64_t>(x.off + 8 * i);
+        v0 = t.at<uint32_t>(t.s("NGVL").off + 8 * i);
+        v1 = t.at<uint32_t>(t.s("NGVL").off + 8 * i + 4);
+      } else if (k == 1) {
+        key = t.at<uint32_t>(x.off + 8 * i);
+        v0 = t.at<uint32_t>(x.off + 8 * i + 4);
+      } else {
+        key = t.at<uint64_t>(x.off + 16 * i);
+        v0 = t.at<uint32_t>(x.off + 16 * i + 8);
+      }
+      uint32_t hs = hash_slot(key, bits);
+      for (;;) {
+        uint32_t* e = sl + 8 * (uint64_t)hs;
+        if (e[2] == 0) {
+          e[0] = (uint32_t)key;
+          e[1] = (uint32_t)(key >> 32);
+          e[2] = 1;
+          e[3] = v0;
+          e[4] = v1;
+          break;
+        }
+        if (((uint64_t)e[1] << 32 | e[0]) == key) break;   // a repeated key keeps its first entry
+        hs = (hs + 1) & (uint32_t)(nslot - 1);
+      }
+    }
+  }
+  return hx;
+}
+
+// The device view of a table uploaded to `dtab` (DraftMeta, ILDraft.swift:73-80), its hash
+// indexes uploaded to `dhash` (HashIndex::bytes).
+inline IllDraftArgs device_args(const Table& t, const uint8_t* dtab, const uint8_t* dtflg, const IllDraftReq* dreq,
+                                const HashIndex& hx, const uint8_t* dhash) {
   IllDraftArgs a{};
   a.tab = dtab;
   a.tflg = dtflg;
@@ -339,6 +398,12 @@ inline IllDraftArgs device_args(const Table& t, const uint8_t* dtab, const uint8
   a.M = (int32_t)t.M;
   a.MAXM = (int32_t)t.MAXM;
   a.H = (int32_t)t.H;
+  a.hng = (const uint4*)(dhash + hx.off[0]);
+  a.hc1 = (const uint4*)(dhash + hx.off[1]);
+  a.hc2 = (const uint4*)(dhash + hx.off[2]);
+  a.bng = hx.bits[0];
+  a.bc1 = hx.bits[1];
+  a.bc2 = hx.bits[2];
   return a;
 }
 

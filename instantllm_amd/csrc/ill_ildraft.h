@@ -27,6 +27,7 @@
 #define ILD_NBSEQ 80
 #define ILD_MAXAS 1024
 #define ILD_NF 53
+#define ILD_FS 56                // LDS row stride of the feature rows (16-byte rows for vector reads)
 #define ILD_MAXH 32
 #define ILD_W1S 57               // LDS row stride of W1 (odd: the lanes of 16 hidden units hit distinct banks)
 #define ILD_THREADS 1024
@@ -82,7 +83,8 @@ __device__ __forceinline__ int ild_tail(int i) {
 struct IldLds {
   IllDraftReq R;
   float w1[ILD_MAXH * ILD_W1S];
-  float b1[ILD_MAXH], w2[ILD_MAXH], wl[ILD_W1S];
+  float b1[ILD_MAXH], w2[ILD_MAXH];
+  alignas(16) float wl[ILD_W1S];
   float b2;
   float lg1p[ILD_LG1P];      // ln(1 + c) of the counts c < ILD_LG1P
   int ob[ILD_OB];
@@ -92,7 +94,7 @@ struct IldLds {
   uint64_t ckey[ILD_NRAW];
   float csc[ILD_NRAW];
   int ctf[ILD_NRAW];         // '`' count of each candidate
-  float F[ILD_NRAW * ILD_NF]; // feature rows
+  alignas(16) float F[ILD_NRAW * ILD_FS];   // feature rows (ILD_NF used of ILD_FS)
   int pm[ILD_MAXP];
   // phase A results
   int dist_tot[8], dist_cnt[8], top_tok[8][8], top_cnt[8][8];
@@ -121,6 +123,7 @@ struct IldLds {
 };
 
 static_assert(ILD_HASH == ILD_THREADS, "the hash sets are cleared one slot per thread");
+static_assert(ILD_FS % 4 == 0 && ILD_FS >= ILD_NF && ILD_W1S >= ILD_FS, "vector reads of feature rows and linear weights");
 static_assert(sizeof(IllDraftReq) % 16 == 0, "the request is staged in 16-byte units");
 
 __device__ __forceinline__ uint32_t ild_hash(int key) { return ((uint32_t)key * 2654435761u) >> 22; }
@@ -200,6 +203,19 @@ __device__ bool ild_hfind(const uint4* slots, uint32_t bits, uint64_t key, uint3
     h = (h + 1u) & mask;
   }
   return false;
+}
+
+// sc + W2[hh] relu(a_hh) for hh = 0, 1, ..., H - 1 in that order, a_hh being lane hh's value
+// of this lane's row of 16 (DPP row_newbcast: no LDS round trip per unit).
+template <int HH>
+__device__ __forceinline__ void ild_w2_terms(float& sc, float acc, const float* w2, int H) {
+  if constexpr (HH < 16) {
+    if (HH < H) {
+      const float ah = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x150 + HH, 0xF, 0xF, false));
+      sc = sc + w2[HH] * fmaxf(ah, 0.f);
+    }
+    ild_w2_terms<HH + 1>(sc, acc, w2, H);
+  }
 }
 
 // float -> uint32 preserving order (so 64-bit keys (score, ~token) compare by score desc, token asc)
@@ -527,7 +543,7 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
     if ((tid & 511) < nu) {
       const int c = tid & 511;
       const int tok = S.uniq[c];
-      float* f = S.F + c * ILD_NF;
+      float* f = S.F + c * ILD_FS;
       if (tid < 512) {
         for (int i = 0; i < 29; ++i) f[i] = 0.f;
         f[0] = 1.f;
@@ -643,22 +659,35 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
       const int h = tid & (HL - 1), gbase = lane & ~(HL - 1);
       for (int c0 = 0; c0 < nu; c0 += ILD_THREADS / HL) {
         const int c = c0 + tid / HL;
-        const float* fr = S.F + min(c, nu - 1) * ILD_NF;
+        const float4* fr = (const float4*)(S.F + min(c, nu - 1) * ILD_FS);
+        const float4* wl = (const float4*)S.wl;
         // the hidden unit's chain and the linear term's chain advance together (two
-        // independent dependency chains in one loop; each keeps its own order)
+        // independent dependency chains in one loop; each keeps its own order); the feature
+        // row and the linear weights are read four at a time
         const float* wr = S.w1 + min(h, H - 1) * ILD_W1S;
         float acc = S.b1[min(h, H - 1)];
         float sc = S.b2;
-#pragma unroll 8
-        for (int i = 0; i < ILD_NF; ++i) {
-          const float x = fr[i];
-          acc = acc + wr[i] * x;
-          sc = sc + S.wl[i] * x;
+#pragma unroll 2
+        for (int i4 = 0; i4 < ILD_FS / 4; ++i4) {
+          const float4 x4 = fr[i4], l4 = wl[i4];
+          const float xs[4] = {x4.x, x4.y, x4.z, x4.w}, ls[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int i = 4 * i4 + q;
+            if (i < ILD_NF) {
+              acc = acc + wr[i] * xs[q];
+              sc = sc + ls[q] * xs[q];
+            }
+          }
         }
         if (h >= H) acc = 0.f;
-        for (int hh = 0; hh < H; ++hh) {
-          const float ah = __shfl(acc, gbase + hh, 64);
-          sc = sc + S.w2[hh] * fmaxf(ah, 0.f);
+        if (HL == 16) {   // a candidate's 16 lanes are a DPP row: row_newbcast hands lane hh's unit to all
+          ild_w2_terms<0>(sc, acc, S.w2, H);
+        } else {
+          for (int hh = 0; hh < H; ++hh) {
+            const float ah = __shfl(acc, gbase + hh, 64);
+            sc = sc + S.w2[hh] * fmaxf(ah, 0.f);
+          }
         }
         if (h == 0 && c < nu) {
           const uint64_t key = ((uint64_t)ild_fkey(sc) << 32) | (uint64_t)(0xffffffffu - (uint32_t)S.uniq[c]);
@@ -753,21 +782,23 @@ __global__ __launch_bounds__(ILD_THREADS) void ill_ildraft_kernel(IllPassArgs a,
               S.tr_cum[i] = cum;
               const int expand = !(tkn == eos0 || tkn == eos1 || i + 1 == K + 1);
               if (expand) {
-                int r = i, dpos = S.tr_dep[i], tk2 = S.ticks0;
-                while (r > 0) {
-                  S.ob[base + dpos - 1] = S.tr_tok[r];
-                  tk2 += S.tr_tf[r];
-                  dpos--;
-                  r = S.tr_par[r];
-                }
                 S.depth = S.tr_dep[i];
                 S.erow = i;
-                S.ticks = tk2;
               }
               S.flag = expand;
             }
             ild_wave_sync();
             if (S.flag) {
+              // the expanded row's path into the window: its rows j > 0 are the set bits of
+              // tr_anc (one lane each), row j's token at depth tr_dep[j]; the ticks add theirs
+              const uint32_t anc = S.tr_anc[S.erow];
+              int tf = 0;
+              if (lane > 0 && lane < 32 && ((anc >> lane) & 1u)) {
+                S.ob[base + S.tr_dep[lane] - 1] = S.tr_tok[lane];
+                tf = S.tr_tf[lane];
+              }
+              tf = gsumi<64>(tf);
+              if (lane == 0) S.ticks = S.ticks0 + tf;
               go = 1;
               break;
             }

@@ -2268,6 +2268,11 @@ __global__ __launch_bounds__(ILL_WG_THREADS, 1) void ill_pass_kernel(IllPassArgs
   extern __shared__ __attribute__((aligned(16))) uint8_t ill_stage[];   // ILL_STAGE_BYTES (dynamic)
   __shared__ PassHdr H;
   trace_mark(a, ILL_TR_TAIL + 8);
+  // the kernel arguments the header and the first weight stage use, read in one batch of
+  // scalar loads before the header (left to the compiler, they came in several dependent
+  // rounds: 1 us per step; adding the arguments the roles use next measured slower)
+  asm volatile("" ::"s"(a.st), "s"(a.ctl), "s"(a.ptoks), "s"(a.tree), "s"(a.L0.wqkv), "s"(a.L0.sqkv), "s"(a.L0.wo),
+               "s"(a.L0.so), "s"(a.L0.wgu), "s"(a.L0.sgu), "s"(a.L0.wd), "s"(a.L0.sd));
   load_hdr(a, H);
   trace_mark(a, ILL_TR_TAIL + 9);
   if (H.done) return;

@@ -319,8 +319,9 @@ def layer_trace(e, prompt: list[int], steps: int) -> dict:
     per-workgroup timestamps (100 MHz device clock). Per layer (medians over layers 2-21,
     us from the attention workgroup 0's layer start): the stages of the ATT (workgroups
     0-13) and GUD (16-91) roles; the tail (final norm, lm_head, commit) from the last
-    layer's start; the step's in-kernel span against the graph's per-step time, with and
-    without the trace."""
+    layer's start; the kernel's edges (workgroups entering, the pass header loaded, the
+    first layer's start, the commit, workgroups leaving) from the first entry; the step's
+    in-kernel span against the graph's per-step time, with and without the trace."""
     no_eos = (-5, -5)
 
     def replay(trace: bool) -> float:

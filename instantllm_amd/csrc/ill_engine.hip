@@ -1562,6 +1562,10 @@ int ill_load_ildraft(ill_engine* e, const char* path) {
   uint8_t* tab = nullptr;
   int rc = ILL_OK;
   const illd::HashIndex hx = illd::build_index(*t);
+  if (hx.bytes.empty()) {
+    delete t;
+    return fail(ILL_E_FILE, "learned drafter table too large to index (a section of more than 2^27 entries)");
+  }
   const size_t hoff = (t->blob.size() + 255) & ~(size_t)255;   // the indexes after the table
   if (hipStreamSynchronize(e->stream) != hipSuccess || hipMalloc((void**)&tab, hoff + hx.bytes.size()) != hipSuccess ||
       hipMemcpy(tab, t->blob.data(), t->blob.size(), hipMemcpyHostToDevice) != hipSuccess ||

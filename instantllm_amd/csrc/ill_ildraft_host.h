@@ -339,6 +339,11 @@ inline HashIndex build_index(const Table& t) {
     const Section& x = t.s(tags[k]);
     uint32_t bits = 4;
     while ((1ull << bits) < 2ull * x.cnt) bits++;
+    if (bits > 28) {   // 2^28 slots (8 GiB) at most: a larger section is refused by the loader
+      hx.bits[k] = 0;
+      hx.bytes.clear();
+      return hx;
+    }
     const uint64_t nslot = 1ull << bits;
     hx.off[k] = hx.bytes.size();
     hx.bits[k] = bits;

@@ -484,15 +484,15 @@ def main() -> int:
     tree = random_tree(vr, 16, F.VOCAB)
     tree[33] = int(e.out_tokens()[st["step"] - 1])
     verify_us = []
-    for _ in range(5):
+    for _ in range(15):   # single launches: the median of 15 (a pass varies by about 10 us)
         e.set_state(pos=st["pos"], n=16, maxsteps=64, eos=no_eos)
         e.verify_pass(16, tree=tree)
         verify_us.append(e.last_pass_ms() * 1e3)
-    # 4-row chain pass (the 4-row instantiation; the reference's default speculative pass
-    # has 3 rows) at the same prefix: the last token and three drafts
+    # 4-row chain pass (passes of 3-4 rows run on the 16-row instantiation; the reference's
+    # default speculative pass has 3 rows) at the same prefix: the last token and three drafts
     chain = [int(tree[33])] + [int(t) for t in vr.integers(0, F.VOCAB, size=3)]
     verify4_us = []
-    for _ in range(5):
+    for _ in range(15):
         e.set_state(pos=st["pos"], n=4, maxsteps=64, eos=no_eos)
         e.verify_pass(4, toks=chain)
         verify4_us.append(e.last_pass_ms() * 1e3)

@@ -287,6 +287,37 @@ ILL_API int ill_gemv_destroy(ill_gemv* g);
 ILL_API int ill_quantize_q4(const float* w, int64_t rows, int cols, uint8_t* packed, uint16_t* sb, int threads);
 ILL_API int ill_quantize_q8(const float* w, int64_t rows, int cols, int group, int8_t* codes, uint16_t* scales, int threads);
 
+/* The tokenizer (Sources/Tokenizer: Tokenizer.swift, Core.swift; host code, no GPU):
+ * Qwen2 byte-level BPE, equal to Hugging Face `tokenizers` on the same tokenizer.json.
+ * `python -m instantllm_amd.tokenizer compile tokenizer.json out.iltk` writes the file
+ * (Tokenizer.compile, Compile.swift:14-371) that ill_tok_open maps (Tokenizer(path:),
+ * Tokenizer.swift:57-117). ill_tok_info: ids in total (vocabulary and added tokens), and the
+ * ids of <|im_start|>, <|im_end|>, <|endoftext|> (-1: absent).
+ * ill_tok_encode: `specials` 0 is Tokenizer.encode (:150-152, no added-token matching),
+ * 1 is encodeWithSpecials (:154-158, added tokens matched leftmost-longest on the raw text);
+ * ill_tok_encode_chat is encodeChat (:160-183, the chat template around system and user);
+ * ill_tok_decode is decode (:275-295: the tokens' bytes, ill-formed UTF-8 replaced by U+FFFD,
+ * ids without a token skipped); ill_tok_token_bytes is tokenBytes (:266-271, valid while
+ * the tokenizer is open); ill_tok_normalize and ill_tok_pretokenize are normalize and
+ * preTokenize (:299-323: the NFC text, and the end offsets of the pieces of an NFC text).
+ * Text arguments are UTF-8 of the given byte length (anything else: ILL_E_ARG). Output
+ * buffers hold `cap` entries; the count or length is always written, and when it exceeds
+ * cap the call fails with ILL_E_ARG. ill_tok_encode_cb is an ill_encode_fn over an ill_tok
+ * (the `user` argument): encodeWithSpecials of a NUL-terminated text, the first cap ids
+ * written and their whole count returned (0 for text that is not UTF-8). */
+typedef struct ill_tok ill_tok;
+ILL_API int ill_tok_open(const char* path, ill_tok** out);
+ILL_API int ill_tok_close(ill_tok* t);
+ILL_API int ill_tok_info(const ill_tok* t, int32_t info[4]);
+ILL_API int ill_tok_encode(const ill_tok* t, const char* text, int64_t len, int specials, int32_t* ids, int64_t cap, int64_t* n);
+ILL_API int ill_tok_encode_chat(const ill_tok* t, const char* system, int64_t slen, const char* user, int64_t ulen, int32_t* ids,
+                                int64_t cap, int64_t* n);
+ILL_API int ill_tok_decode(const ill_tok* t, const int32_t* ids, int64_t n, char* out, int64_t cap, int64_t* len);
+ILL_API int ill_tok_token_bytes(const ill_tok* t, int32_t id, const char** bytes, int64_t* len);
+ILL_API int ill_tok_normalize(const ill_tok* t, const char* text, int64_t len, char* out, int64_t cap, int64_t* olen);
+ILL_API int ill_tok_pretokenize(const ill_tok* t, const char* text, int64_t len, int64_t* ends, int64_t cap, int64_t* n);
+ILL_API int ill_tok_encode_cb(void* user, const char* text, int32_t* ids, int cap);
+
 #ifdef __cplusplus
 }
 #endif

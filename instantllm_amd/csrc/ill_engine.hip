@@ -25,6 +25,7 @@
 #include "ill_ops.h"
 #include "ill_quant.h"
 #include "ill_ildraft_host.h"
+#include "ill_tok.h"
 
 namespace {
 
@@ -1912,6 +1913,137 @@ int ill_gemv_info(const ill_gemv* g, int* slices, int* blocks_per_slice, int64_t
   if (blocks_per_slice) *blocks_per_slice = g->bps;
   if (bytes_per_copy) *bytes_per_copy = (int64_t)g->rows * g->K / 2 + (int64_t)g->rows * (g->K / 64) * 4;
   return ILL_OK;
+}
+
+// ---- tokenizer (host code; ill_tok.h) -----------------------------------------------------
+struct ill_tok {
+  iltk::Tok t;
+};
+
+namespace {
+int tok_ids_out(const std::vector<int32_t>& v, int32_t* ids, int64_t cap, int64_t* n) {
+  *n = (int64_t)v.size();
+  if ((int64_t)v.size() > cap) return fail(ILL_E_ARG, "%lld ids do not fit a buffer of %lld", (long long)v.size(), (long long)cap);
+  if (!v.empty()) memcpy(ids, v.data(), v.size() * 4);
+  return ILL_OK;
+}
+int tok_bytes_out(const std::string& s, char* out, int64_t cap, int64_t* len) {
+  *len = (int64_t)s.size();
+  if ((int64_t)s.size() > cap) return fail(ILL_E_ARG, "%lld bytes do not fit a buffer of %lld", (long long)s.size(), (long long)cap);
+  if (!s.empty()) memcpy(out, s.data(), s.size());
+  return ILL_OK;
+}
+bool tok_text_ok(const char* text, int64_t len) {
+  return len == 0 || (text && len > 0 && iltk::utf8_valid((const uint8_t*)text, (size_t)len));
+}
+}  // namespace
+
+int ill_tok_open(const char* path, ill_tok** out) {
+  if (!path || !out) return fail(ILL_E_ARG, "null tokenizer path or handle");
+  *out = nullptr;
+  ill_tok* t = new ill_tok();
+  const std::string err = iltk::open(path, t->t);
+  if (!err.empty()) {
+    delete t;
+    return fail(ILL_E_FILE, "%s", err.c_str());
+  }
+  *out = t;
+  return ILL_OK;
+}
+
+int ill_tok_close(ill_tok* t) {
+  delete t;
+  return ILL_OK;
+}
+
+int ill_tok_info(const ill_tok* t, int32_t info[4]) {
+  if (!t || !info) return fail(ILL_E_ARG, "null tokenizer");
+  info[0] = (int32_t)t->t.n_total;
+  info[1] = t->t.im_start;
+  info[2] = t->t.im_end;
+  info[3] = t->t.eot;
+  return ILL_OK;
+}
+
+int ill_tok_encode(const ill_tok* t, const char* text, int64_t len, int specials, int32_t* ids, int64_t cap, int64_t* n) {
+  if (!t || !n || (cap > 0 && !ids)) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  if (!tok_text_ok(text, len)) return fail(ILL_E_ARG, "text is not UTF-8");
+  std::vector<int32_t> v;
+  iltk::encode(t->t, (const uint8_t*)text, (size_t)len, specials != 0, v);
+  return tok_ids_out(v, ids, cap, n);
+}
+
+int ill_tok_encode_chat(const ill_tok* t, const char* system, int64_t slen, const char* user, int64_t ulen, int32_t* ids, int64_t cap,
+                        int64_t* n) {
+  if (!t || !n || (cap > 0 && !ids)) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  if (t->t.chat0.empty()) return fail(ILL_E_ARG, "the tokenizer has no <|im_start|> / <|im_end|> tokens");
+  if (!tok_text_ok(system, slen) || !tok_text_ok(user, ulen)) return fail(ILL_E_ARG, "text is not UTF-8");
+  std::string s = t->t.chat0;
+  s.append(system ? system : "", (size_t)slen);
+  s += t->t.chat1;
+  s.append(user ? user : "", (size_t)ulen);
+  s += t->t.chat2;
+  std::vector<int32_t> v;
+  iltk::encode(t->t, (const uint8_t*)s.data(), s.size(), true, v);
+  return tok_ids_out(v, ids, cap, n);
+}
+
+int ill_tok_decode(const ill_tok* t, const int32_t* ids, int64_t n, char* out, int64_t cap, int64_t* len) {
+  if (!t || !len || n < 0 || (n > 0 && !ids) || (cap > 0 && !out)) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  std::string raw;
+  for (int64_t i = 0; i < n; i++) {
+    const int32_t id = ids[i];
+    if (id < 0 || id >= t->t.n_total) continue;
+    raw.append((const char*)t->t.tok_bytes + t->t.tok_off[id], t->t.tok_off[id + 1] - t->t.tok_off[id]);
+  }
+  return tok_bytes_out(iltk::lossy_utf8((const uint8_t*)raw.data(), raw.size()), out, cap, len);
+}
+
+int ill_tok_token_bytes(const ill_tok* t, int32_t id, const char** bytes, int64_t* len) {
+  if (!t || !bytes || !len) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  if (id < 0 || id >= t->t.n_total) {
+    *bytes = "";
+    *len = 0;
+    return ILL_OK;
+  }
+  *bytes = (const char*)t->t.tok_bytes + t->t.tok_off[id];
+  *len = t->t.tok_off[id + 1] - t->t.tok_off[id];
+  return ILL_OK;
+}
+
+int ill_tok_normalize(const ill_tok* t, const char* text, int64_t len, char* out, int64_t cap, int64_t* olen) {
+  if (!t || !olen || (cap > 0 && !out)) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  if (!tok_text_ok(text, len)) return fail(ILL_E_ARG, "text is not UTF-8");
+  std::string s;
+  if (iltk::needs_nfc(t->t, (const uint8_t*)text, (size_t)len)) iltk::nfc(t->t, (const uint8_t*)text, (size_t)len, s);
+  else s.assign(text ? text : "", (size_t)len);
+  return tok_bytes_out(s, out, cap, olen);
+}
+
+int ill_tok_pretokenize(const ill_tok* t, const char* text, int64_t len, int64_t* ends, int64_t cap, int64_t* n) {
+  if (!t || !n || (cap > 0 && !ends)) return fail(ILL_E_ARG, "bad tokenizer arguments");
+  if (!tok_text_ok(text, len)) return fail(ILL_E_ARG, "text is not UTF-8");
+  std::vector<int64_t> v;
+  for (size_t i = 0; i < (size_t)len;) {
+    i = iltk::piece_end(t->t, (const uint8_t*)text, i, (size_t)len);
+    v.push_back((int64_t)i);
+  }
+  *n = (int64_t)v.size();
+  if (*n > cap) return fail(ILL_E_ARG, "%lld pieces do not fit a buffer of %lld", (long long)*n, (long long)cap);
+  if (!v.empty()) memcpy(ends, v.data(), v.size() * 8);
+  return ILL_OK;
+}
+
+int ill_tok_encode_cb(void* user, const char* text, int32_t* ids, int cap) {
+  const ill_tok* t = (const ill_tok*)user;
+  if (!t || !text || cap < 0 || (cap > 0 && !ids)) return 0;
+  const size_t len = strlen(text);
+  if (!iltk::utf8_valid((const uint8_t*)text, len)) return 0;
+  std::vector<int32_t> v;
+  iltk::encode(t->t, (const uint8_t*)text, len, true, v);
+  const size_t k = std::min<size_t>(v.size(), (size_t)cap);
+  if (k) memcpy(ids, v.data(), k * 4);
+  return (int)std::min<size_t>(v.size(), 0x7fffffff);
 }
 
 }  // extern "C"

@@ -37,9 +37,14 @@ DRAFT_REQ = np.dtype([("np", "<i4"), ("ncopy", "<i4"), ("nnb", "<i4"), ("nas", "
 
 
 def _encode_cb(encode):
-    """A C callback for `encode(text: str) -> list[int]` (None: no callback)."""
+    """(C callback, user pointer) for a tokenizer: an instantllm_amd.tokenizer.Tokenizer (the
+    library's own ill_tok_encode_cb on its handle), a function `encode(text: str) ->
+    list[int]`, or None (no callback)."""
     if encode is None:
-        return ENCODE_FN()
+        return ENCODE_FN(), None
+    if hasattr(encode, "encode_fn"):
+        fn, handle = encode.encode_fn
+        return ENCODE_FN(C.cast(fn, C.c_void_p).value), handle
 
     def cb(_user, text, ids, cap):
         try:
@@ -49,7 +54,7 @@ def _encode_cb(encode):
         for i, t in enumerate(got[:cap]):
             ids[i] = int(t)
         return len(got)
-    return ENCODE_FN(cb)
+    return ENCODE_FN(cb), None
 
 
 class IllError(RuntimeError):
@@ -122,6 +127,17 @@ def load_library(path: str | os.PathLike | None = None) -> C.CDLL:
         "ill_set_draft_context": (C.c_int, [P, ip, C.c_int, C.c_char_p, ENCODE_FN, P]),
         "ill_set_learned": (C.c_int, [P, C.c_int, C.c_int, C.c_int]),
         "ill_pending_pass": (C.c_int, [P, ip, ip, ip]),
+        "ill_tok_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "ill_tok_close": (C.c_int, [P]),
+        "ill_tok_info": (C.c_int, [P, ip]),
+        "ill_tok_encode": (C.c_int, [P, C.c_char_p, C.c_int64, C.c_int, ip, C.c_int64, C.POINTER(C.c_int64)]),
+        "ill_tok_encode_chat": (C.c_int, [P, C.c_char_p, C.c_int64, C.c_char_p, C.c_int64, ip, C.c_int64,
+                                          C.POINTER(C.c_int64)]),
+        "ill_tok_decode": (C.c_int, [P, ip, C.c_int64, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
+        "ill_tok_token_bytes": (C.c_int, [P, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.c_int64)]),
+        "ill_tok_normalize": (C.c_int, [P, C.c_char_p, C.c_int64, C.c_char_p, C.c_int64, C.POINTER(C.c_int64)]),
+        "ill_tok_pretokenize": (C.c_int, [P, C.c_char_p, C.c_int64, C.POINTER(C.c_int64), C.c_int64, C.POINTER(C.c_int64)]),
+        "ill_tok_encode_cb": (C.c_int, [P, C.c_char_p, ip, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -311,10 +327,11 @@ class Engine:
         self._check(self.lib.ill_load_ildraft(self.h, str(path).encode()))
 
     def set_draft_context(self, prompt_ids, text: str, encode=None):
-        """Engine.setDraftContext: the next generate_spec call drafts with the learned drafter."""
+        """Engine.setDraftContext: the next generate_spec call drafts with the learned drafter.
+        `encode`: the tokenizer (see _encode_cb)."""
         a = _i32(prompt_ids)
-        cb = _encode_cb(encode)
-        self._check(self.lib.ill_set_draft_context(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, None))
+        cb, user = _encode_cb(encode)
+        self._check(self.lib.ill_set_draft_context(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, user))
 
     def set_learned(self, use: bool = True, chain_rows: int = 8, tree_budget: int = 15):
         self._check(self.lib.ill_set_learned(self.h, int(use), chain_rows, tree_budget))
@@ -448,8 +465,8 @@ class DraftTable:
 
     def prepare(self, prompt_ids, text: str, encode=None) -> np.ndarray:
         a = _i32(prompt_ids)
-        cb = _encode_cb(encode)
-        rc = self.lib.ill_ildraft_prepare(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, None)
+        cb, user = _encode_cb(encode)
+        rc = self.lib.ill_ildraft_prepare(self.h, _ptr(a, C.c_int32), len(a), text.encode("utf-8"), cb, user)
         if rc != ILL_OK:
             raise IllError(rc, self.lib.ill_last_error().decode())
         n = self.lib.ill_ildraft_request(self.h, None, 0)

@@ -582,6 +582,12 @@ inline std::string open(const char* path, Tok& t) {
     if (t.uni_top[k] >= t.n_blocks) return std::string(path) + ": Unicode table out of range";
   for (int64_t k = 0; k < t.n_dec; k++)
     if ((t.dvals[k] >> 8) + (t.dvals[k] & 255) > (uint64_t)t.n_ddata) return std::string(path) + ": decomposition out of range";
+  // the code points NFC may write: scalar values only, so that its output is UTF-8
+  auto scalar = [](uint32_t c) { return c < 0x110000 && (c < 0xD800 || c > 0xDFFF); };
+  for (int64_t k = 0; k < t.n_ddata; k++)
+    if (!scalar(t.ddata[k])) return std::string(path) + ": decomposition holds a non-scalar code point";
+  for (int64_t k = 0; k < t.n_comp; k++)
+    if (!scalar(t.cvals[k])) return std::string(path) + ": composition holds a non-scalar code point";
   const uint64_t abytes = h[27] - h[26];
   for (int64_t k = 0; k < t.n_added; k++) {
     const uint32_t id = t.added[3 * k], off = t.added[3 * k + 1], l = t.added[3 * k + 2];

@@ -659,6 +659,9 @@ struct GudLds {
   float gu[8][T][16];
   uint4 ahi[4 * T], alo[4 * T];
   float2 dsc[T];
+  // T = 1: each wave's own coding of the SiLU row (wave w at [4 w], [w])
+  uint4 wahi[T == 1 ? 4 * ILL_WAVES : 1], walo[T == 1 ? 4 * ILL_WAVES : 1];
+  float2 wdsc[T == 1 ? ILL_WAVES : 1];
 };
 
 template <int T>
@@ -1649,6 +1652,26 @@ __device__ __forceinline__ bool role_gud(const IllPassArgs& a, const PassHdr& H,
   }
   lds_barrier();
   trace_mark(a, ILL_TRL * l + 4);
+  if constexpr (T == 1) {
+    // every wave codes the SiLU row itself (the arithmetic one wave would run for all) into
+    // its own LDS copy, so its down projection waits for no other wave
+    const int gi = lane >> 4, nn = lane & 15;
+    const float gv = G.gu[gi][0][nn], up = G.gu[4 + gi][0][nn];
+    uint4* ah = G.wahi + 4 * w;
+    uint4* al = G.walo + 4 * w;
+    float2* ds = G.wdsc + w;
+    quant_row64<1>(gv / (1.0f + expf(-gv)) * up, 0, ah, al, ds, lane);
+    wave_lds_sync();
+    trace_mark(a, ILL_TRL * l + 5);
+    split_gemv<T>(stage + ILL_ST_DOWN0 + w * ILL_ST_SPLIT, ah, al, ds, lane, nrows,
+                  acc_ptr(a, H.bank, l, ILL_KIND_XB + ub % xb_copies<T>(), 0) + acc_col(16 * 7 * w));
+    trace_mark(a, ILL_TRL * l + 10);
+    if (a.trace) {   // traced runs only: when this wave's contributions have landed
+      wait_vm();
+      trace_mark(a, ILL_TRL * l + 12);
+    }
+    return true;
+  }
   // SiLU(gate) * up for the block's 64 units; each row coded as one 64-wide group
   for (int t = w; t < T; t += ILL_WAVES) {
     if (t < nrows) {

@@ -40,6 +40,24 @@
 #define ILL_WG_THREADS 512   // 8 waves
 #define ILL_WAVES 8
 
+// K/V cache: per (layer, KV head), blocks of 64 slots of 4096 halves. Offsets in halves
+// from the (layer, head) base, in two layouts:
+//  - rows (the q4 engine, whose pass kernel reads 16 keys x 64 dims fragments for MFMA):
+//      K (slot s, dim d): s * 64 + d;  V (slot s, dim d): (s >> 6) * 4096 + d * 64 + (s & 63)
+//  - swizzled (q8 and f16, whose attention kernels give each lane one key or one dim):
+//    K dim-group major and V position-group major inside a block, so that 64 lanes reading
+//    16 bytes each for 64 consecutive slots (K: one key per lane, 8 dims) or 64 dims (V: one
+//    dim per lane, 8 positions) read 1 KB contiguous:
+//      K: (s >> 6) * 4096 + ((d >> 3) * 64 + (s & 63)) * 8 + (d & 7)
+//      V: (s >> 6) * 4096 + (((s & 63) >> 3) * 64 + d) * 8 + (s & 7)
+__host__ __device__ inline size_t kv_k_off(int s, int d, bool swz) {
+  return swz ? (size_t)(s >> 6) * 4096 + (size_t)((((d >> 3) << 6) + (s & 63)) << 3) + (d & 7) : (size_t)s * 64 + d;
+}
+__host__ __device__ inline size_t kv_v_off(int s, int d, bool swz) {
+  return swz ? (size_t)(s >> 6) * 4096 + (size_t)((((s & 63) >> 3 << 6) + d) << 3) + (s & 7)
+             : (size_t)(s >> 6) * 4096 + d * 64 + (s & 63);
+}
+
 // State: the reference's 16-int control block (Shaders.swift:37-54), same field order.
 struct IllState {
   int32_t pos, n, step, done, maxctx, maxsteps, eos0, eos1;

@@ -422,7 +422,7 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     const OpLayerW& L = e->holayers[l];
     if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);
     op_gemm<FMT, OP_QKV>(e, c.xn, L.qkv, M, l, nullptr);
-    if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel, dim3((M + 15) / 16, ILL_NH), dim3(64 * OP_RW), 0, s, c, l, M);
+    if (M > 16) hipLaunchKernelGGL(op_attn_rows_kernel<FMT != 2>, dim3((M + 15) / 16, ILL_NH), dim3(64 * OP_RW), 0, s, c, l, M);
     else {
       float* op1 = ofuse && nsplit == 1 ? opart_o : nullptr;
       hipLaunchKernelGGL(op_attn_kernel<FMT>, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart,
@@ -454,7 +454,7 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((lm_rows + 3) / 4), dim3(256), 0, s, c, c.fnorm, M - lm_rows, lm_rows);
     op_gemm<FMT, OP_LMH>(e, c.xn, c.emb, lm_rows, 0, nullptr);
   }
-  hipLaunchKernelGGL(op_commit_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, s, e->args, (const uint64_t*)c.amax, e->vocab / OP_BN);
+  hipLaunchKernelGGL(op_commit_kernel, dim3(1), dim3(ILL_WG_THREADS), 0, s, e->args, (const uint64_t*)c.amax, e->vocab / OP_BN, c.kvswz);
 }
 
 void op_seq_fmt(ill_engine* e, int M, int lm_rows) {
@@ -784,6 +784,7 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
   oc.rope = e->rope;
   oc.kc = e->kc;
   oc.vt = e->vt;
+  oc.kvswz = e->fmt != 2 ? 1 : 0;
   oc.logits = e->logits;
   oc.maxctx = e->maxctx;
   oc.layers = layers;
@@ -1151,19 +1152,22 @@ int ill_read_logits(ill_engine* e, int row, float* out) {
   return ILL_OK;
 }
 
-// reference cache layout [layer][kvh][npos][64]; the engine keeps K in that layout (with
-// maxctx rows) and V transposed per 64 slots.
+// reference cache layout [layer][kvh][npos][64]; the engine keeps K and V in blocks of 64
+// slots, in rows (q4) or swizzled (q8 / f16): kv_k_off / kv_v_off, ill_common.h.
 int ill_kv_copy_out(ill_engine* e, int npos, uint16_t* k, uint16_t* v) {
   if (!e || !k || !v || npos < 0 || npos > e->maxctx) return fail(ILL_E_ARG, "bad kv copy");
   HCK(hipStreamSynchronize(e->stream));
   const size_t per = (size_t)e->maxctx * 64;
+  const bool swz = e->fmt != 2;
   std::vector<uint16_t> kt(per), vtt(per);
   for (int lh = 0; lh < e->layers * ILL_NKV; lh++) {
     HCK(hipMemcpy(kt.data(), e->kc + lh * per, per * 2, hipMemcpyDeviceToHost));
     HCK(hipMemcpy(vtt.data(), e->vt + lh * per, per * 2, hipMemcpyDeviceToHost));
-    memcpy(k + (size_t)lh * npos * 64, kt.data(), (size_t)npos * 64 * 2);
     for (int p = 0; p < npos; p++)
-      for (int d = 0; d < 64; d++) v[((size_t)lh * npos + p) * 64 + d] = vtt[(size_t)(p >> 6) * 4096 + d * 64 + (p & 63)];
+      for (int d = 0; d < 64; d++) {
+        k[((size_t)lh * npos + p) * 64 + d] = kt[kv_k_off(p, d, swz)];
+        v[((size_t)lh * npos + p) * 64 + d] = vtt[kv_v_off(p, d, swz)];
+      }
   }
   return ILL_OK;
 }
@@ -1173,13 +1177,16 @@ int ill_kv_copy_in(ill_engine* e, int npos, const uint16_t* k, const uint16_t* v
   touch_cache(e);
   HCK(hipStreamSynchronize(e->stream));
   const size_t per = (size_t)e->maxctx * 64;
+  const bool swz = e->fmt != 2;
   std::vector<uint16_t> kt(per), vtt(per);
   for (int lh = 0; lh < e->layers * ILL_NKV; lh++) {
     HCK(hipMemcpy(kt.data(), e->kc + lh * per, per * 2, hipMemcpyDeviceToHost));
     HCK(hipMemcpy(vtt.data(), e->vt + lh * per, per * 2, hipMemcpyDeviceToHost));
-    memcpy(kt.data(), k + (size_t)lh * npos * 64, (size_t)npos * 64 * 2);
     for (int p = 0; p < npos; p++)
-      for (int d = 0; d < 64; d++) vtt[(size_t)(p >> 6) * 4096 + d * 64 + (p & 63)] = v[((size_t)lh * npos + p) * 64 + d];
+      for (int d = 0; d < 64; d++) {
+        kt[kv_k_off(p, d, swz)] = k[((size_t)lh * npos + p) * 64 + d];
+        vtt[kv_v_off(p, d, swz)] = v[((size_t)lh * npos + p) * 64 + d];
+      }
     HCK(hipMemcpy(e->kc + lh * per, kt.data(), per * 2, hipMemcpyHostToDevice));
     HCK(hipMemcpy(e->vt + lh * per, vtt.data(), per * 2, hipMemcpyHostToDevice));
   }

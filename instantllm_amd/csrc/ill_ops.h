@@ -59,6 +59,7 @@ struct OpCtx {
   uint64_t* amax;        // [V/128][16] argmax keys of the lm_head tiles
   float* logits;         // [16][V]
   int maxctx, layers, vocab;
+  int kvswz;             // K/V cache layout: 1 swizzled (q8 / f16), 0 rows (q4; ill_common.h)
 };
 
 // What the kernels need from the State and the control block, read once at kernel entry
@@ -261,13 +262,13 @@ __device__ __forceinline__ void epi_qkv(const OpCtx& c, const OpHdr& hd, int lay
     c.q[(size_t)m * ILL_H + head * 64 + d] = x0;
     c.q[(size_t)m * ILL_H + head * 64 + d + 32] = x1;
   } else if (head < ILL_NH + ILL_NKV) {
-    uint16_t* kr = c.kc + (((size_t)layer * ILL_NKV + (head - ILL_NH)) * c.maxctx + slot) * 64;
-    kr[d] = (uint16_t)f2h(x0);
-    kr[d + 32] = (uint16_t)f2h(x1);
+    uint16_t* kb = c.kc + ((size_t)layer * ILL_NKV + (head - ILL_NH)) * c.maxctx * 64;
+    kb[kv_k_off(slot, d, c.kvswz)] = (uint16_t)f2h(x0);
+    kb[kv_k_off(slot, d + 32, c.kvswz)] = (uint16_t)f2h(x1);
   } else {
-    uint16_t* vb = c.vt + (((size_t)layer * ILL_NKV + (head - ILL_NH - ILL_NKV)) * (c.maxctx / 64) + slot / 64) * 4096;
-    vb[d * 64 + (slot & 63)] = (uint16_t)f2h_sat(x0);
-    vb[(d + 32) * 64 + (slot & 63)] = (uint16_t)f2h_sat(x1);
+    uint16_t* vb = c.vt + ((size_t)layer * ILL_NKV + (head - ILL_NH - ILL_NKV)) * (c.maxctx / 64) * 4096;
+    vb[kv_v_off(slot, d, c.kvswz)] = (uint16_t)f2h_sat(x0);
+    vb[kv_v_off(slot, d + 32, c.kvswz)] = (uint16_t)f2h_sat(x1);
   }
 }
 // gate/up rows in groups of 4: g[2q], g[2q+1], u[2q], u[2q+1] (Convert.swift:134-136)
@@ -861,6 +862,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   __shared__ __attribute__((aligned(16))) uint16_t vstage[ILL_WAVES][64 * OP_VST];   // tree passes: V rows
   __shared__ _Float16 aoh[64];   // with opart: the head's output, the O projection's input
   const OpHdr hd = op_hdr(c);
+  constexpr bool SWZ = FMT != 2;   // the cache layout of the q8 / f16 engines (ill_common.h)
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rh = blockIdx.x / nsplit, j = blockIdx.x % nsplit;
   const int t = rh / ILL_NH, h = rh % ILL_NH, g = h / 7;
@@ -878,12 +880,11 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   uint4 kv[8], vv[8];
   const int ch0 = 16 * j + w;
   {
-    const uint4* kr = (const uint4*)(kb + (size_t)min(64 * ch0 + lane, c.maxctx - 1) * 64);
-    const uint4* vr = (const uint4*)(vb + ((size_t)min(ch0, c.maxctx / 64 - 1) * 64 + lane) * 64);
+    const int ks = min(64 * ch0 + lane, c.maxctx - 1), vc = min(ch0, c.maxctx / 64 - 1);
 #pragma unroll
-    for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
+    for (int i = 0; i < 8; i++) kv[i] = gld((const uint4*)(kb + kv_k_off(ks, 8 * i, SWZ)));
 #pragma unroll
-    for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
+    for (int i = 0; i < 8; i++) vv[i] = gld((const uint4*)(vb + kv_v_off(64 * vc + 8 * i, lane, SWZ)));
   }
   const int pos = hd.pos;
   const bool tree = hd.mode == ILL_MODE_TREE;
@@ -892,16 +893,14 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
   const int nch = (L + 63) >> 6;
   const int nne = min(OP_NSPLIT, (nch + 15) >> 4);   // splits 0 .. nne - 1 hold chunks
   // chunk ch: the K row of position 64 ch + lane (slot remapped along the path in tree
-  // passes) and the transposed V row of dim = lane
+  // passes) and the V values of dim = lane
   auto fetch = [&](int ch, uint4 (&kv)[8], uint4 (&vv)[8]) {
     const int vp = 64 * ch + lane;
     const int slot = min(vp < pos || !tree ? vp : pos + path[min(max(vp - pos, 0), 15)], c.maxctx - 1);
-    const uint4* kr = (const uint4*)(kb + (size_t)slot * 64);
 #pragma unroll
-    for (int i = 0; i < 8; i++) kv[i] = gld(kr + i);
-    const uint4* vr = (const uint4*)(vb + ((size_t)ch * 64 + lane) * 64);
+    for (int i = 0; i < 8; i++) kv[i] = gld((const uint4*)(kb + kv_k_off(slot, 8 * i, SWZ)));
 #pragma unroll
-    for (int i = 0; i < 8; i++) vv[i] = gld(vr + i);
+    for (int i = 0; i < 8; i++) vv[i] = gld((const uint4*)(vb + kv_v_off(64 * ch + 8 * i, lane, SWZ)));
   };
   const bool early = j < nne && ch0 < nch && (!tree || 64 * ch0 + 63 < pos);
   qs[w][lane] = qv * 0.125f;
@@ -967,7 +966,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_kernel(OpCtx c, int la
           const int pp = p0 + k;
           if (pp < p1) {
             const int sl2 = pos + path[64 * ch + pp - pos];
-            pv[k] = gld(vb + ((size_t)(sl2 >> 6) * 64 + lane) * 64 + (sl2 & 63));
+            pv[k] = gld(vb + kv_v_off(sl2, lane, SWZ));
           }
         }
 #pragma unroll
@@ -1129,6 +1128,7 @@ __global__ __launch_bounds__(64 * ILL_WAVES) void op_attn_combine_kernel(OpCtx c
 // and the per-lane row reads (n) spread over the 64 banks (rows of 64 put a wave's 16 row
 // reads, and its 4 kg groups' writes, on the same banks)
 #define OP_PLD 68
+template <bool SWZ>   // the K/V cache layout (ill_common.h): swizzled for q8 / f16, rows for q4
 __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int layer, int M) {
   __shared__ __attribute__((aligned(16))) float pbw[OP_RW][16 * OP_PLD];
   __shared__ float sm_[OP_RW][16], sl_[OP_RW][16], so_[OP_RW][16][64];
@@ -1169,11 +1169,11 @@ __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int l
     for (int nb = 0; nb < 4; nb++) O[nb][j] = 0.f;
   }
   KVFrag f;
-  if (w < nch) kv_fetch(kbase, vbase, w, lane, f);
+  if (w < nch) kv_fetch<SWZ>(kbase, vbase, w, lane, f);
   for (int ch = w; ch < nch; ch += OP_RW) {
     KVFrag fn;
     const bool more = ch + OP_RW < nch;
-    if (more) kv_fetch(kbase, vbase, ch + OP_RW, lane, fn);
+    if (more) kv_fetch<SWZ>(kbase, vbase, ch + OP_RW, lane, fn);
     float sc[4][4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
@@ -1271,7 +1271,7 @@ __global__ __launch_bounds__(64 * OP_RW) void op_attn_rows_kernel(OpCtx c, int l
 // ---- commit ----------------------------------------------------------------------------
 // Global argmax of rows lmh0 .. lmh0 + lmhn - 1 over the lm_head tiles, then the same
 // commit as the pass kernel (greedy, chain or tree accept, KV compaction, State advance).
-__global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a, const uint64_t* amax, int ntiles) {
+__global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a, const uint64_t* amax, int ntiles, int kvswz) {
   __shared__ PassHdr H;
   __shared__ CommitLds C;
   __shared__ uint64_t best[ILL_WAVES];
@@ -1299,5 +1299,5 @@ __global__ __launch_bounds__(ILL_WG_THREADS) void op_commit_kernel(IllPassArgs a
     }
     __syncthreads();
   }
-  commit_apply(a, H, C, false, stopreq);
+  commit_apply(a, H, C, false, stopreq, kvswz != 0);
 }

@@ -789,8 +789,25 @@ struct KVFrag {
   uint4 v[4][2];
 };
 
+// SWZ: the cache in the swizzled layout of the q8 / f16 engines (ill_common.h; the same
+// fragments, read as 256-byte runs); the pass kernel's cache is in rows.
+template <bool SWZ = false>
 __device__ __forceinline__ void kv_fetch(const uint16_t* kbase, const uint16_t* vbase, int c, int lane, KVFrag& f) {
   const int kg = lane >> 4, n = lane & 15;
+  if constexpr (SWZ) {
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      f.k[b][0] = gld((const uint4*)(kbase + kv_k_off(64 * c + 16 * b + n, 8 * kg, true)));
+      f.k[b][1] = gld((const uint4*)(kbase + kv_k_off(64 * c + 16 * b + n, 32 + 8 * kg, true)));
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++)
+        f.v[nb][ks] = gld((const uint4*)(vbase + kv_v_off(64 * c + 32 * ks + 8 * kg, 16 * nb + n, true)));
+    }
+    return;
+  }
 #pragma unroll
   for (int b = 0; b < 4; b++) {
     const uint4* kr = (const uint4*)(kbase + (size_t)(64 * c + 16 * b + n) * 64);
@@ -1939,7 +1956,8 @@ __device__ __forceinline__ void zero_other_bank(const IllPassArgs& a, const Pass
 }
 
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq);
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq,
+                                             bool kvswz = false);
 // stop_word: the LDS copy of the host's stop word, loaded asynchronously by thread 0 when the
 // pass started (complete once thread 0 has waited for its first poll below).
 __device__ __forceinline__ void commit(const IllPassArgs& a, const PassHdr& H, CommitLds& C, const int& stop_word) {
@@ -2179,7 +2197,9 @@ __global__ __launch_bounds__(64) void ill_trunc_kernel(IllPassArgs a) {
 // pass kernel also advances the epoch and its accumulator-bank bookkeeping. The State is
 // read from the header (the snapshot taken at the start of the pass: only the commit
 // writes it during a pass), so the commit issues stores only.
-__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq) {
+// kvswz: the K/V cache is in the swizzled layout (q8 / f16 engines), else in rows.
+__device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr& H, CommitLds& C, bool pass_kernel, int stopreq,
+                                             bool kvswz) {
   const int i = tid_opaque();
   IllState* st = a.st;
   if (i == 0) {
@@ -2268,9 +2288,9 @@ __device__ __forceinline__ void commit_apply(const IllPassArgs& a, const PassHdr
     for (int j = i; j < NL * ILL_NKV * 64; j += ILL_WG_THREADS) {
       const int lh = j >> 6, d = j & 63;
       uint16_t* kb = a.kc + (size_t)lh * a.maxctx * 64;
-      kb[(size_t)dst * 64 + d] = kb[(size_t)src * 64 + d];
+      kb[kv_k_off(dst, d, kvswz)] = kb[kv_k_off(src, d, kvswz)];
       uint16_t* vb = a.vt + (size_t)lh * (a.maxctx / 64) * 4096;
-      vb[(size_t)(dst >> 6) * 4096 + d * 64 + (dst & 63)] = vb[(size_t)(src >> 6) * 4096 + d * 64 + (src & 63)];
+      vb[kv_v_off(dst, d, kvswz)] = vb[kv_v_off(src, d, kvswz)];
     }
     __syncthreads();
   }

@@ -50,8 +50,8 @@ struct IllPassArgs {
   int32_t* ptoks;          // [16] row tokens of the pass (commit writes [0] for the next step)
   int32_t* tree;           // [65] (written by the host or the learned drafter)
   const float2* rope;      // [maxctx + 16][32] (cos, sin)
-  uint16_t* kc;            // K cache [layer][kvh][maxctx][64] f16
-  uint16_t* vt;            // V cache transposed per 64 slots [layer][kvh][maxctx/64][64 dims][64] f16
+  uint16_t* kc;            // K cache [layer][kvh][maxctx][64] f16 (q8 / f16 engines: swizzled, ill_common.h)
+  uint16_t* vt;            // V cache transposed per 64 slots [layer][kvh][maxctx/64][64 dims][64] f16 (idem)
   uint64_t* acc;           // residual accumulators [bank 2][layer][A/B][16][896]
   uint64_t* lmp;           // [256][16][2] lm_head argmax partials (value, index)
   float* logits;           // [16][V]

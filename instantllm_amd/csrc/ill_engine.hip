@@ -426,10 +426,10 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
     else {
       float* op1 = ofuse && nsplit == 1 ? opart_o : nullptr;
       hipLaunchKernelGGL(op_attn_kernel<FMT>, dim3(M * ILL_NH * nsplit), dim3(64 * ILL_WAVES), 0, s, c, l, M, nsplit, e->opart,
-                         L.o, op1);
+                         L.oh, op1);
       if (nsplit > 1)
         hipLaunchKernelGGL(op_attn_combine_kernel<FMT>, dim3(M * ILL_NH), dim3(64 * ILL_WAVES), 0, s, c, (const float*)e->opart,
-                           L.o, ofuse ? opart_o : (float*)nullptr, M);
+                           L.oh, ofuse ? opart_o : (float*)nullptr, M);
       if (ofuse) {   // the residual + norm over the 14 per-head O partials (head order)
         OpGemmArgs g{};
         g.c = c;
@@ -664,9 +664,40 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
       place[id] = otot;
       otot += al256(size(id));
     }
+    // q8 / f16: W_o head-major for the attention-fused O projection (OpLayerW::oh)
+    const bool ohead = fmt != 2;
+    const int es = fmt == 0 ? 2 : 1, nchk = 64 * es / 16, qg = e->q8g;
+    const size_t ohw = (size_t)ILL_NH * nchk * ILL_H * 16, ohs = (size_t)ILL_NH * ILL_H * 4;
+    std::vector<size_t> p_ohw(layers, 0), p_ohs(layers, 0);
+    if (ohead)
+      for (int l = 0; l < layers; l++) {
+        p_ohw[l] = otot;
+        otot += al256(ohw);
+        p_ohs[l] = otot;
+        otot += al256(ohs);
+      }
     std::vector<uint8_t> oh(otot);
     for (int id = 0; id < count; id++)
       if (size(id)) memcpy(oh.data() + place[id], base + off(id), size(id));
+    if (ohead)
+      for (int l = 0; l < layers; l++) {
+        const int b = 3 + 12 * l;
+        if (size(b + 4) < (size_t)ILL_H * ILL_H * es || (fmt == 1 && size(b + 5) < (size_t)ILL_H * (ILL_H / qg) * 2))
+          return cleanup(fail(ILL_E_FILE, "layer %d: W_o tensors too small", l));
+        const uint8_t* wsrc = base + off(b + 4);
+        const uint16_t* ssrc = (const uint16_t*)(base + off(b + 5));
+        for (int h = 0; h < ILL_NH; h++)
+          for (int i = 0; i < nchk; i++)
+            for (int r = 0; r < ILL_H; r++)
+              memcpy(oh.data() + p_ohw[l] + (((size_t)h * nchk + i) * ILL_H + r) * 16, wsrc + ((size_t)r * ILL_H + 64 * h) * es + 16 * i, 16);
+        if (fmt == 1)
+          for (int h = 0; h < ILL_NH; h++)
+            for (int r = 0; r < ILL_H; r++) {
+              const uint32_t v = (uint32_t)ssrc[(size_t)r * (ILL_H / qg) + (64 * h) / qg] |
+                                 ((uint32_t)ssrc[(size_t)r * (ILL_H / qg) + (64 * h + 32) / qg] << 16);
+              memcpy(oh.data() + p_ohs[l] + ((size_t)h * ILL_H + r) * 4, &v, 4);
+            }
+      }
     if (hipMalloc(&e->oweights, otot) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights allocation failed (%zu B)", otot));
     if (hipMemcpy(e->oweights, oh.data(), otot, hipMemcpyHostToDevice) != hipSuccess) return cleanup(fail(ILL_E_HIP, "weights upload failed"));
     uint8_t* O = e->oweights;
@@ -685,6 +716,11 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
       OpLayerW& w = e->holayers[l];
       w.qkv = mk(b + 1, b + 2, ILL_QKV, ILL_H);
       w.o = mk(b + 4, b + 5, ILL_H, ILL_H);
+      w.oh = w.o;
+      if (ohead) {
+        w.oh.w = O + p_ohw[l];
+        w.oh.s = (const uint16_t*)(O + p_ohs[l]);
+      }
       w.gu = mk(b + 7, b + 8, 2 * ILL_FF, ILL_H);
       w.d = mk(b + 9, b + 10, ILL_H, ILL_FF);
       w.bqkv = (const float*)(O + place[b + 3]);

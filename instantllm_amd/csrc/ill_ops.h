@@ -35,6 +35,11 @@ struct OpMat {
 
 struct OpLayerW {
   OpMat qkv, o, gu, d;
+  // W_o again, head-major for the O projection folded into attention (q8 / f16): codes
+  // [head][16-byte column chunk][896 rows] (4 chunks q8, 8 f16), scales (q8) [head][896 rows]
+  // as u32 (scale of k 0-31 | scale of k 32-63 << 16), so that a lane per row reads
+  // consecutive 16 bytes
+  OpMat oh;
   const float* bqkv;
   const float* ln1;
   const float* ln2;
@@ -804,24 +809,19 @@ __device__ __forceinline__ void att_combine(const float* m, const float* l, cons
 template <int FMT>
 struct ORows {
   uint4 q[2][FMT == 0 ? 8 : 4];
-  uint16_t s[2][2];   // q8: the scales of k 0-31 and 32-63 (equal for group 64)
+  uint32_t s[2];   // q8: the scales of k 0-31 (low half) and 32-63 (high; equal for group 64)
 };
+// Woh: the head-major copy (OpLayerW::oh), so each load reads 1 KB contiguous over the lanes
 template <int FMT>
-__device__ __forceinline__ void orows_fetch(const OpMat& Wo, int h, int w, int lane, ORows<FMT>& o) {
+__device__ __forceinline__ void orows_fetch(const OpMat& Woh, int h, int w, int lane, ORows<FMT>& o) {
+  constexpr int NC = FMT == 0 ? 8 : 4;   // 16-byte chunks of a row's 64 columns
 #pragma unroll
   for (int u = 0; u < 2; u++) {
     const int r = min(112 * w + 64 * u + lane, ILL_H - 1);
-    if constexpr (FMT == 1) {
-      const uint4* src = (const uint4*)(Wo.w + (size_t)r * Wo.K + 64 * h);
+    const uint4* src = (const uint4*)Woh.w + (size_t)h * NC * ILL_H + r;
 #pragma unroll
-      for (int i = 0; i < 4; i++) o.q[u][i] = gld(src + i);
-      o.s[u][0] = gld(Wo.s + (size_t)r * (Wo.K / Wo.qg) + (64 * h) / Wo.qg);
-      o.s[u][1] = gld(Wo.s + (size_t)r * (Wo.K / Wo.qg) + (64 * h + 32) / Wo.qg);
-    } else {
-      const uint4* src = (const uint4*)(Wo.w + ((size_t)r * Wo.K + 64 * h) * 2);
-#pragma unroll
-      for (int i = 0; i < 8; i++) o.q[u][i] = gld(src + i);
-    }
+    for (int i = 0; i < NC; i++) o.q[u][i] = gld(src + (size_t)i * ILL_H);
+    if constexpr (FMT == 1) o.s[u] = gld((const uint32_t*)Woh.s + (size_t)h * ILL_H + r);
   }
 }
 template <int FMT>
@@ -839,7 +839,7 @@ __device__ __forceinline__ void orows_apply(const ORows<FMT>& o, const _Float16*
         const int k = PER * i + e;
         _Float16 wv;
         if constexpr (FMT == 1) {
-          const _Float16 sc = (_Float16)h2f(o.s[u][k >> 5]);
+          const _Float16 sc = (_Float16)h2f((uint16_t)(o.s[u] >> (16 * (k >> 5))));
           wv = sc * (_Float16)(float)(int8_t)((x[e >> 2] >> (8 * (e & 3))) & 0xff);
         } else {
           wv = __ushort_as_half((unsigned short)((x[e >> 1] >> (16 * (e & 1))) & 0xffff));

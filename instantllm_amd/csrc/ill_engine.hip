@@ -679,6 +679,31 @@ int ill_create(const char* path, int max_context, int max_pass, int max_steps, i
     std::vector<uint8_t> oh(otot);
     for (int id = 0; id < count; id++)
       if (size(id)) memcpy(oh.data() + place[id], base + off(id), size(id));
+    // q8 / f16: the matrices tiled for the GEMM kernels (op_wt_off / op_st_off, ill_ops.h)
+    auto tile = [&](int idw, int ids, int N, int K) {
+      const int es = fmt == 0 ? 2 : 1, unit = 16 / es;
+      if (N % 128 || K % 64 || size(idw) < (size_t)N * K * es || (fmt == 1 && size(ids) < (size_t)N * (K / qg) * 2)) return false;
+      const uint8_t* src = base + off(idw);
+      uint8_t* dst = oh.data() + place[idw];
+      for (int r = 0; r < N; r++)
+        for (int k = 0; k < K; k += unit) memcpy(dst + op_wt_off(r, k, K, es), src + ((size_t)r * K + k) * es, 16);
+      if (fmt == 1) {
+        const uint16_t* ss = (const uint16_t*)(base + off(ids));
+        uint16_t* sd = (uint16_t*)(oh.data() + place[ids]);
+        for (int r = 0; r < N; r++)
+          for (int g = 0; g < K / qg; g++) sd[op_st_off(r, g * qg, K, qg)] = ss[(size_t)r * (K / qg) + g];
+      }
+      return true;
+    };
+    if (fmt != 2) {
+      bool tiled = tile(0, 1, vocab, ILL_H);
+      for (int l = 0; l < layers && tiled; l++) {
+        const int b = 3 + 12 * l;
+        tiled = tile(b + 1, b + 2, ILL_QKV, ILL_H) && tile(b + 4, b + 5, ILL_H, ILL_H) && tile(b + 7, b + 8, 2 * ILL_FF, ILL_H) &&
+                tile(b + 9, b + 10, ILL_H, ILL_FF);
+      }
+      if (!tiled) return cleanup(fail(ILL_E_FILE, "a q8 / f16 matrix does not have the expected shape"));
+    }
     if (ohead)
       for (int l = 0; l < layers; l++) {
         const int b = 3 + 12 * l;

@@ -28,10 +28,32 @@
 #define ILL_OP_MAXM 512
 
 struct OpMat {
-  const uint8_t* w;    // q4: codes [N][K/2]; q8: int8 [N][K]; f16: [N][K]
-  const uint16_t* s;   // q4: [N][K/64][2] f16 (scale, min); q8: [N][K/qg] f16; f16: unused
+  const uint8_t* w;    // q4: codes [N][K/2]; q8: int8, f16: halves, both tiled (op_wt_off)
+  const uint16_t* s;   // q4: [N][K/64][2] f16 (scale, min); q8: f16 tiled (op_st_off); f16: unused
   int N, K, qg;        // qg: q8 group size (32 or 64)
 };
+
+// The q8 and f16 matrices of the layer-by-layer path are tiled, so that a wave's 16-byte
+// loads of one k-step (64 columns) read whole cache lines: 128-row blocks, k-steps, 16-row
+// sub-tiles of 16 x 64 weights, inside which 16-byte units are ordered (8-column half e,
+// 16-column group kg, row n). Element (r, k) of an N x K matrix of es-byte weights (N a
+// multiple of 128, K of 64) lies at byte op_wt_off:
+//   ((((r >> 7) * (K / 64) + (k >> 6)) * 8 + ((r & 127) >> 4)) * 64 es
+//    + ((e * 4 + kg) * 16 + (r & 15)) * 16 + (k & 7) * es)   with kg = (k & 63) >> 4,
+//   e = (k >> 3) & 1 for f16; for q8 a unit holds 16 columns (e = 0, (k & 15) bytes).
+// A lane (kg, n) of op_fetch_b then reads 1 KB contiguous with its wave, and a thread of
+// op_fetch_w (row, 32 columns) two 256-byte runs. q8 scales: [block][k-step][128 rows]
+// [64 / qg] (op_st_off).
+__host__ __device__ inline size_t op_wt_off(int r, int k, int K, int es) {
+  const size_t tile = ((size_t)(r >> 7) * (K >> 6) + (k >> 6)) * 8 + ((r & 127) >> 4);
+  const int kg = (k & 63) >> 4;
+  if (es == 1) return tile * 1024 + (size_t)((kg * 16 + (r & 15)) * 16 + (k & 15));
+  const int e = (k >> 3) & 1;
+  return tile * 2048 + (size_t)(((e * 4 + kg) * 16 + (r & 15)) * 16 + (k & 7) * 2);
+}
+__host__ __device__ inline size_t op_st_off(int r, int k, int K, int qg) {
+  return (((size_t)(r >> 7) * (K >> 6) + (k >> 6)) * 128 + (r & 127)) * (64 / qg) + ((k & 63) / qg);
+}
 
 struct OpLayerW {
   OpMat qkv, o, gu, d;
@@ -96,10 +118,10 @@ __device__ __forceinline__ float op_dequant1(const OpMat& m, int r, int k) {
     const uint32_t sm = *(const uint32_t*)(m.s + ((size_t)r * (m.K / 64) + k / 64) * 2);
     return h2f(sm & 0xffff) * q + h2f(sm >> 16);
   } else if constexpr (FMT == 1) {
-    const float q = (float)(int8_t)m.w[(size_t)r * m.K + k];
-    return h2f(m.s[(size_t)r * (m.K / m.qg) + k / m.qg]) * q;
+    const float q = (float)(int8_t)m.w[op_wt_off(r, k, m.K, 1)];
+    return h2f(m.s[op_st_off(r, k, m.K, m.qg)]) * q;
   } else {
-    return h2f(((const uint16_t*)m.w)[(size_t)r * m.K + k]);
+    return h2f(*(const uint16_t*)(m.w + op_wt_off(r, k, m.K, 2)));
   }
 }
 
@@ -178,14 +200,12 @@ __device__ __forceinline__ void op_fetch_w(const OpMat& W, int n0, int k0, int t
     r.b[0] = gld((const uint4*)(W.w + (size_t)row * (W.K / 2) + k0 / 2 + 16 * hf));
     r.sm = gld((const uint32_t*)(W.s + ((size_t)row * (W.K / 64) + k0 / 64) * 2));
   } else if constexpr (FMT == 1) {
-    const uint8_t* src = W.w + (size_t)row * W.K + k0 + 32 * hf;
-    r.b[0] = gld((const uint4*)src);
-    r.b[1] = gld((const uint4*)(src + 16));
-    r.sm = gld(W.s + (size_t)row * (W.K / W.qg) + (k0 + 32 * hf) / W.qg);
+    r.b[0] = gld((const uint4*)(W.w + op_wt_off(row, k0 + 32 * hf, W.K, 1)));
+    r.b[1] = gld((const uint4*)(W.w + op_wt_off(row, k0 + 32 * hf + 16, W.K, 1)));
+    r.sm = gld(W.s + op_st_off(row, k0 + 32 * hf, W.K, W.qg));
   } else {
-    const uint4* src = (const uint4*)(W.w + ((size_t)row * W.K + k0 + 32 * hf) * 2);
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.b[i] = gld(src + i);
+    for (int i = 0; i < 4; i++) r.b[i] = gld((const uint4*)(W.w + op_wt_off(row, k0 + 32 * hf + 8 * i, W.K, 2)));
   }
 }
 
@@ -538,12 +558,11 @@ __device__ __forceinline__ void op_fetch_b(const OpMat& W, int col0, int k0, int
       b.q[j][0] = make_uint4(v.x, v.y, 0u, 0u);
       b.s[j] = gld((const uint32_t*)(W.s + (row * (W.K / 64) + k / 64) * 2));
     } else if constexpr (FMT == 1) {
-      b.q[j][0] = gld((const uint4*)(W.w + row * W.K + k));
-      b.s[j] = gld(W.s + row * (W.K / W.qg) + k / W.qg);
+      b.q[j][0] = gld((const uint4*)(W.w + op_wt_off((int)row, k, W.K, 1)));
+      b.s[j] = gld(W.s + op_st_off((int)row, k, W.K, W.qg));
     } else {
-      const uint4* src = (const uint4*)(W.w + (row * W.K + k) * 2);
-      b.q[j][0] = gld(src);
-      b.q[j][1] = gld(src + 1);
+      b.q[j][0] = gld((const uint4*)(W.w + op_wt_off((int)row, k, W.K, 2)));
+      b.q[j][1] = gld((const uint4*)(W.w + op_wt_off((int)row, k + 8, W.K, 2)));
     }
   }
 }

@@ -53,10 +53,10 @@ TRAFFIC_BYTES_PER_STEP = 351_291_187
 MFMA_COUNTERS = {
     "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 47.8},
     "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0112, "int8_TOPs": 51.8},
-    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.141, "f16_TFLOPs": 355.7},
-    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.084, "f16_TFLOPs": 212.5},
-    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.030, "f16_TFLOPs": 74.6},
-    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.097, "f16_TFLOPs": 244.6},
+    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.147, "f16_TFLOPs": 371.0},
+    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.088, "f16_TFLOPs": 222.4},
+    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.031, "f16_TFLOPs": 77.7},
+    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.096, "f16_TFLOPs": 241.8},
 }
 
 

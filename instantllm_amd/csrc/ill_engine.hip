@@ -336,7 +336,11 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
         // QKV: 16-row tiles over the whole K and the epilogue in the GEMM (no partials and no
         // reduction kernel): 512 rows, f16, 13.9 us against 9.7 + 5.4 us split three ways
         g.ksteps = nsteps;
-        hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI, 4>), dim3(ntn, (M + 15) / 16, 1), dim3(256), 0, e->stream, g);
+        if constexpr (FMT != 2)   // q8 / f16: 32-row tiles streamed through the LDS ring
+          hipLaunchKernelGGL((op_gemm_ring_kernel<FMT, 32, EPI, OP_RING_ST(FMT, EPI)>), dim3(ntn, (M + 31) / 32, 1), dim3(256), 0,
+                             e->stream, g);
+        else
+          hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI, 4>), dim3(ntn, (M + 15) / 16, 1), dim3(256), 0, e->stream, g);
         return false;
       }
       const int mt = (M + 63) / 64;
@@ -345,7 +349,10 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
       g.ksteps = (nsteps + S - 1) / S;
       S = (nsteps + g.ksteps - 1) / g.ksteps;
       // the many-tile gate/up GEMM streams best with the one-step kernel (more per CU)
-      hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI, EPI == OP_SILU ? 1 : 4>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
+      if constexpr (FMT != 2)
+        hipLaunchKernelGGL((op_gemm_ring_kernel<FMT, 64, EPI, OP_RING_ST(FMT, EPI)>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
+      else
+        hipLaunchKernelGGL((op_gemm_kernel<FMT, 64, EPI, EPI == OP_SILU ? 1 : 4>), dim3(ntn, mt, S), dim3(256), 0, e->stream, g);
       if (S > 1) {
         if (EPI == OP_RESID && norm_gamma && W.N == ILL_H) {
           hipLaunchKernelGGL(op_epi_norm_kernel, dim3(M), dim3(ILL_H), 0, e->stream, g, S, norm_gamma, norm_row0);

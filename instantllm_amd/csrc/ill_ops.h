@@ -268,12 +268,12 @@ __device__ __forceinline__ void op_store_a(const ARaw<BM>& r, _Float16* As, int 
 // d + 32 (x1, columns 32 b + 16 + i) of head b / 2 (Convert.swift:236-244); q heads 0-13,
 // k 14-15, v 16-17: bias, RoPE at the row's position, then q or the K / V cache slot.
 // cs_at / cs: a rotary row already loaded for position cs_at (-1: none), used when it is
-// the row's position.
+// the row's position; bpre: the two bias values already loaded (nullptr: load them).
 __device__ __forceinline__ void epi_qkv(const OpCtx& c, const OpHdr& hd, int layer, int m, int b, int i, float x0, float x1,
-                                        int cs_at = -1, float2 cs_pre = make_float2(0.f, 0.f)) {
+                                        int cs_at = -1, float2 cs_pre = make_float2(0.f, 0.f), const float* bpre = nullptr) {
   const int head = b >> 1, d = (b & 1) * 16 + i;
-  x0 += gld(c.L[layer].bqkv + 32 * b + i);
-  x1 += gld(c.L[layer].bqkv + 32 * b + 16 + i);
+  x0 += bpre ? bpre[0] : gld(c.L[layer].bqkv + 32 * b + i);
+  x1 += bpre ? bpre[1] : gld(c.L[layer].bqkv + 32 * b + 16 + i);
   const int pos = hd.pos;
   if (head < ILL_NH + ILL_NKV) {
     const int p = pos + op_depth(c, hd.mode, m);
@@ -303,12 +303,13 @@ __device__ __forceinline__ void epi_silu(const OpCtx& c, int m, int unit, float 
 
 // Epilogue of a 128-column tile (lane (kg, n) of wave w holds rows m0 + 16 i + 4 kg + r,
 // columns n0 + 32 w + 16 j + n): fp32 partials of a K slice, or the fused epilogue.
-// QKV: cs_base >= 0 gives the rotary rows cs[r] of rows m0 + 4 kg + r at position cs_base +
-// row (used when that is the row's position).
+// QKV: cs_base >= 0 gives the rotary rows cs[4 i + r] of rows m0 + 16 i + 4 kg + r at
+// position cs_base + row (used when that is the row's position); qbias: the lane's two bias
+// values, already loaded (nullptr: loaded here).
 template <int BM, int EPI>
 __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHdr& hd, const v4f (&acc)[BM / 16][2], int m0,
                                                  int n0, int kz, int w, int kg, int n, uint64_t (&red)[4][16],
-                                                 int cs_base = -1, const float2* cs = nullptr) {
+                                                 int cs_base = -1, const float2* cs = nullptr, const float* qbias = nullptr) {
   constexpr int TM = BM / 16;
   if (hd.done) return;
   const OpCtx& c = a.c;
@@ -337,17 +338,24 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
           if (m < a.M) a.resid[(size_t)m * ILL_H + col] += acc[i][j][r];
         }
   } else if constexpr (EPI == OP_SILU) {
+    // Lanes n % 4 = 0, 1 hold the gate values of units 2 q, 2 q + 1 and lanes 2, 3 their up
+    // values. The quad's halves swap rows (quad_perm 2 3 0 1): lanes 0, 1 then apply rows
+    // 4 kg + 0, 1 and lanes 2, 3 rows 4 kg + 2, 3, so that every lane computes two units.
+    const bool lo = (n & 3) < 2;
+    const int u = (n & 3) - (lo ? 0 : 2);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+      for (int j = 0; j < 2; j++) {
+        const int col = n0 + 32 * w + 16 * j + n;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float v = acc[i][j][r];
-          const float up = __shfl_down(v, 2, 16);
-          const int m = m0 + 16 * i + 4 * kg + r, col = n0 + 32 * w + 16 * j + n;
-          if ((n & 3) < 2 && m < a.M) epi_silu(c, m, (col >> 2) * 2 + (n & 3), v, up);
+        for (int h = 0; h < 2; h++) {
+          const float mine = acc[i][j][lo ? h : 2 + h], send = acc[i][j][lo ? 2 + h : h];
+          const float got = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x4e, 0xf, 0xf, false));
+          const int m = m0 + 16 * i + 4 * kg + (lo ? h : 2 + h);
+          if (m < a.M) epi_silu(c, m, (col >> 2) * 2 + u, lo ? mine : got, lo ? got : mine);
         }
+      }
   } else if constexpr (EPI == OP_QKV) {
     const int b = (n0 + 32 * w) >> 5;
 #pragma unroll
@@ -356,8 +364,8 @@ __device__ __forceinline__ void op_gemm_epilogue(const OpGemmArgs& a, const OpHd
       for (int r = 0; r < 4; r++) {
         const int m = m0 + 16 * i + 4 * kg + r;
         if (m < a.M) {
-          if (cs_base >= 0 && TM == 1) epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r], cs_base + m, cs[r]);
-          else epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r]);
+          if (cs_base >= 0) epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r], cs_base + m, cs[4 * i + r], qbias);
+          else epi_qkv(c, hd, a.layer, m, b, n, acc[i][0][r], acc[i][1][r], -1, make_float2(0.f, 0.f), qbias);
         }
       }
   } else {   // OP_LMH: logits (optional) and per-tile argmax keys per row (BM == 16)
@@ -524,6 +532,191 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
   for (int d = 0; d < OP_DEPTH - 1; d++)
     if (s0 + d < ns) kstep(d, s0 + d, false);
   op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, tl.z, w, kg, n, red);
+}
+
+// ---- prefill GEMM, q8 / f16: operands streamed from memory into an LDS ring --------------
+// op_gemm_kernel holds the next k-step (64 columns) in registers, one step ahead (DEPTH 1)
+// or a ring of DEPTH steps, and a k-step of a 64 x 128 tile is about 0.1 us of MFMA work
+// against a memory round trip of about 1 us: the prefill GEMMs waited on memory at every
+// step. Here the operands go from memory straight into LDS (global_load_lds_dwordx4: lane i
+// of a wave's load writes 16 bytes at the instruction's LDS address + 16 i), into a ring of
+// ST stages, so that ST - 1 k-steps are in flight and no registers hold them. A stage holds
+//   A: BM rows x 64 halves in 16-byte units ordered (row / 16, k / 8, row % 16), so that the
+//      16 lanes of an MFMA operand read 256 contiguous bytes (no bank conflicts);
+//   B: the k-step's block of the tiled weights (128 rows x 64 columns at op_wt_off, 8 KB q8,
+//      16 KB f16) as stored: its units are already in that order;
+//   q8: the block's scales (128 rows x 64 / qg f16, op_st_off), 256 or 512 bytes.
+// q8 weights are dequantized as they leave LDS, with op_store_w's arithmetic, and every
+// output sums the same products in the same order as op_gemm_kernel: the results are
+// identical. The loads are issued in inline assembly: the compiler's own tracking of LDS
+// loads in flight made it wait for all of them before some of the stage's LDS reads (it
+// could not tell the stages apart), which serialized the ring. The wait for the stage about
+// to be read is explicit: vmcnt counts this wave's own loads, and the barrier after it covers
+// the other waves' loads and orders every wave's reads of the stage refilled next before the
+// refill. (The compiler's waits for its own loads count only the loads it knows of, so they
+// wait at least as long as they need: loads complete in issue order.)
+#define OP_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// One wave-wide load into LDS: lane i's `bytes` (16 or 4) at global g go to LDS byte address
+// lds + bytes * i (lds: the same for every lane).
+__device__ __forceinline__ void op_lds_dma16(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)OP_LDS(lds));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g) : "m0");
+}
+__device__ __forceinline__ void op_lds_dma4(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)OP_LDS(lds));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(m), "v"(g) : "m0");
+}
+// Stages: 24 KB (f16) / 16.5 KB (q8) each at BM 64, 20 / 12.5 KB at BM 32. Rings of 6 (f16)
+// and 8 (q8) stages for the GEMMs of at most one workgroup per CU, and for all of them, were
+// slower (512-row prefill 1.96 / 2.24 ms against 1.93 / 2.12 ms; 2.17 / 2.55 ms): issuing the
+// longer prologue took 2 us instead of 0.7 and the k-steps were hardly faster.
+#define OP_RING_ST(FMT, EPI) ((FMT) == 0 ? 3 : 4)
+template <int FMT, int BM>
+struct OpRing {                                  // sizes in 16-byte units
+  static constexpr int A = BM * 8;
+  static constexpr int B = FMT == 0 ? 1024 : 512;
+  static constexpr int SC = FMT == 1 ? 32 : 0;
+  static constexpr int N = A + B + SC;
+  static constexpr int L = A / 256 + B / 256 + (FMT == 1 ? 1 : 0);   // loads per thread and stage
+};
+
+// Thread tid's loads of the k-step at k0 into stage st (rows >= M read row M - 1).
+template <int FMT, int BM>
+__device__ __forceinline__ void op_ring_load(const OpGemmArgs& a, int m0, int n0, int k0, uint4* st, int tid) {
+  using R = OpRing<FMT, BM>;
+  const int K = a.W.K, wb = tid & ~63;   // wave's first unit of each 256-unit run
+#pragma unroll
+  for (int u = 0; u < R::A / 256; u++) {
+    const int p = 256 * u + tid;
+    const int row = min(m0 + ((p >> 7) << 4) + (p & 15), a.M - 1);
+    op_lds_dma16(a.A + (size_t)row * K + k0 + 8 * ((p >> 4) & 7), st + 256 * u + wb);
+  }
+  const uint4* blk = (const uint4*)(a.W.w + op_wt_off(n0, k0, K, FMT == 0 ? 2 : 1));
+#pragma unroll
+  for (int u = 0; u < R::B / 256; u++)
+    op_lds_dma16(blk + 256 * u + tid, st + R::A + 256 * u + wb);
+  if constexpr (FMT == 1) {   // 64 dwords per wave: all of them (qg 64), or half (qg 32: waves 0, 2 the first)
+    const int off = a.W.qg == 32 ? ((tid >> 6) & 1) * 64 : 0;
+    const uint32_t* sc = (const uint32_t*)(a.W.s + op_st_off(n0, k0, K, a.W.qg));
+    op_lds_dma4(sc + off + (tid & 63), (uint32_t*)(st + R::A + R::B) + off);
+  }
+}
+
+// The k-step in stage st: lane (kg, n) of wave w, rows 16 i + n, columns 32 w + 16 j + n.
+template <int FMT, int BM>
+__device__ __forceinline__ void op_ring_mma(const uint4* st, int w, int kg, int n, int qg, v4f (&acc)[BM / 16][2]) {
+  using R = OpRing<FMT, BM>;
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    v8h bf[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int c16 = 2 * w + j;   // 16-row sub-tile of the weight block
+      if constexpr (FMT == 0) {
+        bf[j] = u4_to_v8h(st[R::A + c16 * 128 + ((kg & 1) * 4 + 2 * ks + (kg >> 1)) * 16 + n]);
+      } else {
+        const uint2 q = ((const uint2*)(st + R::A + c16 * 64 + (2 * ks + (kg >> 1)) * 16 + n))[kg & 1];
+        const uint16_t* sc = (const uint16_t*)(st + R::A + R::B);
+        const _Float16 s = (_Float16)h2f(sc[(16 * c16 + n) * (64 / qg) + (qg == 32 ? ks : 0)]);
+        const uint32_t x[2] = {q.x, q.y};
+#pragma unroll
+        for (int i = 0; i < 8; i++) bf[j][i] = s * (_Float16)(float)(int8_t)((x[i >> 2] >> (8 * (i & 3))) & 0xff);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BM / 16; i++) {
+      const v8h af = u4_to_v8h(st[i * 128 + (4 * ks + kg) * 16 + n]);
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+}
+
+// Wait until at most `later` stages of this wave's loads are in flight (a constant once the
+// callers' loops are unrolled), then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void op_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+template <int L>
+__device__ __forceinline__ void op_ring_wait(int later) {
+  switch (later) {
+    case 0: op_vm_barrier<0>(); break;
+    case 1: op_vm_barrier<L>(); break;
+    case 2: op_vm_barrier<2 * L>(); break;
+    case 3: op_vm_barrier<3 * L>(); break;
+    case 4: op_vm_barrier<4 * L>(); break;
+    case 5: op_vm_barrier<5 * L>(); break;
+    default: op_vm_barrier<6 * L>(); break;
+  }
+}
+
+// Grid, tiles and epilogues as op_gemm_kernel (4 waves; wave w owns columns 32 w .. + 31 of
+// the 128-column tile and all BM rows).
+template <int FMT, int BM, int EPI, int ST>
+__global__ __launch_bounds__(256) void op_gemm_ring_kernel(OpGemmArgs a) {
+  static_assert(FMT != 2 && ST >= 2 && ST <= 8 && BM >= 32 && BM <= 64 && EPI != OP_LMH, "ring GEMM shape");
+  using R = OpRing<FMT, BM>;
+  const OpHdr hd = op_hdr(a.c);
+#define OP_RING_ARR(i) __shared__ __attribute__((aligned(16))) uint4 r##i[ST > i ? R::N : 1];
+  OP_RING_ARR(0) OP_RING_ARR(1) OP_RING_ARR(2) OP_RING_ARR(3) OP_RING_ARR(4) OP_RING_ARR(5) OP_RING_ARR(6) OP_RING_ARR(7)
+#undef OP_RING_ARR
+  __shared__ uint64_t red[4][16];   // (the argmax epilogue only)
+  auto ring = [&](int d) -> uint4* {
+    return d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : d == 3 ? r3 : d == 4 ? r4 : d == 5 ? r5 : d == 6 ? r6 : r7;
+  };
+  constexpr int TM = BM / 16;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int kg = lane >> 4, n = lane & 15;
+  const OpTile tl = EPI != OP_SILU ? op_tile_xcd() : OpTile{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int n0 = tl.x * OP_BN, m0 = tl.y * BM;
+  const int K = a.W.K, qg = a.W.qg;
+  const int kb = tl.z * a.ksteps * OP_BK;
+  const int ns = (min(K, kb + a.ksteps * OP_BK) - kb) / OP_BK;
+  v4f acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    acc[i][0] = (v4f){0.f, 0.f, 0.f, 0.f};
+    acc[i][1] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  // QKV: the epilogue's bias values and rotary rows (at the expected positions pos_hint +
+  // row), loaded while the k-steps stream (loaded in the epilogue they cost a memory round
+  // trip each, about 4 us per workgroup)
+  float2 qcs[EPI == OP_QKV ? TM * 4 : 1];
+  float qbias[2];
+  if constexpr (EPI == OP_QKV) {
+    const int b = (n0 + 32 * w) >> 5;
+    const float* bq = a.c.L[a.layer].bqkv + 32 * b + n;
+    qbias[0] = gld(bq);
+    qbias[1] = gld(bq + 16);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        qcs[4 * i + r] = gld(a.c.rope + (size_t)min(a.pos_hint + m0 + 16 * i + 4 * kg + r, a.c.maxctx - 1) * 32 + (b & 1) * 16 + n);
+  }
+  // steps past the slice reload its last one, so that every stage issues the same loads
+#pragma unroll
+  for (int d = 0; d < ST - 1; d++) op_ring_load<FMT, BM>(a, m0, n0, kb + min(d, ns - 1) * OP_BK, ring(d), tid);
+  int s0 = 0;
+  for (; s0 + ST <= ns; s0 += ST) {
+#pragma unroll
+    for (int d = 0; d < ST; d++) {
+      op_ring_wait<R::L>(ST - 2);
+      op_ring_load<FMT, BM>(a, m0, n0, kb + min(s0 + d + ST - 1, ns - 1) * OP_BK, ring((d + ST - 1) % ST), tid);
+      op_ring_mma<FMT, BM>(ring(d), w, kg, n, qg, acc);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < ST - 1; d++)
+    if (s0 + d < ns) {
+      op_ring_wait<R::L>(ST - 2 - d);
+      op_ring_mma<FMT, BM>(ring(d), w, kg, n, qg, acc);
+    }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no LDS load outlives the workgroup
+  if constexpr (EPI == OP_QKV) op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, tl.z, w, kg, n, red, a.pos_hint, qcs, qbias);
+  else op_gemm_epilogue<BM, EPI>(a, hd, acc, m0, n0, tl.z, w, kg, n, red);
 }
 
 // ---- GEMM of passes of up to 16 rows --------------------------------------------------

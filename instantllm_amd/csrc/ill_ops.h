@@ -209,6 +209,23 @@ __device__ __forceinline__ void op_fetch_w(const OpMat& W, int n0, int k0, int t
   }
 }
 
+// q8 dequantization, 4 weights at a time: s * (f16)q for the 4 int8 codes of x. Each code
+// q becomes the half 1024 + (q + 128) (exponent 0x64 over the byte q ^ 0x80, built with
+// v_perm), from which 1152 is subtracted: both exact, so the products equal
+// s * (_Float16)(float)q, computed two at a time on packed f16 (v_pk_add_f16, v_pk_mul_f16).
+typedef _Float16 op_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void op_q8x4(uint32_t x, _Float16 s, _Float16* o) {
+  const uint32_t u = x ^ 0x80808080u;
+  const op_h2 k = {(_Float16)1152.f, (_Float16)1152.f}, sc = {s, s};
+  const op_h2 a = __builtin_bit_cast(op_h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - k;
+  const op_h2 b = __builtin_bit_cast(op_h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - k;
+  const op_h2 pa = a * sc, pb = b * sc;
+  o[0] = pa[0];
+  o[1] = pa[1];
+  o[2] = pb[0];
+  o[3] = pb[1];
+}
+
 template <int FMT>
 __device__ __forceinline__ void op_store_w(const WRaw<FMT>& r, _Float16* Bs, int tid) {
   _Float16* dst = Bs + (tid >> 1) * OP_LDK + 32 * (tid & 1);
@@ -229,7 +246,7 @@ __device__ __forceinline__ void op_store_w(const WRaw<FMT>& r, _Float16* Bs, int
     const uint32_t x[8] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[0].w, r.b[1].x, r.b[1].y, r.b[1].z, r.b[1].w};
     _Float16 o[32];
 #pragma unroll
-    for (int i = 0; i < 32; i++) o[i] = s * (_Float16)(float)(int8_t)((x[i >> 2] >> (8 * (i & 3))) & 0xff);
+    for (int i = 0; i < 8; i++) op_q8x4(x[i], s, o + 4 * i);
 #pragma unroll
     for (int i = 0; i < 4; i++) *(uint4*)(dst + 8 * i) = *(const uint4*)(o + 8 * i);
   } else {
@@ -569,8 +586,10 @@ __device__ __forceinline__ void op_lds_dma4(const void* g, const void* lds) {
 // Stages: 24 KB (f16) / 16.5 KB (q8) each at BM 64, 20 / 12.5 KB at BM 32. Rings of 6 (f16)
 // and 8 (q8) stages for the GEMMs of at most one workgroup per CU, and for all of them, were
 // slower (512-row prefill 1.96 / 2.24 ms against 1.93 / 2.12 ms; 2.17 / 2.55 ms): issuing the
-// longer prologue took 2 us instead of 0.7 and the k-steps were hardly faster.
-#define OP_RING_ST(FMT, EPI) ((FMT) == 0 ? 3 : 4)
+// longer prologue took 2 us instead of 0.7 and the k-steps were hardly faster. The gate/up
+// GEMM (608 workgroups at 512 rows) takes 2 (f16) / 3 (q8) stages, so that three workgroups
+// fit per CU and all of them run in one round (f16: 1.90 -> 1.86 ms).
+#define OP_RING_ST(FMT, EPI) ((EPI) == OP_SILU ? ((FMT) == 0 ? 2 : 3) : ((FMT) == 0 ? 3 : 4))
 template <int FMT, int BM>
 struct OpRing {                                  // sizes in 16-byte units
   static constexpr int A = BM * 8;
@@ -618,9 +637,11 @@ __device__ __forceinline__ void op_ring_mma(const uint4* st, int w, int kg, int 
         const uint2 q = ((const uint2*)(st + R::A + c16 * 64 + (2 * ks + (kg >> 1)) * 16 + n))[kg & 1];
         const uint16_t* sc = (const uint16_t*)(st + R::A + R::B);
         const _Float16 s = (_Float16)h2f(sc[(16 * c16 + n) * (64 / qg) + (qg == 32 ? ks : 0)]);
-        const uint32_t x[2] = {q.x, q.y};
+        _Float16 o[8];
+        op_q8x4(q.x, s, o);
+        op_q8x4(q.y, s, o + 4);
 #pragma unroll
-        for (int i = 0; i < 8; i++) bf[j][i] = s * (_Float16)(float)(int8_t)((x[i >> 2] >> (8 * (i & 3))) & 0xff);
+        for (int i = 0; i < 8; i++) bf[j][i] = o[i];
       }
     }
 #pragma unroll

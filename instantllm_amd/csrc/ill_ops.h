@@ -796,11 +796,11 @@ __device__ __forceinline__ v8h op_bvals(const BOp<FMT>& b, int j, int ks) {
   } else if constexpr (FMT == 1) {
     const _Float16 sc = (_Float16)h2f(b.s[j]);
     const uint32_t x0 = ks == 0 ? b.q[j][0].x : b.q[j][0].z, x1 = ks == 0 ? b.q[j][0].y : b.q[j][0].w;
+    _Float16 h[8];
+    op_q8x4(x0, sc, h);
+    op_q8x4(x1, sc, h + 4);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      o[i] = sc * (_Float16)(float)(int8_t)((x0 >> (8 * i)) & 0xff);
-      o[4 + i] = sc * (_Float16)(float)(int8_t)((x1 >> (8 * i)) & 0xff);
-    }
+    for (int i = 0; i < 8; i++) o[i] = h[i];
   } else {
     o = u4_to_v8h(b.q[j][ks]);
   }
@@ -1067,16 +1067,18 @@ __device__ __forceinline__ void orows_apply(const ORows<FMT>& o, const _Float16*
     for (int i = 0; i < (FMT == 0 ? 8 : 4); i++) {
       const uint32_t x[4] = {o.q[u][i].x, o.q[u][i].y, o.q[u][i].z, o.q[u][i].w};
       constexpr int PER = FMT == 0 ? 8 : 16;   // k values per uint4
+      _Float16 wq[FMT == 1 ? 16 : 1];
+      if constexpr (FMT == 1) {   // k = 16 i + e: the scale of k / 32 = i / 2
+        const _Float16 sc = (_Float16)h2f((uint16_t)(o.s[u] >> (16 * (i >> 1))));
+#pragma unroll
+        for (int q = 0; q < 4; q++) op_q8x4(x[q], sc, wq + 4 * q);
+      }
 #pragma unroll
       for (int e = 0; e < PER; e++) {
         const int k = PER * i + e;
         _Float16 wv;
-        if constexpr (FMT == 1) {
-          const _Float16 sc = (_Float16)h2f((uint16_t)(o.s[u] >> (16 * (k >> 5))));
-          wv = sc * (_Float16)(float)(int8_t)((x[e >> 2] >> (8 * (e & 3))) & 0xff);
-        } else {
-          wv = __ushort_as_half((unsigned short)((x[e >> 1] >> (16 * (e & 1))) & 0xffff));
-        }
+        if constexpr (FMT == 1) wv = wq[e];
+        else wv = __ushort_as_half((unsigned short)((x[e >> 1] >> (16 * (e & 1))) & 0xffff));
         acc = fmaf((float)wv, (float)ao[k], acc);
       }
     }

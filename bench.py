@@ -48,15 +48,16 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # (163,349.8 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 4bcea3b.
 # Source and commands: profiles/pass_kernel_q4_decode_config2.md
 TRAFFIC_BYTES_PER_STEP = 351_291_187
-# MFMA utilisation of the pass kernels and of the prefill kernels (commit 4bcea3b), from
-# rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations (same profile files)
+# MFMA utilisation of the pass kernels (commit 4bcea3b) and of the prefill kernels (commit
+# cfa15c6), from rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations
+# (profiles/pass_kernel_q4_decode_config2.md, profiles/layer_by_layer_q8_f16_config4.md)
 MFMA_COUNTERS = {
     "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 47.8},
     "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0112, "int8_TOPs": 51.8},
-    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.147, "f16_TFLOPs": 371.0},
-    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.088, "f16_TFLOPs": 222.4},
-    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.031, "f16_TFLOPs": 77.7},
-    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.096, "f16_TFLOPs": 241.8},
+    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.153, "f16_TFLOPs": 385.4},
+    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.103, "f16_TFLOPs": 258.1},
+    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.040, "f16_TFLOPs": 99.8},
+    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.095, "f16_TFLOPs": 239.7},
 }
 
 

@@ -127,6 +127,35 @@ def test_long_prefill_chunks(model):
     assert metrics.rel_l2(e.read_logits(0), m.forward([tok], cache)) <= REL_L2_TOL
 
 
+@pytest.mark.parametrize("n", [17, 31, 33, 63, 65, 511, 513])
+def test_prefill_chunk_edges(model, n):
+    """Prompt lengths at the edges of the prefill GEMMs' row tiles (16, 32 and 64 rows) and of
+    the 512-row chunk, prefilled in one call and again in two calls whose second chunk starts
+    at a position that is not a multiple of 64 (the QKV epilogue's rotary rows are read for
+    pos + row): last-row logits and the first decode step after it against the oracle."""
+    fmt, e, m = model
+    rng = np.random.default_rng(1000 + 10 * fmt + n)
+    prompt = [int(t) for t in rng.integers(0, VOCAB, size=n)]
+    cache = m.new_cache(n + 8)
+    ref = m.forward(prompt, cache)
+    nxt = m.forward([int(np.argmax(ref))], cache)
+    for split in (n, 17 + (n - 17) // 3):
+        log(f"format {fmt}: prompt {n}, first call {split} rows")
+        e.reset_out_tokens()
+        e.set_state(pos=0, n=n, maxsteps=64, eos=NO_EOS)
+        e.prefill(prompt[:split], write_logits=split == n)
+        if split < n:
+            e.prefill(prompt[split:], write_logits=True)
+        lg = e.read_logits(0)
+        assert metrics.rel_l2(lg, ref) <= REL_L2_TOL, split
+        tok = int(e.out_tokens()[e.get_state()["step"] - 1])   # the last call's token
+        assert tok == int(np.argmax(lg))
+        if tok != int(np.argmax(ref)):   # a near tie in the logits: the step would differ
+            continue
+        e.decode_step(write_logits=True)
+        assert metrics.rel_l2(e.read_logits(0), nxt) <= REL_L2_TOL, split
+
+
 def test_split_attention_rows_bit_identical_long_context(tmp_path):
     """Past 1024 positions the 1-row and 16-row attention of the layer-by-layer path is split
     over several workgroups per (row, head). The split follows the launch (1-row steps here

@@ -552,12 +552,14 @@ __global__ __launch_bounds__(256) void op_gemm_kernel(OpGemmArgs a) {
 }
 
 // ---- prefill GEMM, q8 / f16: operands streamed from memory into an LDS ring --------------
-// op_gemm_kernel holds the next k-step (64 columns) in registers, one step ahead (DEPTH 1)
-// or a ring of DEPTH steps, and a k-step of a 64 x 128 tile is about 0.1 us of MFMA work
-// against a memory round trip of about 1 us: the prefill GEMMs waited on memory at every
-// step. Here the operands go from memory straight into LDS (global_load_lds_dwordx4: lane i
-// of a wave's load writes 16 bytes at the instruction's LDS address + 16 i), into a ring of
-// ST stages, so that ST - 1 k-steps are in flight and no registers hold them. A stage holds
+// op_gemm_kernel stages the next k-step (64 columns) in registers, one step ahead (DEPTH 1)
+// or a ring of DEPTH steps, and stores it to LDS. Here the operands go from memory straight
+// into LDS (global_load_lds_dwordx4: lane i of a wave's load writes 16 bytes at the
+// instruction's LDS address + 16 i), into a ring of ST stages, so that ST - 1 k-steps are in
+// flight with no registers or LDS stores spent on them. (Per workgroup at 512 rows: 0.7 us
+// to issue the prologue, then 0.3-0.7 us per k-step; the gate/up GEMM, three workgroups per
+// CU, is bound by the LDS traffic of its k-steps: 24 KB written and 48 KB read, the four
+// waves reading the same A rows.) A stage holds
 //   A: BM rows x 64 halves in 16-byte units ordered (row / 16, k / 8, row % 16), so that the
 //      16 lanes of an MFMA operand read 256 contiguous bytes (no bank conflicts);
 //   B: the k-step's block of the tiled weights (128 rows x 64 columns at op_wt_off, 8 KB q8,

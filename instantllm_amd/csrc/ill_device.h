@@ -132,6 +132,33 @@ __device__ __forceinline__ bool wave_wait2(L&& light, F&& ready, IllCtl* ctl, in
   }
 }
 
+// The light stage of wave_wait2 alone, pipelined: D polls of the light words in flight, each
+// iteration checks the oldest and issues it again (samples every round trip / D). `issue(st)`
+// loads the light words into st, `check(st)` tests them. False on an error or a timeout.
+// (SLEEP: s_sleep units of 64 cycles between iterations.)
+template <int D, int SLEEP, class W, class I, class C>
+__device__ __forceinline__ bool wave_light_p(I&& issue, C&& check, IllCtl* ctl, int code) {
+  const uint64_t t0 = clk();
+  W st[D];
+#pragma unroll
+  for (int d = 0; d < D; d++) issue(st[d]);
+  for (int it = 1;; it++) {
+    bool lit = false;
+#pragma unroll
+    for (int d = 0; d < D; d++)
+      if (!lit) {
+        lit = __all(check(st[d]));
+        if (!lit) issue(st[d]);
+      }
+    if (lit) return true;
+    if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);
+    if ((it & 7) == 0) {
+      if (aload32(&ctl->err) != 0) return false;
+      if (clk() - t0 > ILL_WAIT_TICKS) { set_err(ctl, code); return false; }
+    }
+  }
+}
+
 // A wave-uniform value held in a vector register, so that loads from addresses built on it
 // stay vector memory loads.
 __device__ __forceinline__ int vgpr_uniform(int v) {
@@ -309,6 +336,7 @@ struct PrepLds {
   float2 sc[14 * T];          // per (group, row): step d and d * sum of the codes
   alignas(16) float red[ILL_WAVES][T];   // per-wave partial sums of squares
   alignas(16) int ok[ILL_WAVES];         // per-wave "input complete" votes
+  int lit;                               // 1-row passes: the watcher wave's verdict
 };
 
 // MFMA A-operand row read by lane row m: at T = 1 every lane row aliases row 0, so the

@@ -260,6 +260,23 @@ __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>(
 #ifndef ILL_POLL
 #define ILL_POLL 2
 #endif
+// Inputs of prep896<1> from an accumulator: 1 = wave 0 alone polls the light words
+// (ILL_POLL_D polls in flight, ILL_WATCH_SLEEP x 64 cycles between rounds) while the other
+// waves wait at an LDS barrier, then every wave reads its columns as before. A step
+// (config 2, graph-replayed, A/B in both orders on one box): every wave polling 318.0-318.5
+// us, one watcher 314.0-314.5 us. Fewer polls of words that the atomics are updating is what
+// pays (the workgroups' spread in the trace did not shrink): two or three watcher polls in
+// flight 316.9-317.1 / 320.2-320.4 us, sleeps of 8 or 16 314.7-314.9 / 315.6-315.9 us, a
+// watcher waiting for the complete word (no slack) 319.5 us.
+#ifndef ILL_WATCH
+#define ILL_WATCH 1
+#endif
+#ifndef ILL_POLL_D
+#define ILL_POLL_D 1
+#endif
+#ifndef ILL_WATCH_SLEEP
+#define ILL_WATCH_SLEEP 4
+#endif
 #ifndef ILL_SLACK_XA
 #define ILL_SLACK_XA 4
 #endif
@@ -269,7 +286,28 @@ __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>(
 template <int T, bool XB>
 struct SrcRes {
   static constexpr int kSlack = XB ? ILL_SLACK_XB : ILL_SLACK_XA;
+  static constexpr bool kPipe = true;
+  static constexpr int NC = XB ? xb_copies<T>() : xa_copies<T>();
+  struct Light {   // the light words of rows t < T, copies k < NC, in flight
+    uint64_t w[T][NC];
+  };
   const uint64_t* base;   // copy 0, row 0
+  __device__ __forceinline__ void light_issue(Light& L, int nrows, int c) const {
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int k = 0; k < NC; k++)
+        L.w[t][k] = t < nrows ? aload64(base + ((size_t)k * 16 + t) * ILL_ACC_ROW + acc_col(c)) : 0;
+  }
+  __device__ __forceinline__ bool light_check(const Light& L, int nrows, int slack) const {
+    bool ok = true;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int k = 0; k < NC; k++)
+        if (t < nrows) ok &= fx_count(L.w[t][k]) + slack >= (XB ? xb_expect<T>(k) : xa_expect<T>(k));
+    return ok;
+  }
   // every copy of column c of row t lacks at most `slack` contributions
   __device__ __forceinline__ bool near1(int t, int c, int slack) const {
     constexpr int NC = XB ? xb_copies<T>() : xa_copies<T>();
@@ -325,6 +363,7 @@ __device__ __forceinline__ float embed1(const IllWeights& W, int tok, int c) {
 
 struct SrcEmbed {
   static constexpr int kSlack = 0;
+  static constexpr bool kPipe = false;
   IllWeights W;
   const int* toks;   // LDS copy of the row tokens
   __device__ __forceinline__ bool load1(int t, int c, float& v) const {
@@ -393,17 +432,7 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
   const float g0 = gld(gamma + c0), g1 = gld(gamma + c1);
   float v0[T], v1[T];
   const int cl = vgpr_uniform(64 * w);   // light poll: the wave's first column of each row
-  const bool alive = wave_wait2([&]() {
-    bool ok = true;
-    float x;
-#pragma unroll
-    for (int t = 0; t < T; t++)
-      if (t < nrows) {
-        if constexpr (ILL_POLL == 0) ok &= src.load1(t, cl, x);
-        else if constexpr (ILL_POLL == 2) ok &= src.near1(t, cl, Src::kSlack);
-      }
-    return ok;
-  }, [&]() {
+  auto full = [&]() {
     bool ok = true;
 #pragma unroll
     for (int t = 0; t < T; t++) {
@@ -415,7 +444,33 @@ __device__ __forceinline__ bool prep896(const Src& src, const float* gamma, int 
       }
     }
     return ok;
-  }, ctl, code);
+  };
+  bool alive;
+  if constexpr (T == 1 && ILL_WATCH && Src::kPipe) {
+    // wave 0 watches the light words; its verdict, written just before the barrier, is read
+    // after it, so no earlier value of the word is ever taken for it
+    using LW = typename Src::Light;
+    if (w == 0) {
+      const bool lit = wave_light_p<ILL_POLL_D, ILL_WATCH_SLEEP, LW>([&](LW& L) { src.light_issue(L, nrows, cl); },
+                                                    [&](const LW& L) { return src.light_check(L, nrows, Src::kSlack); },
+                                                    ctl, code);
+      if (lane == 0) P.lit = lit;
+    }
+    lds_barrier();
+    alive = P.lit && wave_wait(full, ctl, code);
+  } else {
+    alive = wave_wait2([&]() {
+      bool ok = true;
+      float x;
+#pragma unroll
+      for (int t = 0; t < T; t++)
+        if (t < nrows) {
+          if constexpr (ILL_POLL == 0) ok &= src.load1(t, cl, x);
+          else if constexpr (ILL_POLL == 2) ok &= src.near1(t, cl, Src::kSlack);
+        }
+      return ok;
+    }, full, ctl, code);
+  }
   if (trs >= 0) trace_mark(a, trs);
   // stage by stage over blocks of up to 4 rows, so the rows' reduction chains interleave
   constexpr int RB = T < 4 ? T : 4;

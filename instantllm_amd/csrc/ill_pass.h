@@ -277,6 +277,13 @@ __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>(
 #ifndef ILL_WATCH_SLEEP
 #define ILL_WATCH_SLEEP 4
 #endif
+// 16-row REDUCE: 1 = one watcher wave polls a word of producers 0-12, the rest wait at a
+// barrier, then every thread reads its words (0: every thread polls its own word first).
+// 16-row verify at prefix 512, A/B in three rounds: 818.6-820.2 -> 816.6-817.1 us (median
+// of 25 passes each), the same logits.
+#ifndef ILL_WATCH_RED
+#define ILL_WATCH_RED 1
+#endif
 #ifndef ILL_SLACK_XA
 #define ILL_SLACK_XA 4
 #endif
@@ -1169,9 +1176,7 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
     const uint32_t tag = tagof_pub(H.epoch, l);
     const __amdgpu_buffer_rsrc_t rs = pub_rsrc(a.part + (size_t)(l & 1) * ILL_NGU * ILL_MAXT * ILL_PART_ROW, ILL_NGU * PSTRIDE);
     int64_t s0 = 0, s1 = 0, s2 = 0;
-    const bool alive = wave_wait2([&]() {
-      return !act || pub_ok(__builtin_amdgcn_raw_buffer_load_b128(rs, opq(off + g * PSTRIDE), 0, ILL_BUF_SC1), tag);
-    }, [&]() {
+    auto full = [&]() {
       bool ok = true;
       s0 = s1 = s2 = 0;
       if (act) {
@@ -1193,7 +1198,27 @@ __device__ __forceinline__ bool role_red(const IllPassArgs& a, const PassHdr& H,
         }
       }
       return ok;
-    }, a.ctl, 900 + l);
+    };
+    bool alive;
+    if constexpr (ILL_WATCH_RED) {
+      // wave 0 watches one word (the first of the segment) of producers 0 .. NG - 1, the
+      // others wait at the barrier; its verdict goes through red[0], which the sums
+      // overwrite only after the barrier below
+      if (tid < 64) {
+        const int l64 = tid;
+        const int o0 = (t * ILL_PART_ROW + q * ILL_PART_Q) * 16 + min(l64, NG - 1) * PSTRIDE;
+        const bool lit = wave_light_p<ILL_POLL_D, ILL_WATCH_SLEEP, ill_v4u>(
+            [&](ill_v4u& v) { v = __builtin_amdgcn_raw_buffer_load_b128(rs, opq(o0), 0, ILL_BUF_SC1); },
+            [&](const ill_v4u& v) { return pub_ok(v, tag); }, a.ctl, 900 + l);
+        if (tid == 0) red[0] = lit;
+      }
+      lds_barrier();
+      alive = red[0] != 0 && wave_wait(full, a.ctl, 900 + l);
+    } else {
+      alive = wave_wait2([&]() {
+        return !act || pub_ok(__builtin_amdgcn_raw_buffer_load_b128(rs, opq(off + g * PSTRIDE), 0, ILL_BUF_SC1), tag);
+      }, full, a.ctl, 900 + l);
+    }
     if (!__syncthreads_and(alive)) return false;
     trace_mark(a, ILL_TRL * l + 1);
     if (act) {

@@ -45,14 +45,14 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # HBM bytes per launch of ill_pass_kernel<1> measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (one counter per run, median over single dispatches), each scaled by the
 # reading of a plain 256 MiB device copy (fetch x 2.000, write x 1.000):
-# (162,672.2 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 6af3781.
+# (162,670.1 x 2 + 16,358.2) KiB, measured on the pass kernel of commit 12e9d07.
 # Source and commands: profiles/pass_kernel_q4_decode_config2.md
-TRAFFIC_BYTES_PER_STEP = 349_903_424
-# MFMA utilisation of the pass kernels (commit 6af3781) and of the prefill kernels (commit
+TRAFFIC_BYTES_PER_STEP = 349_899_200
+# MFMA utilisation of the pass kernels (commit 12e9d07) and of the prefill kernels (commit
 # cfa15c6), from rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations
 # (profiles/pass_kernel_q4_decode_config2.md, profiles/layer_by_layer_q8_f16_config4.md)
 MFMA_COUNTERS = {
-    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 48.0},
+    "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 48.1},
     "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0122, "int8_TOPs": 54.8},
     "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.153, "f16_TFLOPs": 385.4},
     "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.103, "f16_TFLOPs": 258.1},

@@ -412,7 +412,8 @@ template <int FMT>
 void op_seq(ill_engine* e, int M, int lm_rows) {
   const OpCtx& c = e->octx;
   hipStream_t s = e->stream;
-  hipLaunchKernelGGL(op_embed_kernel<FMT>, dim3((M * ILL_H + 255) / 256), dim3(256), 0, s, c, M);
+  // the embedding with layer 0's RMSNorm (one launch)
+  hipLaunchKernelGGL(op_embed_norm_kernel<FMT>, dim3((M + 3) / 4), dim3(256), 0, s, c, e->holayers[0].ln1, M);
   // passes of up to 16 rows: attention split over up to 8 workgroups per (row, head), one
   // per 1024 positions of context (the result does not depend on the split)
   const int nch = (e->pos_hint + M + 63) / 64;
@@ -424,7 +425,7 @@ void op_seq(ill_engine* e, int M, int lm_rows) {
   float* opart_o = e->opart + ILL_OP_PART_SPLIT;   // [head][row][896] O partials
   // each residual update also writes the next RMSNorm where its K is split (op_gemm returns
   // whether it did)
-  bool normed = false;
+  bool normed = true;   // (layer 0's came with the embedding)
   for (int l = 0; l < e->layers; l++) {
     const OpLayerW& L = e->holayers[l];
     if (!normed) hipLaunchKernelGGL(op_norm_kernel, dim3((M + 3) / 4), dim3(256), 0, s, c, L.ln1, 0, M);

@@ -126,15 +126,6 @@ __device__ __forceinline__ float op_dequant1(const OpMat& m, int r, int k) {
 }
 
 // x[t][:] = embedding row of ptoks[t] (Shaders.swift:118-126, :179-190)
-template <int FMT>
-__global__ __launch_bounds__(256) void op_embed_kernel(OpCtx c, int M) {
-  const int done = gld(&c.st->done);
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= M * ILL_H) return;
-  const int t = i / ILL_H, k = i % ILL_H;
-  const float v = op_dequant1<FMT>(c.emb, gld(c.ptoks + t), k);
-  if (!done) gst(c.x + i, v);
-}
 
 // xn[t] = f16(x[t] * rsqrt(mean(x^2) + eps) * gamma) for rows row0 .. row0 + M - 1 (one wave
 // per row; sum of squares in a fixed order). Output row index t - row0.
@@ -149,6 +140,38 @@ __global__ __launch_bounds__(256) void op_norm_kernel(OpCtx c, const float* gamm
   for (int i = 0; i < 14; i++) {
     v[i] = gld(xr + 64 * i + lane);
     g[i] = gld(gamma + 64 * i + lane);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 14; i++) ss += v[i] * v[i];
+  ss = gsum<64>(ss);
+  const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / (float)ILL_H) + ILL_EPS);
+  if (done) return;
+#pragma unroll
+  for (int i = 0; i < 14; i++)
+    gst((uint16_t*)(c.xn + (size_t)t * ILL_H + 64 * i + lane), (uint16_t)__half_as_ushort(__float2half(v[i] * scale * g[i])));
+}
+
+// The embedding rows of the pass's tokens into x and, from the same registers, layer 0's
+// RMSNorm of them into xn, in one launch (one wave per row; the sum of squares in
+// op_norm_kernel's order).
+template <int FMT>
+__global__ __launch_bounds__(256) void op_embed_norm_kernel(OpCtx c, const float* gamma, int M) {
+  const int done = gld(&c.st->done);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + w;
+  if (t >= M) return;
+  const int tok = gld(c.ptoks + t);
+  float v[14], g[14];
+#pragma unroll
+  for (int i = 0; i < 14; i++) {
+    v[i] = op_dequant1<FMT>(c.emb, tok, 64 * i + lane);
+    g[i] = gld(gamma + 64 * i + lane);
+  }
+  float* xr = c.x + (size_t)t * ILL_H;
+  if (!done) {
+#pragma unroll
+    for (int i = 0; i < 14; i++) gst(xr + 64 * i + lane, v[i]);
   }
   float ss = 0.f;
 #pragma unroll

@@ -621,7 +621,8 @@ struct OpRing {                                  // sizes in 16-byte units
   static constexpr int B = FMT == 0 ? 1024 : 512;
   static constexpr int SC = FMT == 1 ? 32 : 0;
   static constexpr int N = A + B + SC;
-  static constexpr int L = A / 256 + B / 256 + (FMT == 1 ? 1 : 0);   // loads per thread and stage
+  static constexpr int LA = A >= 256 ? A / 256 : 1;   // A loads per thread (BM 16: waves 2, 3 repeat 0, 1)
+  static constexpr int L = LA + B / 256 + (FMT == 1 ? 1 : 0);   // loads per thread and stage
 };
 
 // Thread tid's loads of the k-step at k0 into stage st (rows >= M read row M - 1).
@@ -630,10 +631,12 @@ __device__ __forceinline__ void op_ring_load(const OpGemmArgs& a, int m0, int n0
   using R = OpRing<FMT, BM>;
   const int K = a.W.K, wb = tid & ~63;   // wave's first unit of each 256-unit run
 #pragma unroll
-  for (int u = 0; u < R::A / 256; u++) {
-    const int p = 256 * u + tid;
+  for (int u = 0; u < R::LA; u++) {
+    // unit p (BM 16: 128 units, which waves 2, 3 load again into the same bytes, so that every
+    // wave issues the same loads)
+    const int p = (256 * u + tid) & (R::A - 1);
     const int row = min(m0 + ((p >> 7) << 4) + (p & 15), a.M - 1);
-    op_lds_dma16(a.A + (size_t)row * K + k0 + 8 * ((p >> 4) & 7), st + 256 * u + wb);
+    op_lds_dma16(a.A + (size_t)row * K + k0 + 8 * ((p >> 4) & 7), st + ((256 * u + wb) & (R::A - 1)));
   }
   const uint4* blk = (const uint4*)(a.W.w + op_wt_off(n0, k0, K, FMT == 0 ? 2 : 1));
 #pragma unroll
@@ -702,7 +705,7 @@ __device__ __forceinline__ void op_ring_wait(int later) {
 // the 128-column tile and all BM rows).
 template <int FMT, int BM, int EPI, int ST>
 __global__ __launch_bounds__(256) void op_gemm_ring_kernel(OpGemmArgs a) {
-  static_assert(FMT != 2 && ST >= 2 && ST <= 8 && BM >= 32 && BM <= 64 && EPI != OP_LMH, "ring GEMM shape");
+  static_assert(FMT != 2 && ST >= 2 && ST <= 8 && BM >= 16 && BM <= 64 && (EPI != OP_LMH || BM == 16), "ring GEMM shape");
   using R = OpRing<FMT, BM>;
   const OpHdr hd = op_hdr(a.c);
 #define OP_RING_ARR(i) __shared__ __attribute__((aligned(16))) uint4 r##i[ST > i ? R::N : 1];
@@ -715,7 +718,9 @@ __global__ __launch_bounds__(256) void op_gemm_ring_kernel(OpGemmArgs a) {
   constexpr int TM = BM / 16;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kg = lane >> 4, n = lane & 15;
-  const OpTile tl = EPI != OP_SILU ? op_tile_xcd() : OpTile{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  // (tiles renumbered per XCD for the 32- and 64-row prefill tiles but gate/up, as
+  // op_gemm_kernel; the argmax epilogue indexes by blockIdx.x)
+  const OpTile tl = EPI != OP_SILU && BM > 16 ? op_tile_xcd() : OpTile{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
   const int n0 = tl.x * OP_BN, m0 = tl.y * BM;
   const int K = a.W.K, qg = a.W.qg;
   const int kb = tl.z * a.ksteps * OP_BK;

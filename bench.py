@@ -49,15 +49,15 @@ KV_BYTES_PER_POS = 12_288         # 24 layers x 2 KV heads x (K + V) x 64 x 2 B
 # Source and commands: profiles/pass_kernel_q4_decode_config2.md
 TRAFFIC_BYTES_PER_STEP = 349_899_200
 # MFMA utilisation of the pass kernels (commit 12e9d07) and of the prefill kernels (commit
-# ae277c2), from rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations
+# 0827496), from rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES over the kernel durations
 # (profiles/pass_kernel_q4_decode_config2.md, profiles/layer_by_layer_q8_f16_config4.md)
 MFMA_COUNTERS = {
     "ill_pass_kernel<16> (16-row verify)": {"mfma_busy": 0.0111, "int8_TOPs": 48.1},
     "ill_pass_kernel<1> (1-row step)": {"mfma_busy": 0.0122, "int8_TOPs": 54.8},
-    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.152, "f16_TFLOPs": 382.8},
-    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.102, "f16_TFLOPs": 257.8},
-    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.040, "f16_TFLOPs": 99.5},
-    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.096, "f16_TFLOPs": 241.7},
+    "prefill gate/up GEMM (f16, 512 rows)": {"mfma_busy": 0.154, "f16_TFLOPs": 387.7},
+    "prefill O/down GEMM (f16, 512 rows)": {"mfma_busy": 0.103, "f16_TFLOPs": 259.1},
+    "prefill QKV GEMM (f16, 512 rows)": {"mfma_busy": 0.041, "f16_TFLOPs": 102.6},
+    "prefill attention (512-row chunks, q8 / f16)": {"mfma_busy": 0.097, "f16_TFLOPs": 243.3},
 }
 
 

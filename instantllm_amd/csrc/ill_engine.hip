@@ -309,11 +309,16 @@ int write_pos_n(ill_engine* e, int pos, int n) {
 
 // ---- layer-by-layer path -----------------------------------------------------------------
 // Passes of up to 16 rows: the GEMMs that are not register-direct GEMVs (the lm_head, and the
-// gate/up GEMM with K split) run on the LDS-ring GEMM for q8, on op_gemm_kernel for f16 and
+// gate/up GEMM with K split) run on the LDS-ring GEMM for q8 and f16, on op_gemm_kernel for
 // q4. q8 dequantizes its weights as they leave the ring instead of into an LDS tile: q8
 // decode after 512 positions 892 -> 859 us, at 4096 1,004 -> 975 us (the lm_head alone
-// 4 us of it); f16 on the ring was 14 us slower per step.
-#define OP_SMALL_RING(FMT) ((FMT) == 1)
+// 4 us of it). f16 takes a ring of 4 stages here (with the prefill gate/up's 2 it was 14 us
+// slower than op_gemm_kernel; with 4, 873 -> 855 us, at 4096 991 -> 973 us).
+#define OP_SMALL_RING(FMT) ((FMT) != 2)
+#ifndef OP_RING_ST_SMALL_F16
+#define OP_RING_ST_SMALL_F16 4
+#endif
+#define OP_RING_ST_SMALL(FMT, EPI) ((FMT) == 0 ? OP_RING_ST_SMALL_F16 : OP_RING_ST(FMT, EPI))
 #define ILL_OP_PART_BYTES (16u << 20)   // >= slices x rows x N x 4 of every split GEMM
 #define ILL_OP_PART_SPLIT (2u << 20)    // floats: passes of up to 16 rows keep the gate/up
                                         // partials below, the down GEMM's above
@@ -393,7 +398,7 @@ bool op_gemm(ill_engine* e, const __half* A, const OpMat& W, int M, int layer, f
   } else if constexpr (QKV1) {
     hipLaunchKernelGGL((op_gemv_kernel<FMT, EPI, false, 2>), dim3(W.N / 32), dim3(128), 0, e->stream, g);
   } else if constexpr (OP_SMALL_RING(FMT)) {
-    hipLaunchKernelGGL((op_gemm_ring_kernel<FMT, 16, EPI, OP_RING_ST(FMT, EPI)>), grid, dim3(256), 0, e->stream, g);
+    hipLaunchKernelGGL((op_gemm_ring_kernel<FMT, 16, EPI, OP_RING_ST_SMALL(FMT, EPI)>), grid, dim3(256), 0, e->stream, g);
   } else {
     hipLaunchKernelGGL((op_gemm_kernel<FMT, 16, EPI, 4>), grid, dim3(256), 0, e->stream, g);
   }

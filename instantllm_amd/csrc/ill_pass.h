@@ -256,7 +256,9 @@ __device__ __forceinline__ int xb_expect(int c) { return ILL_NGU / xb_copies<T>(
 // The slack is per accumulator (XA: 15 contributions at 16 rows, 8 / 7 per copy at one row;
 // XB: 77, or 39 / 38): the full read is issued while the last contributions land, so it
 // returns about when they are complete (one row, config 2: 333 -> 327.6 us per step with
-// slack 4 / 8 against the plain two-stage poll; the full input every time: 339 us).
+// slack 4 / 8 against the plain two-stage poll; the full input every time: 339 us). With the
+// watcher wave below, A/B in both orders on one box: 4 / 8 314.4-314.7 us, 2 / 4 314.8-314.9,
+// 6 / 12 316.5-316.8 (the same tokens).
 #ifndef ILL_POLL
 #define ILL_POLL 2
 #endif
